@@ -1,0 +1,327 @@
+#!/usr/bin/env python3
+"""QuantizedLinear forward on one MI355X: the decode GEMV and the prefill GEMM.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+Default workload: INT4 grouped (g=128) QuantizedLinear
+4096 -> 4096, no bias, decode M=1.  A step is one forward call; K steps run
+back to back as one captured hipGraph over `--copies` rotating weight copies
+(> 256 MB in total, so the weights stream from HBM, not the Infinity Cache).
+`value` is algorithmic bytes per call * K / time (GB/s).
+
+The same line carries the M=2048 INT8 per-tensor GEMM (config 4) under
+"secondary" (TFLOP/s against the fp32 MFMA peak) and the reference's CPU path
+(compiled from its own sources into oracle/_ref, or the C port when that is
+absent) timed on this host under "cpu_baseline".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, TFLOP/s
+METRIC = "QuantizedLinear GB/s at M=1 (% HBM peak); TFLOP/s at M=2048 (% MFMA)"
+
+# Shapes of BASELINE.json's configs.  scheme: 0 per-tensor, 1 per-channel.
+CONFIGS = {
+    "c1": dict(name="C1: INT8 per-tensor QuantizedLinear 1024->1024 + bias, M=128", bits=8, M=128, K=1024,
+               N=1024, G=0, scheme=0, bias=True, seed=0),
+    "c2": dict(name="C2: INT4 g128 QuantizedLinear 4096->4096, decode GEMV M=1", bits=4, M=1, K=4096, N=4096,
+               G=128, scheme=2, bias=False, seed=1),
+    "c3_gate_m1": dict(name="C3: INT4 g128 gate/up 4096->11008, M=1", bits=4, M=1, K=4096, N=11008, G=128,
+                       scheme=2, bias=False, seed=2),
+    "c3_gate_m4": dict(name="C3: INT4 g128 gate/up 4096->11008, M=4", bits=4, M=4, K=4096, N=11008, G=128,
+                       scheme=2, bias=False, seed=2),
+    "c3_gate_m8": dict(name="C3: INT4 g128 gate/up 4096->11008, M=8", bits=4, M=8, K=4096, N=11008, G=128,
+                       scheme=2, bias=False, seed=2),
+    "c3_gate_m16": dict(name="C3: INT4 g128 gate/up 4096->11008, M=16", bits=4, M=16, K=4096, N=11008, G=128,
+                        scheme=2, bias=False, seed=2),
+    "c3_down_m1": dict(name="C3: INT4 g128 down 11008->4096, M=1", bits=4, M=1, K=11008, N=4096, G=128,
+                       scheme=2, bias=False, seed=2),
+    "c3_down_m16": dict(name="C3: INT4 g128 down 11008->4096, M=16", bits=4, M=16, K=11008, N=4096, G=128,
+                        scheme=2, bias=False, seed=2),
+    "c4": dict(name="C4: INT8 per-tensor QuantizedLinear 4096->4096, prefill M=2048", bits=8, M=2048, K=4096,
+               N=4096, G=0, scheme=0, bias=False, seed=3),
+}
+
+
+def alg_bytes(c) -> int:
+    K, N, M = c["K"], c["N"], c["M"]
+    w = K * N // 2 if c["bits"] == 4 else K * N
+    if c["bits"] == 4:
+        ns = (K * N + c["G"] - 1) // c["G"]
+    else:
+        ns = 1 if c["scheme"] == 0 else K
+    return w + 4 * ns + 4 * M * K + 4 * M * N + (4 * N if c["bias"] else 0)
+
+
+def alg_flops(c) -> int:
+    return 2 * c["M"] * c["N"] * c["K"]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Case:
+    """One quantized weight (with `copies` device copies), its input and output."""
+
+    def __init__(self, pkg, c, dev, copies: int):
+        import torch
+        from soverign_grad_amd import synth
+
+        self.pkg, self.c, self.dev = pkg, c, dev
+        self.lib = pkg.load_library()
+        seed = synth.config_seed(c["seed"])
+        t0 = time.time()
+        self.W = synth.normal((c["K"], c["N"]), seed, synth.STREAM_W, 0.0, 0.02)
+        self.x = synth.normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
+        self.b = synth.normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
+        Wd = torch.from_numpy(self.W).to(dev)
+        if c["bits"] == 4:
+            self.qw = pkg.quantize_int4(Wd, c["G"], keep_qdata=False)
+        else:
+            self.qw = pkg.quantize_int8(Wd, c["scheme"], keep_qdata=False)
+        del Wd
+        self.packed = [self.qw.packed] + [self.qw.packed.clone() for _ in range(copies - 1)]
+        self.devscales = None
+        if self.qw.devscales is not None:
+            self.devscales = [self.qw.devscales] + [self.qw.devscales.clone() for _ in range(copies - 1)]
+        self.xd = torch.from_numpy(self.x).to(dev)
+        self.bd = torch.from_numpy(self.b).to(dev) if self.b is not None else None
+        self.y = torch.empty((c["M"], c["N"]), dtype=torch.float32, device=dev)
+        nbytes = self.lib.sgq_linear_workspace_bytes(c["bits"], c["M"], c["K"], c["N"])
+        self.ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        assert self.lib.sgq_workspace_init(self.ws.data_ptr(), self.ws.numel(), stream) == 0
+        torch.cuda.synchronize()
+        log(f"[bench] set up {c['name']} x{copies} copies in {time.time() - t0:.1f}s")
+
+    def launch(self, i: int) -> None:
+        import torch
+
+        c = self.c
+        j = i % len(self.packed)
+        stream = torch.cuda.current_stream(self.dev).cuda_stream
+        bp = self.bd.data_ptr() if self.bd is not None else None
+        if c["bits"] == 4:
+            rc = self.lib.sgq_linear_int4(self.xd.data_ptr(), c["M"], c["K"], c["N"], self.packed[j].data_ptr(),
+                                          self.qw.scales.data_ptr(), self.devscales[j].data_ptr(), c["G"], bp,
+                                          self.y.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream)
+        else:
+            rc = self.lib.sgq_linear_int8(self.xd.data_ptr(), c["M"], c["K"], c["N"], self.packed[j].data_ptr(),
+                                          self.qw.scales.data_ptr(), c["scheme"], bp, self.y.data_ptr(),
+                                          self.ws.data_ptr(), self.ws.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"sgq launch failed: {self.lib.sgq_last_error().decode()}")
+
+    def time_eager(self, steps: int, warmup: int) -> float:
+        import torch
+
+        for i in range(warmup):
+            self.launch(i)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(steps):
+            self.launch(i)
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps  # ms per step
+
+    def time_graph(self, steps: int, warmup: int) -> float:
+        """K launches captured into one hipGraph, replayed once in the timed region."""
+        import torch
+
+        for i in range(warmup):
+            self.launch(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream(self.dev)
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(steps):
+                self.launch(i)
+        g.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / steps
+
+    def check(self, oracle, rows=None) -> float:
+        """max rel error of the last output against the oracle (row subset for big M)."""
+        import torch
+
+        torch.cuda.synchronize()
+        y = self.y.cpu().numpy()
+        q = self.pkg.unpack_codes(self.qw).cpu().numpy()
+        s = self.qw.scales.cpu().numpy()
+        xs = self.x if rows is None else self.x[rows]
+        if self.c["bits"] == 4:
+            yref = oracle.quantized_matmul_int4(xs, q, s, self.c["G"], self.b)
+        else:
+            yref = oracle.quantized_matmul_int8(xs, q, s, self.c["scheme"], self.b)
+        yg = y if rows is None else y[rows]
+        return float(np.max(np.abs(yg.astype(np.float64) - yref)) / max(np.max(np.abs(yref)), 1e-30))
+
+
+def cpu_baseline(c, budget_s: float):
+    """The reference forward (dequantize + matmul + bias) on this host's cores."""
+    from oracle.oracle import Oracle, Reference, reference_available
+    from soverign_grad_amd import synth
+
+    seed = synth.config_seed(c["seed"])
+    W = synth.normal((c["K"], c["N"]), seed, synth.STREAM_W, 0.0, 0.02)
+    x = synth.normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
+    b = synth.normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
+    orc = Oracle()
+    if c["bits"] == 4:
+        q, s = orc.quantize_int4(W, c["G"])
+    else:
+        q, s = orc.quantize_int8(W, c["scheme"])
+    if reference_available():
+        ref = Reference()
+        first, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, 1)
+        reps = int(max(3, min(200, budget_s / max(first[0], 1e-6))))
+        secs, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, reps)
+        kind, cores = "reference", ref.omp_max_threads()
+    else:
+        secs = []
+        t_end = time.time() + budget_s
+        while time.time() < t_end or len(secs) < 3:
+            t0 = time.perf_counter()
+            if c["bits"] == 4:
+                orc.quantized_matmul_int4(x, q, s, c["G"], b)
+            else:
+                orc.quantized_matmul_int8(x, q, s, c["scheme"], b)
+            secs.append(time.perf_counter() - t0)
+            if len(secs) >= 200:
+                break
+        kind, cores = "port", 1
+    med = statistics.median(secs)
+    return {
+        "value": round(alg_bytes(c) / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": f"{c['name']}: {len(secs)} forward calls, median {med * 1e3:.2f} ms "
+                  f"(dequantize + blocked AVX2 matmul + bias), host {platform.processor() or platform.machine()}, "
+                  f"nproc={os.cpu_count()}",
+        "tflops": round(alg_flops(c) / med / 1e12, 4),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--copies", type=int, default=0, help="rotating weight copies (default: > 256 MB)")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the M=2048 GEMM line")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (use --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch
+    import __graft_entry__ as ge
+
+    pkg = ge.load_package()
+    pkg.load_library()
+    from oracle.oracle import Oracle
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    c = CONFIGS[args.config]
+    nbytes = alg_bytes(c)
+    copies = args.copies or max(1, min(64, -(-300_000_000 // nbytes)))
+    log(f"[bench] device {torch.cuda.get_device_name(dev)}; config {args.config}; steps={args.steps} "
+        f"warmup={args.warmup} copies={copies}")
+    case = Case(pkg, c, dev, copies)
+    ms_eager = case.time_eager(min(args.steps, 500), args.warmup)
+    ms = ms_eager if args.eager else case.time_graph(args.steps, args.warmup)
+    err = case.check(Oracle(), rows=None if c["M"] <= 256 else np.r_[0:8, c["M"] - 8:c["M"]])
+    log(f"[bench] {args.config}: {ms * 1e3:.3f} us/step (eager {ms_eager * 1e3:.3f} us), rel_err {err:.2e}")
+    if err > 1e-5:
+        raise SystemExit(f"parity failure in bench: rel err {err}")
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tfl = alg_flops(c) / (ms * 1e-3) / 1e12
+    hbm_bound = c["M"] <= 4
+    roofline = (
+        {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+        if hbm_bound else
+        {"bound": "mfma", "achieved": round(tfl, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+         "frac": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+    )
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded counter RNG; W~N(0,0.02) quantized on device, x~N(0,1))",
+        "config": {"workload": c["name"], "M": c["M"], "K": c["K"], "N": c["N"],
+                   "group_size": c["G"] or None, "bits": c["bits"], "weight_copies": copies,
+                   "launch": "eager" if args.eager else "one hipGraph of K back-to-back forward calls",
+                   "eager_us_per_step": round(ms_eager * 1e3, 3), "tflops": round(tfl, 4),
+                   "rel_err_vs_oracle": err},
+        "roofline": roofline,
+    }
+    del case
+    torch.cuda.empty_cache()
+
+    if not args.no_secondary and args.config == "c2":
+        c4 = CONFIGS["c4"]
+        case4 = Case(pkg, c4, dev, 1)
+        ms4 = case4.time_eager(max(3, min(20, args.steps // 100)), 2)
+        err4 = case4.check(Oracle(), rows=np.r_[0:8, 2040:2048])
+        tfl4 = alg_flops(c4) / (ms4 * 1e-3) / 1e12
+        log(f"[bench] c4: {ms4:.3f} ms/step, {tfl4:.2f} TFLOP/s, rel_err {err4:.2e}")
+        if err4 > 1e-5:
+            raise SystemExit(f"parity failure in bench (c4): rel err {err4}")
+        out["secondary"] = {
+            "metric": "QuantizedLinear TFLOP/s at M=2048 (INT8 per-tensor 4096x4096, fp32 MFMA)",
+            "value": round(tfl4, 3), "unit": "TFLOP/s", "ms_per_step": round(ms4, 4),
+            "workload": c4["name"], "rel_err_vs_oracle": err4,
+            "roofline": {"bound": "mfma", "achieved": round(tfl4, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tfl4 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        }
+        del case4
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        t0 = time.time()
+        out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget)
+        log(f"[bench] cpu baseline {out['cpu_baseline']['value']} GB/s in {time.time() - t0:.1f}s")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,177 @@
+/*
+ * sgq.h -- C ABI of the MI355X (gfx950) quantized-linear library, libsgq.so.
+ *
+ * This is the drop-in boundary for SovereignGrad's quantized inference path.
+ * Each entry point replaces one piece of the reference (paths relative to the
+ * reference checkout); the reference has no GPU code for this path, so these
+ * replace its host functions, called with device pointers.
+ *
+ * Conventions (shared by every function below):
+ *   - Plain pointers and sizes.  Every pointer argument is DEVICE memory
+ *     (hipMalloc'd or equivalent) unless stated otherwise.  The library never
+ *     allocates or frees; callers own every buffer, including workspaces.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default
+ *     stream.  Calls are asynchronous on that stream unless stated otherwise.
+ *   - Return value: SGQ_OK (0) or an SGQ_ERR_* code.  sgq_last_error() gives
+ *     a message for the calling thread's most recent failure.  Argument errors
+ *     are detected before anything is launched.
+ *   - Reentrant: no mutable global state; safe to call concurrently from
+ *     several host threads as long as each concurrent call has its own
+ *     workspace.
+ *
+ * Weight shape convention: W is [K, N] row-major ([in_features,
+ * out_features], include/sovereigngrad/nn.hpp:938) and the forward is
+ * y[M,N] = x[M,K] . dequant(W) (+ bias[1,N]) (src/quantization.cpp:189-206).
+ *
+ * Device layouts ("packed" buffers) are this library's own; they are built by
+ * sgq_quantize_* or sgq_pack_* and read back with sgq_unpack_* /
+ * sgq_dequantize_*.  The reference-layout tensors (fp32 codes `qdata` [K,N],
+ * fp32 `scales`) are bit-identical to what the reference produces.
+ */
+#ifndef SGQ_H
+#define SGQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define SGQ_OK 0
+#define SGQ_ERR_INVALID_ARGUMENT 1 /* null pointer, negative size, bad scheme   */
+#define SGQ_ERR_UNSUPPORTED 2      /* shape/layout combination not supported   */
+#define SGQ_ERR_WORKSPACE 3        /* workspace missing or too small           */
+#define SGQ_ERR_HIP 4              /* a HIP runtime call failed                */
+#define SGQ_ERR_CODES 5            /* codes not integral / out of range (pack) */
+
+/* ---- quantization schemes (include/sovereigngrad/quantization.hpp:11-15) */
+#define SGQ_PER_TENSOR_SYMMETRIC 0
+#define SGQ_PER_CHANNEL_SYMMETRIC 1
+#define SGQ_GROUPED_ASYMMETRIC 2
+
+/* ---- INT4 device layouts ----------------------------------------------- */
+#define SGQ_LAYOUT_INT4_TILED 0 /* N % 8 == 0 and group % 8 == 0: fast kernels */
+#define SGQ_LAYOUT_INT4_FLAT 1  /* any shape: flat nibble stream, generic kernels */
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* sgq_last_error(void);
+
+/* Library ABI version (SGQ_ABI_VERSION). */
+int sgq_abi_version(void);
+
+/* ---- size queries (host-only; no GPU work) ----------------------------- */
+
+/* Bytes of the packed INT8 buffer for a [K,N] weight. */
+int64_t sgq_int8_packed_bytes(int64_t K, int64_t N);
+
+/* INT4 layout chosen for a [K,N] weight with this group size
+ * (group_size <= 0 means 32, as src/quantization.cpp:118). */
+int sgq_int4_layout(int64_t K, int64_t N, int64_t group_size);
+
+/* Bytes of the packed INT4 buffer for a [K,N] weight. */
+int64_t sgq_int4_packed_bytes(int64_t K, int64_t N, int64_t group_size);
+
+/* Number of floats in the INT4 device-scale buffer (0 for the flat layout,
+ * which reads the reference-layout scales directly). */
+int64_t sgq_int4_devscale_count(int64_t K, int64_t N, int64_t group_size);
+
+/* Number of reference-layout scales: 1 (per-tensor), rows (per-channel),
+ * ceil(rows*cols/group) (INT4), following src/quantization.cpp:22,44-48,119. */
+int64_t sgq_int8_scale_count(int64_t rows, int64_t cols, int scheme);
+int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size);
+
+/* Workspace bytes needed by sgq_quantize_int8 / sgq_quantize_int4 / sgq_pack_*. */
+int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size);
+
+/* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
+ * The workspace must be zero-filled once before its first use (for example
+ * with sgq_workspace_init); every call leaves it ready for the next one. */
+int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
+
+/* Zero-fills a workspace with a kernel (no hipMemset), on `stream`. */
+int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- quantize (construction path) ------------------------------------- */
+
+/* Replaces quantization::quantize_int8 (src/quantization.cpp:11-78) for a
+ * device tensor viewed as [rows, cols].  scheme SGQ_PER_TENSOR_SYMMETRIC or
+ * SGQ_PER_CHANNEL_SYMMETRIC; per-channel means one scale per row, like the
+ * reference.  (The reference also takes the per-tensor branch for rank<2
+ * tensors; callers pass scheme 0 for those.)
+ *   qdata_f32  optional [rows*cols] fp32 codes in reference layout, bit-exact
+ *              (including -0.0 codes).
+ *   scales     required, sgq_int8_scale_count() floats, bit-exact.
+ *   packed     optional, sgq_int8_packed_bytes(rows, cols) bytes (K=rows, N=cols).
+ */
+int sgq_quantize_int8(const float* x, int64_t rows, int64_t cols, int scheme, float* qdata_f32,
+                      float* scales, void* packed, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces quantization::quantize_int4 (src/quantization.cpp:113-159): groups
+ * of group_size consecutive elements of the flattened tensor (group_size <= 0
+ * means 32).  The packed layout treats the tensor as [rows, cols].
+ *   qdata_f32  optional [rows*cols] fp32 codes, bit-exact.
+ *   scales     required, sgq_int4_scale_count() floats, bit-exact.
+ *   packed     optional, sgq_int4_packed_bytes() bytes.
+ *   devscales  required when packed is given and the layout is TILED
+ *              (sgq_int4_devscale_count() floats), else ignored.
+ */
+int sgq_quantize_int4(const float* x, int64_t rows, int64_t cols, int64_t group_size, float* qdata_f32,
+                      float* scales, void* packed, float* devscales, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/* ---- repack / unpack (persistence bridge) ------------------------------ */
+
+/* Packs reference-layout fp32 codes (as stored in a QuantizedTensor's qdata,
+ * or loaded by load_state_dict, src/module.cpp:114-134) into the device layout.
+ * Returns SGQ_ERR_CODES (after synchronising `stream`) when a code is not an
+ * integer in [-127,127] (INT8) or [-8,7] (INT4). */
+int sgq_pack_int8(const float* qdata_f32, int64_t K, int64_t N, void* packed, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+int sgq_pack_int4(const float* qdata_f32, const float* scales, int64_t K, int64_t N, int64_t group_size,
+                  void* packed, float* devscales, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Writes the fp32 codes [K,N] in reference layout from a packed buffer (codes
+ * that were -0.0 come back as +0.0; every other code is exact). */
+int sgq_unpack_int8(const void* packed, int64_t K, int64_t N, float* qdata_f32, void* stream);
+int sgq_unpack_int4(const void* packed, int64_t K, int64_t N, int64_t group_size, float* qdata_f32,
+                    void* stream);
+
+/* ---- dequantize ------------------------------------------------------- */
+
+/* Replaces quantization::dequantize_int8 (src/quantization.cpp:80-111):
+ * out[k,n] = code * scale with one IEEE multiply, scale = scales[0] for
+ * per-tensor, scales[k] for per-channel. */
+int sgq_dequantize_int8(const void* packed, const float* scales, int scheme, int64_t K, int64_t N, float* out,
+                        void* stream);
+
+/* Replaces quantization::dequantize_int4 (src/quantization.cpp:161-187):
+ * out[i] = code[i] * scales[i / group_size] over the flattened [K,N]. */
+int sgq_dequantize_int4(const void* packed, const float* scales, int64_t K, int64_t N, int64_t group_size,
+                        float* out, void* stream);
+
+/* ---- forward ---------------------------------------------------------- */
+
+/* Replaces quantization::quantized_matmul_int8 (src/quantization.cpp:189-197)
+ * and with it nn::QuantizedLinear::forward (include/sovereigngrad/nn.hpp:956-958):
+ *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
+ * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
+ * Dispatch: M <= 16 runs the wavefront GEMV/skinny kernel, larger M the
+ * LDS-staged fp32-MFMA GEMM.  workspace: sgq_linear_workspace_bytes(8, M, K, N). */
+int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                    int scheme, const float* bias, float* y, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+
+/* Replaces quantization::quantized_matmul_int4 (src/quantization.cpp:199-206)
+ * and nn::QuantizedLinear4Bit::forward (include/sovereigngrad/nn.hpp:994-996).
+ * scales: the reference-layout scales (used by the FLAT layout); devscales:
+ * the device scales written by sgq_quantize_int4/sgq_pack_int4 (TILED layout). */
+int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                    const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGQ_H */

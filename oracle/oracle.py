@@ -1,0 +1,229 @@
+"""ctypes front end of the CPU oracle.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module.  It loads:
+
+  oracle/liboracle.so    the C restatement of the reference path (sgq_oracle.c);
+  oracle/_ref/libsgref.so  the reference's own sources compiled in place
+                         (oracle/Makefile target `ref`), when it has been built.
+
+Both expose the same operations, returned as numpy arrays, so a test can run a
+case through either and compare.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional, Tuple
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+ORACLE_LIB = ORACLE_DIR / "liboracle.so"
+REF_LIB = ORACLE_DIR / "_ref" / "libsgref.so"
+
+_i64, _int, _vp, _dbl = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Oracle:
+    """The C restatement (sgq_oracle.c)."""
+
+    def __init__(self, path: Path = ORACLE_LIB):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = ctypes.CDLL(str(path))
+        L.oracle_quantize_int8_per_tensor.argtypes = [_vp, _i64, _vp, _vp]
+        L.oracle_quantize_int8_per_channel.argtypes = [_vp, _i64, _i64, _vp, _vp]
+        L.oracle_dequantize_int8.argtypes = [_vp, _vp, _i64, _i64, _int, _vp]
+        L.oracle_int4_num_groups.argtypes = [_i64, _i64]
+        L.oracle_int4_num_groups.restype = _i64
+        L.oracle_quantize_int4.argtypes = [_vp, _i64, _i64, _vp, _vp]
+        L.oracle_dequantize_int4.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp]
+        L.oracle_matmul.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64]
+        L.oracle_add_row_bias.argtypes = [_vp, _vp, _i64, _i64]
+        L.oracle_quantized_matmul_int8.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp]
+        L.oracle_quantized_matmul_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp]
+        L.oracle_matmul_f64.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64]
+
+    # quantize_int8: per-tensor for scheme 0 or rank < 2 (src/quantization.cpp:22)
+    def quantize_int8(self, x: np.ndarray, scheme: int) -> Tuple[np.ndarray, np.ndarray]:
+        x = _f32(x)
+        q = np.empty_like(x)
+        if scheme == 0 or x.ndim < 2:
+            s = np.empty(1, np.float32)
+            self.lib.oracle_quantize_int8_per_tensor(_p(x), x.size, _p(q), _p(s))
+        else:
+            rows = x.shape[0]
+            s = np.empty(rows, np.float32)
+            self.lib.oracle_quantize_int8_per_channel(_p(x), rows, x.size // rows, _p(q), _p(s))
+        return q, s
+
+    def dequantize_int8(self, q: np.ndarray, s: np.ndarray, scheme: int) -> np.ndarray:
+        q, s = _f32(q), _f32(s)
+        out = np.empty_like(q)
+        rows = q.shape[0] if q.ndim >= 2 else 1
+        per_tensor = 1 if (scheme == 0 or s.size == 1) else 0
+        self.lib.oracle_dequantize_int8(_p(q), _p(s), rows, q.size // max(rows, 1), per_tensor, _p(out))
+        return out
+
+    def quantize_int4(self, x: np.ndarray, group_size: int = 32) -> Tuple[np.ndarray, np.ndarray]:
+        x = _f32(x)
+        q = np.empty_like(x)
+        s = np.empty(self.lib.oracle_int4_num_groups(x.size, group_size), np.float32)
+        self.lib.oracle_quantize_int4(_p(x), x.size, group_size, _p(q), _p(s))
+        return q, s
+
+    def dequantize_int4(self, q: np.ndarray, s: np.ndarray, group_size: int) -> np.ndarray:
+        q, s = _f32(q), _f32(s)
+        out = np.empty_like(q)
+        g = group_size if group_size > 0 else 32
+        self.lib.oracle_dequantize_int4(_p(q), _p(s), q.size, g, s.size, _p(out))
+        return out
+
+    def matmul(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        a, b = _f32(a), _f32(b)
+        out = np.empty((a.shape[0], b.shape[1]), np.float32)
+        self.lib.oracle_matmul(_p(a), _p(b), _p(out), a.shape[0], a.shape[1], b.shape[1])
+        return out
+
+    def quantized_matmul_int8(self, x, q, s, scheme: int, bias=None) -> np.ndarray:
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        out = np.empty((x.shape[0], q.shape[1]), np.float32)
+        per_tensor = 1 if (scheme == 0 or s.size == 1) else 0
+        b = None if bias is None else _f32(bias).reshape(-1)
+        self.lib.oracle_quantized_matmul_int8(_p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s), per_tensor,
+                                              _p(b), _p(out))
+        return out
+
+    def quantized_matmul_int4(self, x, q, s, group_size: int, bias=None) -> np.ndarray:
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        out = np.empty((x.shape[0], q.shape[1]), np.float32)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        self.lib.oracle_quantized_matmul_int4(_p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s), group_size,
+                                              _p(b), _p(out))
+        return out
+
+    def matmul_f64(self, a: np.ndarray, b: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+        a, b = _f32(a), _f32(b)
+        c = np.empty((a.shape[0], b.shape[1]), np.float64)
+        cabs = np.empty_like(c)
+        self.lib.oracle_matmul_f64(_p(a), _p(b), _p(c), _p(cabs), a.shape[0], a.shape[1], b.shape[1])
+        return c, cabs
+
+
+class Reference:
+    """The reference's own code, compiled by oracle/Makefile (`ref` target)."""
+
+    def __init__(self, path: Path = REF_LIB):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where the reference is mounted")
+        L = self.lib = ctypes.CDLL(str(path))
+        L.ref_quantize_int8.argtypes = [_vp, _i64, _i64, _int, _int, _vp, _vp]
+        L.ref_quantize_int8.restype = _i64
+        L.ref_quantize_int4.argtypes = [_vp, _i64, _i64, _int, _i64, _vp, _vp]
+        L.ref_quantize_int4.restype = _i64
+        L.ref_dequantize_int8.argtypes = [_vp, _vp, _i64, _i64, _i64, _int, _vp]
+        L.ref_dequantize_int4.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp]
+        L.ref_quantized_matmul_int8.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _int, _vp, _vp]
+        L.ref_quantized_matmul_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp]
+        L.ref_matmul.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp]
+        L.ref_time_quantized_matmul.argtypes = [_int, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _int, _i64, _vp, _int,
+                                                ctypes.POINTER(_dbl), _vp]
+        L.ref_omp_max_threads.restype = _int
+
+    @staticmethod
+    def _rc(x: np.ndarray):
+        if x.ndim >= 2:
+            return x.shape[0], x.size // max(x.shape[0], 1), 2
+        return 1, x.size, 1
+
+    def quantize_int8(self, x: np.ndarray, scheme: int):
+        x = _f32(x)
+        rows, cols, rank = self._rc(x)
+        q = np.empty_like(x)
+        s = np.empty(max(rows, 1), np.float32)
+        n = self.lib.ref_quantize_int8(_p(x), rows, cols, rank, scheme, _p(q), _p(s))
+        if n < 0:
+            raise RuntimeError("reference quantize_int8 raised")
+        return q, s[:n].copy()
+
+    def quantize_int4(self, x: np.ndarray, group_size: int = 32):
+        x = _f32(x)
+        rows, cols, rank = self._rc(x)
+        g = group_size if group_size > 0 else 32
+        q = np.empty_like(x)
+        s = np.empty(max((x.size + g - 1) // g, 1), np.float32)
+        n = self.lib.ref_quantize_int4(_p(x), rows, cols, rank, group_size, _p(q), _p(s))
+        if n < 0:
+            raise RuntimeError("reference quantize_int4 raised")
+        return q, s[:n].copy()
+
+    def dequantize_int8(self, q, s, scheme: int):
+        q, s = _f32(q), _f32(s)
+        out = np.empty_like(q)
+        rows = q.shape[0]
+        if self.lib.ref_dequantize_int8(_p(q), _p(s), s.size, rows, q.size // rows, scheme, _p(out)) != 0:
+            raise RuntimeError("reference dequantize_int8 raised")
+        return out
+
+    def dequantize_int4(self, q, s, group_size: int):
+        q, s = _f32(q), _f32(s)
+        out = np.empty_like(q)
+        rows = q.shape[0]
+        if self.lib.ref_dequantize_int4(_p(q), _p(s), s.size, rows, q.size // rows, group_size, _p(out)) != 0:
+            raise RuntimeError("reference dequantize_int4 raised")
+        return out
+
+    def matmul(self, a, b):
+        a, b = _f32(a), _f32(b)
+        out = np.empty((a.shape[0], b.shape[1]), np.float32)
+        if self.lib.ref_matmul(_p(a), _p(b), a.shape[0], a.shape[1], b.shape[1], _p(out)) != 0:
+            raise RuntimeError("reference matmul raised")
+        return out
+
+    def quantized_matmul_int8(self, x, q, s, scheme: int, bias=None):
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        out = np.empty((x.shape[0], q.shape[1]), np.float32)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        rc = self.lib.ref_quantized_matmul_int8(_p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s), s.size,
+                                                scheme, _p(b), _p(out))
+        if rc != 0:
+            raise RuntimeError("reference quantized_matmul_int8 raised")
+        return out
+
+    def quantized_matmul_int4(self, x, q, s, group_size: int, bias=None):
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        out = np.empty((x.shape[0], q.shape[1]), np.float32)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        rc = self.lib.ref_quantized_matmul_int4(_p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s), s.size,
+                                                group_size, _p(b), _p(out))
+        if rc != 0:
+            raise RuntimeError("reference quantized_matmul_int4 raised")
+        return out
+
+    def time_quantized_matmul(self, bits: int, x, q, s, scheme: int, group_size: int, bias, reps: int):
+        """Per-call seconds of the reference forward (dequantize + matmul + bias)."""
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        secs = (_dbl * reps)()
+        out = np.empty((x.shape[0], q.shape[1]), np.float32)
+        rc = self.lib.ref_time_quantized_matmul(bits, _p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s),
+                                                s.size, scheme, group_size, _p(b), reps, secs, _p(out))
+        if rc != 0:
+            raise RuntimeError("reference forward raised")
+        return list(secs), out
+
+    def omp_max_threads(self) -> int:
+        return int(self.lib.ref_omp_max_threads())
+
+
+def reference_available() -> bool:
+    return REF_LIB.exists()

@@ -1,0 +1,188 @@
+// ref_shim.cpp -- C entry points over the compiled reference library.
+//
+// TEST INFRASTRUCTURE ONLY.  Built by oracle/Makefile together with the
+// reference's own sources (read in place under the reference checkout) into
+// oracle/_ref/libsgref.so.  Used to pin the C restatement (sgq_oracle.c), to
+// write the golden fixtures in tests/golden/, and as the "reference" CPU
+// baseline timed by bench.py.  The product library never links it.
+//
+// Each function wraps one reference entry point unchanged:
+//   ref_quantize_int8         quantization::quantize_int8   (src/quantization.cpp:11-78)
+//   ref_dequantize_int8       quantization::dequantize_int8 (src/quantization.cpp:80-111)
+//   ref_quantize_int4         quantization::quantize_int4   (src/quantization.cpp:113-159)
+//   ref_dequantize_int4       quantization::dequantize_int4 (src/quantization.cpp:161-187)
+//   ref_quantized_matmul_int8 quantization::quantized_matmul_int8 (src/quantization.cpp:189-197)
+//   ref_quantized_matmul_int4 quantization::quantized_matmul_int4 (src/quantization.cpp:199-206)
+//   ref_matmul                matmul (src/ops.cpp:378-455)
+#include "sovereigngrad/quantization.hpp"
+#include "sovereigngrad/ops.hpp"
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+using namespace sovereigngrad;
+using quantization::QuantizationScheme;
+using quantization::QuantizedTensor;
+
+namespace {
+
+std::vector<int64_t> make_shape(int64_t rows, int64_t cols, int rank) {
+    if (rank == 1) return {rows * cols};
+    return {rows, cols};
+}
+
+Tensor from_host(const float* p, const std::vector<int64_t>& shape) {
+    int64_t n = 1;
+    for (auto d : shape) n *= d;
+    std::vector<float> v(p, p + n);
+    return Tensor(v, shape, Device::CPU, false);
+}
+
+void to_host(const Tensor& t, float* out) {
+    Tensor c = t.to(Device::CPU).contiguous();
+    std::memcpy(out, c.data(), sizeof(float) * (size_t)c.numel());
+}
+
+QuantizedTensor make_qt(const float* q, const float* scales, int64_t nscales, int64_t K, int64_t N,
+                        int scheme, int64_t group_size, int bits) {
+    QuantizedTensor qt;
+    qt.qdata = from_host(q, {K, N});
+    qt.scales = from_host(scales, {nscales});
+    qt.scheme = static_cast<QuantizationScheme>(scheme);
+    qt.original_shape = {K, N};
+    qt.group_size = group_size;
+    qt.bits = bits;
+    return qt;
+}
+
+}  // namespace
+
+extern "C" {
+
+// scheme: 0 PerTensorSymmetric, 1 PerChannelSymmetric (quantization.hpp:11-15).
+// Writes qdata[rows*cols] and scales; returns the scale count, or -1 on error.
+int64_t ref_quantize_int8(const float* x, int64_t rows, int64_t cols, int rank, int scheme, float* q,
+                          float* scales) {
+    try {
+        Tensor t = from_host(x, make_shape(rows, cols, rank));
+        QuantizedTensor qt = quantization::quantize_int8(t, static_cast<QuantizationScheme>(scheme));
+        to_host(qt.qdata, q);
+        to_host(qt.scales, scales);
+        return qt.scales.numel();
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int64_t ref_quantize_int4(const float* x, int64_t rows, int64_t cols, int rank, int64_t group_size, float* q,
+                          float* scales) {
+    try {
+        Tensor t = from_host(x, make_shape(rows, cols, rank));
+        QuantizedTensor qt = quantization::quantize_int4(t, group_size);
+        to_host(qt.qdata, q);
+        to_host(qt.scales, scales);
+        return qt.scales.numel();
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_dequantize_int8(const float* q, const float* scales, int64_t nscales, int64_t K, int64_t N, int scheme,
+                        float* out) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, scheme, K * N, 8);
+        to_host(quantization::dequantize_int8(qt), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_dequantize_int4(const float* q, const float* scales, int64_t nscales, int64_t K, int64_t N,
+                        int64_t group_size, float* out) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, 2, group_size, 4);
+        to_host(quantization::dequantize_int4(qt), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_quantized_matmul_int8(const float* x, int64_t M, int64_t K, int64_t N, const float* q, const float* scales,
+                              int64_t nscales, int scheme, const float* bias, float* out) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, scheme, K * N, 8);
+        Tensor tx = from_host(x, {M, K});
+        Tensor tb = bias ? from_host(bias, {1, N}) : Tensor();
+        to_host(quantization::quantized_matmul_int8(tx, qt, tb), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_quantized_matmul_int4(const float* x, int64_t M, int64_t K, int64_t N, const float* q, const float* scales,
+                              int64_t nscales, int64_t group_size, const float* bias, float* out) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, 2, group_size, 4);
+        Tensor tx = from_host(x, {M, K});
+        Tensor tb = bias ? from_host(bias, {1, N}) : Tensor();
+        to_host(quantization::quantized_matmul_int4(tx, qt, tb), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_matmul(const float* a, const float* b, int64_t M, int64_t K, int64_t N, float* out) {
+    try {
+        to_host(matmul(from_host(a, {M, K}), from_host(b, {K, N})), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Times `reps` calls of the reference forward (dequantize + matmul + bias) on
+// tensors built once outside the timed region.  bits selects the INT8 or INT4
+// entry point.  Writes per-call seconds into secs[reps]; returns 0 on success.
+int ref_time_quantized_matmul(int bits, const float* x, int64_t M, int64_t K, int64_t N, const float* q,
+                              const float* scales, int64_t nscales, int scheme, int64_t group_size,
+                              const float* bias, int reps, double* secs, float* out) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, bits == 8 ? scheme : 2,
+                                     bits == 8 ? K * N : group_size, bits);
+        Tensor tx = from_host(x, {M, K});
+        Tensor tb = bias ? from_host(bias, {1, N}) : Tensor();
+        Tensor y;
+        for (int r = 0; r < reps; ++r) {
+            auto t0 = std::chrono::steady_clock::now();
+            y = bits == 8 ? quantization::quantized_matmul_int8(tx, qt, tb)
+                          : quantization::quantized_matmul_int4(tx, qt, tb);
+            auto t1 = std::chrono::steady_clock::now();
+            secs[r] = std::chrono::duration<double>(t1 - t0).count();
+        }
+        if (out) to_host(y, out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_omp_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+/*
+ * sgq_oracle.c -- CPU restatement of SovereignGrad's quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the GPU path is compared
+ * against.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it; the product library (libsgq.so) never links or calls it.
+ *
+ * Every function restates one piece of the reference, cited file:line
+ * (paths relative to the reference checkout):
+ *
+ *   oracle_quantize_int8_per_tensor   src/quantization.cpp:22-41
+ *   oracle_quantize_int8_per_channel  src/quantization.cpp:42-75
+ *   oracle_dequantize_int8            src/quantization.cpp:80-111
+ *   oracle_quantize_int4              src/quantization.cpp:113-159
+ *   oracle_dequantize_int4            src/quantization.cpp:161-187
+ *   oracle_matmul                     src/ops.cpp:378-455 with
+ *                                     include/sovereigngrad/simd.hpp:152-221
+ *   oracle_add_row_bias               src/ops.cpp:132-171
+ *   oracle_quantized_matmul_int8      src/quantization.cpp:189-197
+ *   oracle_quantized_matmul_int4      src/quantization.cpp:199-206
+ *
+ * Floating-point contract.  The reference is built with GCC -O3 -mavx2 -mfma
+ * in gnu++17 mode, where -ffp-contract=fast is the default, so every
+ * `c += a * b` in its matmul becomes one fused multiply-add.  This file is
+ * compiled with -ffp-contract=off and spells each fused operation out as
+ * fmaf(); every other operation is a single IEEE op.  Parity of every function
+ * here is pinned by tests/test_oracle.py against the compiled reference
+ * (oracle/_ref) through the golden fixtures in tests/golden/, and by closed
+ * forms and special cases.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* std::max(lo, std::min(hi, v)) exactly as <algorithm> defines them:
+ * std::min(a, b) = (b < a) ? b : a;  std::max(a, b) = (a < b) ? b : a.
+ * A NaN v therefore yields hi (src/quantization.cpp:37,69,152). */
+static inline float ref_clamp(float v, float lo, float hi) {
+    float m = (v < hi) ? v : hi;
+    return (lo < m) ? m : lo;
+}
+
+/* max_abs starts at 1e-8f and is replaced only when fabs(x) > max_abs, so a
+ * NaN never wins (src/quantization.cpp:23-27, 57-61, 140-144). */
+static inline float ref_absmax(const float* x, int64_t n) {
+    float m = 1e-8f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i]);
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+/* src/quantization.cpp:22-41 */
+void oracle_quantize_int8_per_tensor(const float* x, int64_t total, float* q, float* scale_out) {
+    float max_abs = ref_absmax(x, total);
+    float scale = max_abs / 127.0f;
+    float inv_scale = 127.0f / max_abs;
+    for (int64_t i = 0; i < total; ++i) {
+        float v = roundf(x[i] * inv_scale);
+        q[i] = ref_clamp(v, -127.0f, 127.0f);
+    }
+    scale_out[0] = scale;
+}
+
+/* src/quantization.cpp:42-75: one scale per row r of x viewed as [rows, total/rows]. */
+void oracle_quantize_int8_per_channel(const float* x, int64_t rows, int64_t cols, float* q, float* scales) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float max_abs = ref_absmax(xr, cols);
+        float scale = max_abs / 127.0f;
+        float inv_scale = 127.0f / max_abs;
+        scales[r] = scale;
+        for (int64_t c = 0; c < cols; ++c) {
+            float v = roundf(xr[c] * inv_scale);
+            q[r * cols + c] = ref_clamp(v, -127.0f, 127.0f);
+        }
+    }
+}
+
+/* src/quantization.cpp:80-111.  per_tensor mirrors the branch condition
+ * `scheme == PerTensorSymmetric || scales.numel() == 1` (:90). */
+void oracle_dequantize_int8(const float* q, const float* scales, int64_t rows, int64_t cols,
+                            int per_tensor, float* out) {
+    int64_t total = rows * cols;
+    if (per_tensor) {
+        float s = scales[0];
+        for (int64_t i = 0; i < total; ++i) out[i] = q[i] * s;
+    } else {
+        for (int64_t r = 0; r < rows; ++r) {
+            float s = scales[r];
+            for (int64_t c = 0; c < cols; ++c) out[r * cols + c] = q[r * cols + c] * s;
+        }
+    }
+}
+
+/* src/quantization.cpp:113-159: groups of group_size contiguous elements of
+ * the flattened tensor; group_size <= 0 means 32 (:118); last group partial. */
+int64_t oracle_int4_num_groups(int64_t total, int64_t group_size) {
+    if (group_size <= 0) group_size = 32;
+    return (total + group_size - 1) / group_size;
+}
+
+void oracle_quantize_int4(const float* x, int64_t total, int64_t group_size, float* q, float* scales) {
+    if (group_size <= 0) group_size = 32;
+    int64_t num_groups = (total + group_size - 1) / group_size;
+    for (int64_t g = 0; g < num_groups; ++g) {
+        int64_t g_start = g * group_size;
+        int64_t g_end = g_start + group_size < total ? g_start + group_size : total;
+        float max_abs = ref_absmax(x + g_start, g_end - g_start);
+        float scale = max_abs / 7.0f;
+        float inv_scale = 7.0f / max_abs;
+        scales[g] = scale;
+        for (int64_t i = g_start; i < g_end; ++i) {
+            float v = roundf(x[i] * inv_scale);
+            q[i] = ref_clamp(v, -8.0f, 7.0f);
+        }
+    }
+}
+
+/* src/quantization.cpp:161-187 */
+void oracle_dequantize_int4(const float* q, const float* scales, int64_t total, int64_t group_size,
+                            int64_t num_groups, float* out) {
+    for (int64_t g = 0; g < num_groups; ++g) {
+        int64_t g_start = g * group_size;
+        int64_t g_end = g_start + group_size < total ? g_start + group_size : total;
+        float s = scales[g];
+        for (int64_t i = g_start; i < g_end; ++i) out[i] = q[i] * s;
+    }
+}
+
+/* src/ops.cpp:378-455.  Output zero-filled (:393,:399); tiles of 32 rows x 64
+ * columns, k-blocks of 128 visited in order (:401-403,:411-413).  Inside a
+ * tile: full 8-row x 8-column blocks run the AVX2 micro-kernel, which loads
+ * C, adds one fused multiply-add per k in order and stores C back
+ * (simd.hpp:152-221); the column tail of an 8-row group sums its k-block into
+ * a zero-started local accumulator (contracted to FMA) and then adds it to C
+ * with a plain add (:426-434); rows left over after the 8-row groups take
+ * `c += a*b` per k in order, contracted to FMA (:436-443).  Tiles are
+ * independent, so the OpenMP schedule does not change any result. */
+void oracle_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
+    const int64_t BLOCK_M = 32, BLOCK_N = 64, BLOCK_K = 128;
+    memset(C, 0, (size_t)(M * N) * sizeof(float));
+    for (int64_t i0 = 0; i0 < M; i0 += BLOCK_M) {
+        for (int64_t j0 = 0; j0 < N; j0 += BLOCK_N) {
+            int64_t i_max = i0 + BLOCK_M < M ? i0 + BLOCK_M : M;
+            int64_t j_max = j0 + BLOCK_N < N ? j0 + BLOCK_N : N;
+            for (int64_t k0 = 0; k0 < K; k0 += BLOCK_K) {
+                int64_t k_max = k0 + BLOCK_K < K ? k0 + BLOCK_K : K;
+                int64_t i = i0;
+                for (; i + 8 <= i_max; i += 8) {
+                    int64_t j = j0;
+                    for (; j + 8 <= j_max; j += 8) {
+                        for (int64_t r = 0; r < 8; ++r) {
+                            for (int64_t c = 0; c < 8; ++c) {
+                                float acc = C[(i + r) * N + j + c];
+                                for (int64_t k = k0; k < k_max; ++k)
+                                    acc = fmaf(A[(i + r) * K + k], B[k * N + j + c], acc);
+                                C[(i + r) * N + j + c] = acc;
+                            }
+                        }
+                    }
+                    for (; j < j_max; ++j) {
+                        for (int64_t r = 0; r < 8; ++r) {
+                            float acc = 0.0f;
+                            for (int64_t k = k0; k < k_max; ++k)
+                                acc = fmaf(A[(i + r) * K + k], B[k * N + j], acc);
+                            C[(i + r) * N + j] += acc;
+                        }
+                    }
+                }
+                for (; i < i_max; ++i) {
+                    for (int64_t k = k0; k < k_max; ++k) {
+                        float a_ik = A[i * K + k];
+                        for (int64_t j = j0; j < j_max; ++j)
+                            C[i * N + j] = fmaf(a_ik, B[k * N + j], C[i * N + j]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* src/ops.cpp:132-171 for out[M,N] + bias[1,N]: the broadcast branch computes
+ * va + vb per element (:149-165); the equal-shape branch (M == 1) is
+ * simd::vec_add, the same single addition per element (simd.hpp:15-28). */
+void oracle_add_row_bias(float* out, const float* bias, int64_t M, int64_t N) {
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) out[i * N + j] = out[i * N + j] + bias[j];
+}
+
+/* src/quantization.cpp:189-197: dequantize, matmul, optional bias. */
+void oracle_quantized_matmul_int8(const float* x, int64_t M, int64_t K, int64_t N, const float* q,
+                                  const float* scales, int per_tensor, const float* bias, float* out) {
+    float* w = (float*)malloc((size_t)(K * N > 0 ? K * N : 1) * sizeof(float));
+    oracle_dequantize_int8(q, scales, K, N, per_tensor, w);
+    oracle_matmul(x, w, out, M, K, N);
+    if (bias) oracle_add_row_bias(out, bias, M, N);
+    free(w);
+}
+
+/* src/quantization.cpp:199-206 */
+void oracle_quantized_matmul_int4(const float* x, int64_t M, int64_t K, int64_t N, const float* q,
+                                  const float* scales, int64_t group_size, const float* bias, float* out) {
+    if (group_size <= 0) group_size = 32;
+    int64_t total = K * N;
+    float* w = (float*)malloc((size_t)(total > 0 ? total : 1) * sizeof(float));
+    oracle_dequantize_int4(q, scales, total, group_size, oracle_int4_num_groups(total, group_size), w);
+    oracle_matmul(x, w, out, M, K, N);
+    if (bias) oracle_add_row_bias(out, bias, M, N);
+    free(w);
+}
+
+/* fp64 reference dot products for tolerance pinning: out[m,n] = sum_k x[m,k]*w[k,n]
+ * in double, plus the magnitude sum_k |x||w| used for error floors. */
+void oracle_matmul_f64(const float* A, const float* B, double* C, double* Cabs, int64_t M, int64_t K, int64_t N) {
+    for (int64_t i = 0; i < M; ++i) {
+        for (int64_t j = 0; j < N; ++j) { C[i * N + j] = 0.0; Cabs[i * N + j] = 0.0; }
+        for (int64_t k = 0; k < K; ++k) {
+            double a = A[i * K + k];
+            for (int64_t j = 0; j < N; ++j) {
+                double b = B[k * N + j];
+                C[i * N + j] += a * b;
+                Cabs[i * N + j] += fabs(a * b);
+            }
+        }
+    }
+}

@@ -1,0 +1,351 @@
+// sgq_abi.hip -- the extern "C" entry points of libsgq.so (declared in include/sgq.h).
+//
+// Every function validates its arguments on the host, then enqueues kernels
+// on the caller's stream.  No allocation, no global mutable state; the only
+// per-thread state is the last error message.
+#include "sgq.h"
+#include "sgq_internal.h"
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#define SGQ_ABI_VERSION 1
+
+using namespace sgq;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return SGQ_OK;
+}
+
+#define SGQ_HIP(expr, what)                                                                   \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess) return fail(SGQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+constexpr int64_t kAlign = 256;
+constexpr int64_t kPartialMax = 1024;
+
+int64_t align_up(int64_t v) { return round_up(v, kAlign); }
+
+// Quantize / pack workspace: [inv: ngroups floats][partials: 1024 floats][bad flag].
+struct QuantWs {
+    int64_t inv_off, part_off, bad_off, total;
+};
+QuantWs quant_ws(int64_t ngroups) {
+    QuantWs w;
+    w.inv_off = 0;
+    w.part_off = align_up((ngroups > 0 ? ngroups : 1) * 4);
+    w.bad_off = w.part_off + align_up(kPartialMax * 4);
+    w.total = w.bad_off + kAlign;
+    return w;
+}
+
+int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 32 : G); }
+
+// Linear workspace: [counters: NCB u32][partials: ksplit * M * Npad floats].
+struct LinWs {
+    int64_t cnt_off, part_off, total;
+};
+LinWs lin_ws(int bits, int64_t M, int64_t K, int64_t N) {
+    const int64_t KT = ceil_div(K, kTileK);
+    const int64_t tn = bits == 8 ? kI8TileN : kI4TileN;
+    const int64_t Npad = round_up(N, tn), NCB = Npad / tn;
+    LinWs w;
+    w.cnt_off = 0;
+    w.part_off = align_up((NCB > 0 ? NCB : 1) * 4);
+    w.total = w.part_off;
+    if (M >= 1 && M <= kGemvMaxM) {
+        const GemvPlan p = gemv_plan(KT, NCB);
+        w.total += align_up((int64_t)p.ksplit * M * Npad * 4);
+    }
+    return w;
+}
+
+bool bad_dims(int64_t a, int64_t b) { return a < 0 || b < 0 || a > kMaxDim || b > kMaxDim || a * b > ((int64_t)1 << 40); }
+
+int check_codes_flag(const int* dflag, hipStream_t s) {
+    int host_flag = 0;
+    SGQ_HIP(hipMemcpyAsync(&host_flag, dflag, sizeof(int), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flag)");
+    SGQ_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (host_flag) return fail(SGQ_ERR_CODES, "qdata holds a value that is not an integer code in range");
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sgq_last_error(void) { return g_err; }
+
+int sgq_abi_version(void) { return SGQ_ABI_VERSION; }
+
+int64_t sgq_int8_packed_bytes(int64_t K, int64_t N) {
+    if (bad_dims(K, N)) return -1;
+    return I8Geom(K, N).bytes();
+}
+
+int sgq_int4_layout(int64_t K, int64_t N, int64_t group_size) {
+    return I4Geom(K, N, group_size).tiled ? SGQ_LAYOUT_INT4_TILED : SGQ_LAYOUT_INT4_FLAT;
+}
+
+int64_t sgq_int4_packed_bytes(int64_t K, int64_t N, int64_t group_size) {
+    if (bad_dims(K, N)) return -1;
+    return I4Geom(K, N, group_size).bytes();
+}
+
+int64_t sgq_int4_devscale_count(int64_t K, int64_t N, int64_t group_size) {
+    if (bad_dims(K, N)) return -1;
+    return I4Geom(K, N, group_size).devscale_count();
+}
+
+int64_t sgq_int8_scale_count(int64_t rows, int64_t cols, int scheme) {
+    if (bad_dims(rows, cols)) return -1;
+    return scheme == SGQ_PER_TENSOR_SYMMETRIC ? 1 : rows;
+}
+
+int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size) {
+    if (bad_dims(rows, cols)) return -1;
+    return int4_groups(rows * cols, group_size);
+}
+
+int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size) {
+    if (bad_dims(rows, cols)) return -1;
+    const int64_t ngroups = bits == 8 ? rows : int4_groups(rows * cols, group_size);
+    return quant_ws(ngroups).total;
+}
+
+int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N) {
+    if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4)) return -1;
+    return lin_ws(bits, M, K, N).total;
+}
+
+int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
+    if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_workspace_init: bad workspace");
+    SGQ_HIP(launch_fill_zero(workspace, workspace_bytes, (hipStream_t)stream), "fill_zero");
+    return ok();
+}
+
+int sgq_quantize_int8(const float* x, int64_t rows, int64_t cols, int scheme, float* qdata_f32, float* scales,
+                      void* packed, void* workspace, int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(rows, cols)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: bad shape");
+    if (scheme != SGQ_PER_TENSOR_SYMMETRIC && scheme != SGQ_PER_CHANNEL_SYMMETRIC)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: scheme must be per-tensor or per-channel");
+    if (scheme == SGQ_PER_CHANNEL_SYMMETRIC && rows == 0)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: per-channel needs rows > 0");
+    const int64_t total = rows * cols;
+    if (!scales || (total > 0 && !x)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: null pointer");
+    const QuantWs w = quant_ws(rows);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(SGQ_ERR_WORKSPACE, "sgq_quantize_int8: workspace needs %lld bytes", (long long)w.total);
+    char* ws = (char*)workspace;
+    float* inv = (float*)(ws + w.inv_off);
+    const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
+    if (per_tensor) {
+        float* part = (float*)(ws + w.part_off);
+        const int64_t nparts = absmax_partial_count(total);
+        SGQ_HIP(launch_absmax_partial(x, total, part, nparts, s), "absmax_partial");
+        SGQ_HIP(launch_group_scales(part, nparts, nparts, 1, 127.0f, scales, inv, s), "group_scales");
+    } else {
+        SGQ_HIP(launch_group_scales(x, total, cols, rows, 127.0f, scales, inv, s), "group_scales");
+    }
+    if ((packed || qdata_f32) && total > 0)
+        SGQ_HIP(launch_pack_i8_tiled(x, false, rows, cols, inv, per_tensor, packed, qdata_f32, nullptr, s),
+                "pack_i8_tiled");
+    return ok();
+}
+
+int sgq_quantize_int4(const float* x, int64_t rows, int64_t cols, int64_t group_size, float* qdata_f32,
+                      float* scales, void* packed, float* devscales, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(rows, cols)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: bad shape");
+    const int64_t total = rows * cols;
+    const I4Geom g(rows, cols, group_size);
+    const int64_t ngroups = int4_groups(total, g.G);
+    if ((ngroups > 0 && !scales) || (total > 0 && !x))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: null pointer");
+    if (packed && g.tiled && !devscales)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: tiled layout needs devscales");
+    const QuantWs w = quant_ws(ngroups);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(SGQ_ERR_WORKSPACE, "sgq_quantize_int4: workspace needs %lld bytes", (long long)w.total);
+    float* inv = (float*)((char*)workspace + w.inv_off);
+    if (ngroups > 0) SGQ_HIP(launch_group_scales(x, total, g.G, ngroups, 7.0f, scales, inv, s), "group_scales");
+    if (total > 0) {
+        if (packed && g.tiled) {
+            SGQ_HIP(launch_pack_i4_tiled(x, false, rows, cols, g.G, inv, packed, qdata_f32, nullptr, s),
+                    "pack_i4_tiled");
+            SGQ_HIP(launch_devscales_i4(scales, g, devscales, s), "devscales_i4");
+        } else if (packed || qdata_f32) {
+            SGQ_HIP(launch_pack_i4_flat(x, false, total, g.G, inv, packed, qdata_f32, nullptr, s), "pack_i4_flat");
+        }
+    } else if (packed && g.tiled && g.devscale_count() > 0) {
+        SGQ_HIP(launch_devscales_i4(scales, g, devscales, s), "devscales_i4");
+    }
+    return ok();
+}
+
+int sgq_pack_int8(const float* qdata_f32, int64_t K, int64_t N, void* packed, void* workspace,
+                  int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int8: bad shape");
+    if (!packed || (K * N > 0 && !qdata_f32)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int8: null pointer");
+    const QuantWs w = quant_ws(K);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(SGQ_ERR_WORKSPACE, "sgq_pack_int8: workspace needs %lld bytes", (long long)w.total);
+    int* flag = (int*)((char*)workspace + w.bad_off);
+    SGQ_HIP(launch_fill_zero(flag, sizeof(int), s), "fill_zero");
+    SGQ_HIP(launch_pack_i8_tiled(qdata_f32, true, K, N, nullptr, false, packed, nullptr, flag, s), "pack_i8_tiled");
+    return check_codes_flag(flag, s);
+}
+
+int sgq_pack_int4(const float* qdata_f32, const float* scales, int64_t K, int64_t N, int64_t group_size,
+                  void* packed, float* devscales, void* workspace, int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int4: bad shape");
+    const I4Geom g(K, N, group_size);
+    if (!packed || (K * N > 0 && (!qdata_f32 || !scales)) || (g.tiled && !devscales))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int4: null pointer");
+    const QuantWs w = quant_ws(int4_groups(K * N, g.G));
+    if (!workspace || workspace_bytes < w.total)
+        return fail(SGQ_ERR_WORKSPACE, "sgq_pack_int4: workspace needs %lld bytes", (long long)w.total);
+    int* flag = (int*)((char*)workspace + w.bad_off);
+    SGQ_HIP(launch_fill_zero(flag, sizeof(int), s), "fill_zero");
+    if (g.tiled) {
+        SGQ_HIP(launch_pack_i4_tiled(qdata_f32, true, K, N, g.G, nullptr, packed, nullptr, flag, s), "pack_i4_tiled");
+        SGQ_HIP(launch_devscales_i4(scales, g, devscales, s), "devscales_i4");
+    } else {
+        SGQ_HIP(launch_pack_i4_flat(qdata_f32, true, K * N, g.G, nullptr, packed, nullptr, flag, s), "pack_i4_flat");
+    }
+    return check_codes_flag(flag, s);
+}
+
+int sgq_unpack_int8(const void* packed, int64_t K, int64_t N, float* qdata_f32, void* stream) {
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int8: bad shape");
+    if (K * N > 0 && (!packed || !qdata_f32)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int8: null pointer");
+    SGQ_HIP(launch_unpack_i8_tiled(packed, K, N, nullptr, false, qdata_f32, (hipStream_t)stream), "unpack_i8");
+    return ok();
+}
+
+int sgq_unpack_int4(const void* packed, int64_t K, int64_t N, int64_t group_size, float* qdata_f32, void* stream) {
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int4: bad shape");
+    if (K * N > 0 && (!packed || !qdata_f32)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int4: null pointer");
+    const I4Geom g(K, N, group_size);
+    hipStream_t s = (hipStream_t)stream;
+    if (g.tiled)
+        SGQ_HIP(launch_unpack_i4_tiled(packed, K, N, g.G, nullptr, qdata_f32, s), "unpack_i4_tiled");
+    else
+        SGQ_HIP(launch_unpack_i4_flat(packed, K * N, g.G, nullptr, qdata_f32, s), "unpack_i4_flat");
+    return ok();
+}
+
+int sgq_dequantize_int8(const void* packed, const float* scales, int scheme, int64_t K, int64_t N, float* out,
+                        void* stream) {
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: bad shape");
+    if (scheme != SGQ_PER_TENSOR_SYMMETRIC && scheme != SGQ_PER_CHANNEL_SYMMETRIC)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: bad scheme");
+    if (K * N > 0 && (!packed || !scales || !out))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: null pointer");
+    SGQ_HIP(launch_unpack_i8_tiled(packed, K, N, scales, scheme == SGQ_PER_TENSOR_SYMMETRIC, out,
+                                   (hipStream_t)stream),
+            "unpack_i8");
+    return ok();
+}
+
+int sgq_dequantize_int4(const void* packed, const float* scales, int64_t K, int64_t N, int64_t group_size,
+                        float* out, void* stream) {
+    if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int4: bad shape");
+    if (K * N > 0 && (!packed || !scales || !out))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int4: null pointer");
+    const I4Geom g(K, N, group_size);
+    hipStream_t s = (hipStream_t)stream;
+    if (g.tiled)
+        SGQ_HIP(launch_unpack_i4_tiled(packed, K, N, g.G, scales, out, s), "unpack_i4_tiled");
+    else
+        SGQ_HIP(launch_unpack_i4_flat(packed, K * N, g.G, scales, out, s), "unpack_i4_flat");
+    return ok();
+}
+
+int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                    int scheme, const float* bias, float* y, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: bad shape");
+    if (scheme != SGQ_PER_TENSOR_SYMMETRIC && scheme != SGQ_PER_CHANNEL_SYMMETRIC)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: bad scheme");
+    if (M == 0 || N == 0) return ok();
+    if (!y) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: null output");
+    if (K == 0) {
+        SGQ_HIP(launch_fill_bias(y, M, N, bias, s), "fill_bias");
+        return ok();
+    }
+    if (!x || !packed || !scales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: null pointer");
+    const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
+    if (M <= kGemvMaxM) {
+        const LinWs w = lin_ws(8, M, K, N);
+        if (!workspace || workspace_bytes < w.total)
+            return fail(SGQ_ERR_WORKSPACE, "sgq_linear_int8: workspace needs %lld bytes", (long long)w.total);
+        char* ws = (char*)workspace;
+        SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, (float*)(ws + w.part_off),
+                               (unsigned*)(ws + w.cnt_off), s),
+                "gemv_i8");
+    } else {
+        SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemm_i8");
+    }
+    return ok();
+}
+
+int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                    const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: bad shape");
+    if (M == 0 || N == 0) return ok();
+    if (!y) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: null output");
+    if (K == 0) {
+        SGQ_HIP(launch_fill_bias(y, M, N, bias, s), "fill_bias");
+        return ok();
+    }
+    const I4Geom g(K, N, group_size);
+    if (!x || !packed) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: null pointer");
+    if (!g.tiled) {
+        if (!scales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: flat layout needs scales");
+        SGQ_HIP(launch_linear_i4_flat(x, M, K, N, packed, scales, g.G, bias, y, s), "linear_i4_flat");
+        return ok();
+    }
+    if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
+    if (M <= kGemvMaxM) {
+        const LinWs w = lin_ws(4, M, K, N);
+        if (!workspace || workspace_bytes < w.total)
+            return fail(SGQ_ERR_WORKSPACE, "sgq_linear_int4: workspace needs %lld bytes", (long long)w.total);
+        char* ws = (char*)workspace;
+        SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, (float*)(ws + w.part_off),
+                               (unsigned*)(ws + w.cnt_off), s),
+                "gemv_i4");
+    } else {
+        SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemm_i4");
+    }
+    return ok();
+}
+
+}  // extern "C"

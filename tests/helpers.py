@@ -1,0 +1,151 @@
+"""Shared test helpers: package loader, golden fixtures, numpy models of the
+device layouts, error metrics."""
+from __future__ import annotations
+
+import importlib.util
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+PKG_DIR = ROOT / "soverign-grad_amd"
+GOLDEN_DIR = Path(__file__).resolve().parent / "golden"
+SGQ_HEADER = ROOT / "include" / "sgq.h"
+
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def load_sgq():
+    """Imports soverign-grad_amd/ as the package `soverign_grad_amd`."""
+    name = "soverign_grad_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, PKG_DIR / "__init__.py",
+                                                  submodule_search_locations=[str(PKG_DIR)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def load_synth():
+    load_sgq()
+    import soverign_grad_amd.synth as synth  # noqa: E402
+
+    return synth
+
+
+def load_golden():
+    meta = json.loads((GOLDEN_DIR / "golden.json").read_text())
+    arrays = np.load(GOLDEN_DIR / "golden.npz", allow_pickle=False)
+    out = []
+    for c in meta["cases"]:
+        out.append({"kind": c["kind"], "params": c["params"], **{k: arrays[v] for k, v in c["arrays"].items()}})
+    return out
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    return a.shape == b.shape and np.array_equal(bits(a), bits(b))
+
+
+def same_value_allow_zero_sign(a: np.ndarray, b: np.ndarray) -> bool:
+    """Bitwise equal except that +0.0 and -0.0 count as equal (NaN == NaN)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    if a.shape != b.shape:
+        return False
+    ba, bb = bits(a).copy(), bits(b).copy()
+    ba[a == 0] = 0
+    bb[b == 0] = 0
+    return np.array_equal(ba, bb)
+
+
+def rel_err(y: np.ndarray, yref: np.ndarray) -> float:
+    """max|y - yref| / max|yref| (the parity metric of the forward)."""
+    y = np.asarray(y, np.float64)
+    yref = np.asarray(yref, np.float64)
+    den = np.max(np.abs(yref)) if yref.size else 0.0
+    num = np.max(np.abs(y - yref)) if y.size else 0.0
+    if den == 0.0:
+        return float(num)
+    return float(num / den)
+
+
+# ---- numpy models of the device layouts (see csrc/sgq_internal.h) ---------
+
+def _ceil(a, b):
+    return (a + b - 1) // b
+
+
+def i8_geom(K, N):
+    Kpad, Npad = _ceil(K, 16) * 16, _ceil(N, 64) * 64
+    return Kpad, Npad, Kpad // 16, Npad // 64
+
+
+def i4_geom(K, N, G):
+    G = G if G > 0 else 32
+    Kpad, Npad = _ceil(K, 16) * 16, _ceil(N, 128) * 128
+    tiled = N % 8 == 0 and G % 8 == 0
+    spc = G // 8 if (tiled and N % G == 0) else 1
+    nsc = _ceil(Npad // 128 * 16, spc) if tiled else 0
+    return dict(G=G, Kpad=Kpad, Npad=Npad, KT=Kpad // 16, NCB=Npad // 128, tiled=tiled, spc=spc, nsc=nsc)
+
+
+def model_pack_i8(codes: np.ndarray) -> np.ndarray:
+    """INT8 tiled: super-tile (cb, kt) of 16 rows x 64 cols at (cb*KT+kt)*1024;
+    chunk c = (band, strip); dword d = column 4*strip+d; byte r = row 4*band+r."""
+    K, N = codes.shape
+    Kpad, Npad, KT, NCB = i8_geom(K, N)
+    full = np.zeros((Kpad, Npad), np.int8)
+    full[:K, :N] = codes.astype(np.int8)
+    # [NCB][KT][band 4][strip 16][col d 4][row r 4]
+    t = full.reshape(KT, 4, 4, NCB, 16, 4)  # kt, band, r, cb, strip, d
+    t = t.transpose(3, 0, 1, 4, 5, 2)  # cb, kt, band, strip, d, r
+    return np.ascontiguousarray(t).view(np.uint8).reshape(-1)
+
+
+def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
+    """INT4 tiled: super-tile of 16 rows x 128 cols; chunk c = (band, strip);
+    dword r = row 4*band+r; nibble e = column 8*strip+e (low nibble first)."""
+    K, N = codes.shape
+    g = i4_geom(K, N, G)
+    full = np.zeros((g["Kpad"], g["Npad"]), np.int64)
+    full[:K, :N] = codes.astype(np.int64)
+    t = full.reshape(g["KT"], 4, 4, g["NCB"], 16, 8)  # kt, band, r, cb, strip, e
+    t = t.transpose(3, 0, 1, 4, 2, 5)  # cb, kt, band, strip, r, e
+    nib = (t & 0xF).astype(np.uint32)
+    shifts = (np.arange(8, dtype=np.uint32) * 4)
+    words = np.bitwise_or.reduce(nib << shifts, axis=-1).astype(np.uint32)
+    return np.ascontiguousarray(words).view(np.uint8).reshape(-1)
+
+
+def model_pack_i4_flat(codes: np.ndarray) -> np.ndarray:
+    flat = codes.reshape(-1).astype(np.int64) & 0xF
+    if flat.size % 2:
+        flat = np.concatenate([flat, [0]])
+    return (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
+
+
+def model_devscales_i4(scales: np.ndarray, K: int, N: int, G: int) -> np.ndarray:
+    g = i4_geom(K, N, G)
+    out = np.zeros((g["nsc"], g["Kpad"]), np.float32)
+    for sc in range(g["nsc"]):
+        n = sc * g["spc"] * 8
+        if n < N:
+            idx = (np.arange(K, dtype=np.int64) * N + n) // g["G"]
+            out[sc, :K] = scales[idx]
+    return out.reshape(-1)
+
+
+def header_symbols() -> list:
+    import re
+
+    text = SGQ_HEADER.read_text()
+    return sorted(set(re.findall(r"\b(sgq_[a-z0-9_]+)\s*\(", text)))

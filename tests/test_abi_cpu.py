@@ -1,0 +1,118 @@
+"""CPU tests of the C ABI: the library loads, exports every declared symbol,
+answers its host-only size queries, and rejects bad arguments before any GPU
+work.  Also checks the numpy models of the device layouts used by the GPU
+tests.  No call here launches a kernel."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import helpers
+
+
+@pytest.fixture(scope="module")
+def lib(sgq):
+    return sgq.load_library()
+
+
+def test_exports_every_declared_symbol(sgq):
+    raw = ctypes.CDLL(str(sgq.LIB_PATH))
+    declared = helpers.header_symbols()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(raw, name), name
+    assert set(declared) == set(sgq.SIGNATURES), "binding and header disagree"
+
+
+def test_abi_version(lib):
+    assert lib.sgq_abi_version() == 1
+    assert lib.sgq_last_error() is not None
+
+
+@pytest.mark.parametrize("K,N", [(1, 1), (16, 64), (17, 65), (1024, 1024), (4096, 11008), (11008, 4096), (3, 0)])
+def test_int8_sizes(lib, K, N):
+    Kpad, Npad, KT, NCB = helpers.i8_geom(K, N)
+    assert lib.sgq_int8_packed_bytes(K, N) == NCB * KT * 1024
+    assert lib.sgq_int8_scale_count(K, N, 0) == 1
+    assert lib.sgq_int8_scale_count(K, N, 1) == K
+
+
+@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (2048, 5632, 128), (16, 32, 32), (32, 16, 16), (5, 13, 7),
+                                   (3, 11, 8), (16, 40, 24), (8, 24, 0), (4, 9, -5), (100, 12, 8)])
+def test_int4_sizes(lib, K, N, G):
+    g = helpers.i4_geom(K, N, G)
+    assert lib.sgq_int4_layout(K, N, G) == (0 if g["tiled"] else 1)
+    exp_bytes = g["NCB"] * g["KT"] * 1024 if g["tiled"] else (K * N + 1) // 2
+    assert lib.sgq_int4_packed_bytes(K, N, G) == exp_bytes
+    assert lib.sgq_int4_devscale_count(K, N, G) == (g["nsc"] * g["Kpad"] if g["tiled"] else 0)
+    assert lib.sgq_int4_scale_count(K, N, G) == (K * N + g["G"] - 1) // g["G"]
+
+
+def test_workspace_sizes(lib):
+    assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) >= 4096 * 4
+    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) > 0
+    assert lib.sgq_linear_workspace_bytes(3, 1, 4, 4) == -1
+    assert lib.sgq_quantize_workspace_bytes(4, 4096, 4096, 128) >= 4096 * 4096 // 128 * 4
+
+
+def test_argument_errors_before_gpu(lib, sgq):
+    # Each of these fails validation on the host; nothing reaches the GPU.
+    assert lib.sgq_quantize_int8(None, -1, 4, 0, None, None, None, None, 0, None) == 1
+    assert lib.sgq_quantize_int8(None, 4, 4, 7, None, None, None, None, 0, None) == 1
+    assert lib.sgq_quantize_int8(None, 0, 4, 1, None, None, None, None, 0, None) == 1
+    assert b"per-channel" in lib.sgq_last_error()
+    assert lib.sgq_quantize_int8(1, 4, 4, 0, None, None, None, None, 0, None) == 1
+    assert lib.sgq_linear_int8(None, 1, 4, 4, None, None, 9, None, None, None, 0, None) == 1
+    assert lib.sgq_linear_int4(None, -2, 4, 4, None, None, None, 32, None, None, None, 0, None) == 1
+    assert lib.sgq_linear_int4(16, 1, 64, 64, 16, 16, None, 32, None, 16, None, 0, None) == 1  # no devscales
+    assert lib.sgq_linear_int4(16, 1, 64, 64, 16, 16, 16, 32, None, 16, None, 0, None) == 3  # no workspace
+    assert b"workspace" in lib.sgq_last_error()
+    # empty outputs are a no-op success
+    assert lib.sgq_linear_int8(None, 0, 4, 4, None, None, 0, None, None, None, 0, None) == 0
+
+
+# ---- numpy layout models -------------------------------------------------
+
+def _unpack_model_i8(buf, K, N):
+    Kpad, Npad, KT, NCB = helpers.i8_geom(K, N)
+    t = buf.view(np.int8).reshape(NCB, KT, 4, 16, 4, 4)  # cb, kt, band, strip, d, r
+    full = t.transpose(1, 2, 5, 0, 3, 4).reshape(Kpad, Npad)
+    return full[:K, :N]
+
+
+def test_model_pack_i8_roundtrip():
+    rng = np.random.default_rng(0)
+    for K, N in [(16, 64), (17, 70), (33, 130)]:
+        q = rng.integers(-127, 128, size=(K, N))
+        buf = helpers.model_pack_i8(q)
+        assert buf.size == helpers.i8_geom(K, N)[2] * helpers.i8_geom(K, N)[3] * 1024
+        assert np.array_equal(_unpack_model_i8(buf, K, N), q)
+        # element (k, n) sits at the documented byte
+        k, n = K - 1, N - 1
+        cb, kt, band, strip, d, r = n // 64, k // 16, (k % 16) // 4, (n % 64) // 4, n % 4, k % 4
+        KT = helpers.i8_geom(K, N)[2]
+        off = (cb * KT + kt) * 1024 + (band * 16 + strip) * 16 + d * 4 + r
+        assert buf.view(np.int8)[off] == q[k, n]
+
+
+def test_model_pack_i4_positions():
+    rng = np.random.default_rng(1)
+    K, N = 20, 136
+    q = rng.integers(-7, 8, size=(K, N))
+    buf = helpers.model_pack_i4_tiled(q, 8)
+    g = helpers.i4_geom(K, N, 8)
+    for (k, n) in [(0, 0), (19, 135), (5, 77), (16, 128)]:
+        cb, kt, band, strip, r, e = n // 128, k // 16, (k % 16) // 4, (n % 128) // 8, k % 4, n % 8
+        off = (cb * g["KT"] + kt) * 1024 + (band * 16 + strip) * 16 + r * 4 + e // 2
+        nib = (int(buf[off]) >> (4 * (e % 2))) & 0xF
+        assert ((nib ^ 8) - 8) == q[k, n]
+
+
+def test_model_devscales():
+    K, N, G = 5, 24, 8
+    s = np.arange(1, (K * N) // G + 1, dtype=np.float32)
+    ds = helpers.model_devscales_i4(s, K, N, G).reshape(-1, 16)
+    g = helpers.i4_geom(K, N, G)
+    assert g["spc"] == 1
+    # strip 1 of row 2 covers elements 2*24+8 .. +7 -> group (56)//8 = 7
+    assert ds[1, 2] == s[7]

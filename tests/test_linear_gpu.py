@@ -1,0 +1,194 @@
+"""GPU parity of the fused dequantize + matmul forward.
+
+Outputs must be within max|y - y_ref| / max|y_ref| <= 1e-5 of the CPU
+dequantize-then-matmul (fp32 accumulate; the kernels accumulate in a different
+order, so bits are not expected to match).  y_ref comes from the golden
+fixtures (compiled reference) or the oracle on the same quantized weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+import helpers
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # max relative error of the forward against the CPU reference
+
+
+def _to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+
+
+def _np(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def test_golden_linear(sgq, dev, golden):
+    n = 0
+    for c in golden:
+        if c["kind"] not in ("linear_int8", "linear_int4"):
+            continue
+        p = c["params"]
+        print(f"  case {c['kind']} {p}", flush=True)
+        x = _to_dev(c["x"], dev)
+        b = _to_dev(c["bias"], dev) if "bias" in c else None
+        if c["kind"] == "linear_int8":
+            qw = sgq.pack_int8(_to_dev(c["q"], dev), _to_dev(c["s"], dev), p["scheme"])
+            y = sgq.quantized_matmul_int8(x, qw, b)
+        else:
+            qw = sgq.pack_int4(_to_dev(c["q"], dev), _to_dev(c["s"], dev), p["group_size"])
+            y = sgq.quantized_matmul_int4(x, qw, b)
+        e = rel_err(_np(y), c["y"])
+        assert e <= TOL, (p, e)
+        n += 1
+    assert n >= 16
+
+
+def _case(sgq, dev, oracle, synth, bits_, M, K, N, G=128, scheme=0, bias=False, seed=1, rows=None):
+    W = synth.normal((K, N), synth.config_seed(seed), synth.STREAM_W, 0.0, 0.02)
+    x = synth.normal((M, K), synth.config_seed(seed), synth.STREAM_X, 0.0, 1.0)
+    b = synth.normal((1, N), synth.config_seed(seed), synth.STREAM_BIAS, 0.0, 0.02) if bias else None
+    xd = _to_dev(x, dev)
+    bd = _to_dev(b, dev) if bias else None
+    if bits_ == 8:
+        qw = sgq.quantize_int8(_to_dev(W, dev), scheme)
+        y = sgq.quantized_matmul_int8(xd, qw, bd)
+        q, s = oracle.quantize_int8(W, scheme)
+        sub = x if rows is None else x[rows]
+        yref = oracle.quantized_matmul_int8(sub, q, s, scheme, b)
+    else:
+        qw = sgq.quantize_int4(_to_dev(W, dev), G)
+        y = sgq.quantized_matmul_int4(xd, qw, bd)
+        q, s = oracle.quantize_int4(W, G)
+        sub = x if rows is None else x[rows]
+        yref = oracle.quantized_matmul_int4(sub, q, s, G, b)
+    yg = _np(y)
+    if rows is not None:
+        yg = yg[rows]
+    return yg, yref
+
+
+# BASELINE configs 1-5 (config 4 checked on a row subset: rows of the GEMM are independent)
+@pytest.mark.parametrize(
+    "name,bits_,M,K,N,G,scheme,bias,seed",
+    [
+        ("C1_int8_pt_bias_M128", 8, 128, 1024, 1024, 0, 0, True, 0),
+        ("C2_int4_g128_M1", 4, 1, 4096, 4096, 128, 0, False, 1),
+        ("C3_gate_M1", 4, 1, 4096, 11008, 128, 0, False, 2),
+        ("C3_gate_M4", 4, 4, 4096, 11008, 128, 0, False, 2),
+        ("C3_gate_M8", 4, 8, 4096, 11008, 128, 0, False, 2),
+        ("C3_gate_M16", 4, 16, 4096, 11008, 128, 0, False, 2),
+        ("C3_down_M1", 4, 1, 11008, 4096, 128, 0, False, 2),
+        ("C3_down_M16", 4, 16, 11008, 4096, 128, 0, False, 2),
+        ("C5_qkv_M8", 4, 8, 2048, 6144, 128, 0, False, 4),
+        ("C5_o_M8", 4, 8, 2048, 2048, 128, 0, False, 4),
+        ("C5_up_M8", 4, 8, 2048, 5632, 128, 0, False, 4),
+        ("C5_down_M8", 4, 8, 5632, 2048, 128, 0, False, 4),
+    ],
+)
+def test_configs(sgq, dev, oracle, synth, name, bits_, M, K, N, G, scheme, bias, seed):
+    print(f"  case {name}", flush=True)
+    y, yref = _case(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme, bias, seed)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
+def test_config4_gemm_rows(sgq, dev, oracle, synth):
+    M = 2048
+    rows = np.r_[0:16, 1000:1016, 2032:2048]
+    print("  case C4_int8_pt_M2048 (48 rows vs oracle)", flush=True)
+    y, yref = _case(sgq, dev, oracle, synth, 8, M, 4096, 4096, 0, 0, False, 3, rows=rows)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 15, 16, 17, 31, 33, 64, 129])
+@pytest.mark.parametrize("bits_", [8, 4])
+def test_batch_sizes(sgq, dev, oracle, synth, M, bits_):
+    y, yref = _case(sgq, dev, oracle, synth, bits_, M, 320, 192, 32, 1, True, 7)
+    assert rel_err(y, yref) <= TOL
+
+
+@pytest.mark.parametrize(
+    "M,K,N,G",
+    [(1, 1, 8, 8), (3, 17, 24, 8), (5, 130, 77, 7), (2, 33, 40, 24), (19, 18, 200, 40), (7, 100, 12, 8),
+     (40, 61, 136, 8), (1, 4099, 24, 8), (20, 45, 13, 5)],
+)
+def test_ragged_int4(sgq, dev, oracle, synth, M, K, N, G):
+    y, yref = _case(sgq, dev, oracle, synth, 4, M, K, N, G, 0, True, 8)
+    assert rel_err(y, yref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,scheme", [(1, 1, 1, 0), (3, 17, 70, 1), (18, 130, 65, 0), (33, 7, 129, 1),
+                                          (2, 4099, 3, 0), (200, 45, 300, 1)])
+def test_ragged_int8(sgq, dev, oracle, synth, M, K, N, scheme):
+    y, yref = _case(sgq, dev, oracle, synth, 8, M, K, N, 0, scheme, True, 9)
+    assert rel_err(y, yref) <= TOL
+
+
+def test_unaligned_x_pointer(sgq, dev, oracle, synth):
+    # x offset by one float: the kernels must not assume 16-byte alignment.
+    W = synth.normal((64, 128), 31, 0, 0.0, 0.02)
+    xs = synth.normal((4 * 64 + 1,), 31, 1)
+    x = _to_dev(xs, dev)[1:].view(4, 64)
+    for bits_ in (8, 4):
+        qw = sgq.quantize_int8(_to_dev(W, dev), 0) if bits_ == 8 else sgq.quantize_int4(_to_dev(W, dev), 32)
+        y = sgq.quantized_matmul(x, qw)
+        if bits_ == 8:
+            q, s = oracle.quantize_int8(W, 0)
+            yref = oracle.quantized_matmul_int8(xs[1:].reshape(4, 64), q, s, 0)
+        else:
+            q, s = oracle.quantize_int4(W, 32)
+            yref = oracle.quantized_matmul_int4(xs[1:].reshape(4, 64), q, s, 32)
+        assert rel_err(_np(y), yref) <= TOL
+
+
+def test_empty_shapes(sgq, dev):
+    qw = sgq.quantize_int4(torch.zeros((0, 16), device=dev), 8)
+    b = torch.arange(16, dtype=torch.float32, device=dev)
+    y = sgq.quantized_matmul_int4(torch.zeros((3, 0), device=dev), qw, b)
+    assert torch.equal(y, b.expand(3, 16))  # K == 0: y = bias (matmul of zeros, then bias)
+    qw8 = sgq.quantize_int8(torch.ones((8, 4), device=dev), 1)
+    y0 = sgq.quantized_matmul_int8(torch.zeros((0, 8), device=dev), qw8)
+    assert y0.shape == (0, 4)
+
+
+def test_deterministic_and_workspace_reuse(sgq, dev, synth):
+    # The split-K reduction sums partials in a fixed order: repeated calls give
+    # identical bits, also after the workspace served other shapes.
+    W = _to_dev(synth.normal((4096, 4096), 41, 0, 0.0, 0.02), dev)
+    x = _to_dev(synth.normal((1, 4096), 41, 1), dev)
+    qw = sgq.quantize_int4(W, 128)
+    y1 = sgq.quantized_matmul_int4(x, qw).clone()
+    W2 = _to_dev(synth.normal((512, 640), 42, 0, 0.0, 0.02), dev)
+    qw2 = sgq.quantize_int8(W2, 1)
+    for m in (1, 7, 16):
+        sgq.quantized_matmul_int8(_to_dev(synth.normal((m, 512), 43, 1), dev), qw2)
+    for _ in range(3):
+        y2 = sgq.quantized_matmul_int4(x, qw)
+        assert torch.equal(y1, y2)
+
+
+def test_nonfinite_propagates(sgq, dev):
+    # A NaN activation poisons the outputs it touches, as in the reference.
+    W = torch.full((32, 64), 0.01, device=dev)
+    x = torch.ones((1, 32), device=dev)
+    x[0, 5] = float("nan")
+    for qw in (sgq.quantize_int8(W, 0), sgq.quantize_int4(W, 32)):
+        y = sgq.quantized_matmul(x, qw)
+        assert torch.isnan(y).all()
+
+
+def test_dequantize_matches_reference_product(sgq, dev, oracle, synth):
+    W = synth.normal((130, 72), 51, 0, 0.0, 0.02)
+    qx = sgq.quantize_int8(_to_dev(W, dev), 1)
+    q, s = oracle.quantize_int8(W, 1)
+    assert helpers.same_value_allow_zero_sign(_np(sgq.dequantize_int8(qx)), oracle.dequantize_int8(q, s, 1))
+    qx4 = sgq.quantize_int4(_to_dev(W, dev), 24)
+    q4, s4 = oracle.quantize_int4(W, 24)
+    assert helpers.same_value_allow_zero_sign(_np(sgq.dequantize_int4(qx4)), oracle.dequantize_int4(q4, s4, 24))

@@ -1,0 +1,200 @@
+"""CPU tests of the oracle (the checker every GPU parity test relies on).
+
+The oracle (oracle/sgq_oracle.c) is pinned by:
+  * the golden fixtures, written by the compiled reference (bit-exact);
+  * a live comparison with the compiled reference on fresh shapes, when
+    oracle/_ref is built (dev container);
+  * closed forms and invariants that do not restate the oracle's formulas:
+    round-trip error bounds, the fp64 error bound of the dot products,
+    identity weights, linearity, special values.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import bits, same_bits
+
+pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
+
+
+# ---- golden fixtures (reference outputs) ---------------------------------
+
+def test_golden_quantize_int8(oracle, golden):
+    n = 0
+    for c in golden:
+        if c["kind"] != "quantize_int8":
+            continue
+        q, s = oracle.quantize_int8(c["x"], c["params"]["scheme"])
+        assert same_bits(q, c["q"]), c["params"]
+        assert same_bits(s, c["s"]), c["params"]
+        if "deq" in c and c["x"].size:
+            d = oracle.dequantize_int8(q, s, c["params"]["scheme"])
+            assert same_bits(d, c["deq"]), c["params"]
+        n += 1
+    assert n >= 20
+
+
+def test_golden_quantize_int4(oracle, golden):
+    n = 0
+    for c in golden:
+        if c["kind"] != "quantize_int4":
+            continue
+        g = c["params"]["group_size"]
+        q, s = oracle.quantize_int4(c["x"], g)
+        assert same_bits(q, c["q"]), c["params"]
+        assert same_bits(s, c["s"]), c["params"]
+        if "deq" in c:
+            d = oracle.dequantize_int4(q, s, g)
+            assert same_bits(d, c["deq"]), c["params"]
+        n += 1
+    assert n >= 10
+
+
+def test_golden_linear(oracle, golden):
+    n = 0
+    for c in golden:
+        if c["kind"] == "linear_int8":
+            y = oracle.quantized_matmul_int8(c["x"], c["q"], c["s"], c["params"]["scheme"], c.get("bias"))
+        elif c["kind"] == "linear_int4":
+            y = oracle.quantized_matmul_int4(c["x"], c["q"], c["s"], c["params"]["group_size"], c.get("bias"))
+        else:
+            continue
+        # The oracle restates the reference's loop order and FMA contraction,
+        # so the outputs agree to the bit.
+        assert same_bits(y, c["y"]), c["params"]
+        n += 1
+    assert n >= 16
+
+
+# ---- live comparison with the compiled reference -------------------------
+
+@pytest.mark.parametrize("shape", [(1, 1), (9, 17), (64, 100), (257, 31), (128, 1024)])
+def test_reference_live_quantize(oracle, ref, synth, shape):
+    x = synth.normal(shape, 77, 0, 0.0, 0.02)
+    for scheme in (0, 1):
+        assert same_bits(oracle.quantize_int8(x, scheme)[0], ref.quantize_int8(x, scheme)[0])
+        assert same_bits(oracle.quantize_int8(x, scheme)[1], ref.quantize_int8(x, scheme)[1])
+    for g in (0, 8, 32, 128, 7, 1000):
+        qo, so = oracle.quantize_int4(x, g)
+        qr, sr = ref.quantize_int4(x, g)
+        assert same_bits(qo, qr) and same_bits(so, sr), g
+
+
+@pytest.mark.parametrize("mkn", [(1, 300, 70), (7, 129, 33), (9, 257, 131), (37, 130, 77), (8, 2048, 512)])
+def test_reference_live_matmul(oracle, ref, synth, mkn):
+    M, K, N = mkn
+    a = synth.normal((M, K), 5, 1)
+    b = synth.normal((K, N), 5, 0, 0.0, 0.02)
+    assert same_bits(oracle.matmul(a, b), ref.matmul(a, b))
+
+
+# ---- closed forms and special cases --------------------------------------
+
+def test_zero_tensor_uses_floor(oracle):
+    x = np.zeros((3, 4), np.float32)
+    q, s = oracle.quantize_int8(x, 0)
+    assert s[0] == np.float32(np.float32(1e-8) / np.float32(127.0))
+    assert np.all(q == 0)
+    q4, s4 = oracle.quantize_int4(x, 4)
+    assert np.all(s4 == np.float32(np.float32(1e-8) / np.float32(7.0)))
+
+
+def test_ties_round_away_and_negative_zero(oracle):
+    # max |x| = 127 -> inv_scale = 1, so codes are round-half-away of x itself.
+    x = np.array([127, 2.5, -2.5, 0.5, -0.5, -0.3, 126.5, -126.5], np.float32).reshape(2, 4)
+    q, s = oracle.quantize_int8(x, 0)
+    assert s[0] == 1.0
+    assert q.reshape(-1).tolist() == [127, 3, -3, 1, -1, -0.0, 127, -127]
+    assert bits(q.reshape(-1)[5:6])[0] == 0x80000000  # -0.0 is kept in qdata
+
+
+def test_nan_and_inf(oracle):
+    x = np.array([np.nan, 1.0, -2.0, 0.25], np.float32).reshape(2, 2)
+    q, s = oracle.quantize_int8(x, 0)
+    assert q.reshape(-1)[0] == 127  # NaN never sets max_abs and clamps to +hi
+    assert s[0] == np.float32(2.0) / np.float32(127.0)
+    x = np.array([np.inf, 1.0, -2.0, -0.25], np.float32).reshape(2, 2)
+    q, s = oracle.quantize_int8(x, 0)
+    assert math.isinf(s[0]) and q.reshape(-1)[0] == 127
+    assert np.all(q.reshape(-1)[1:] == 0) and bits(q.reshape(-1)[2:3])[0] == 0x80000000
+    q4, s4 = oracle.quantize_int4(np.array([np.nan, 3.0], np.float32), 2)
+    assert q4.tolist() == [7.0, 7.0]
+
+
+def test_group_defaults_and_partial(oracle):
+    x = np.arange(1, 71, dtype=np.float32).reshape(7, 10)
+    q0, s0 = oracle.quantize_int4(x, 0)
+    q32, s32 = oracle.quantize_int4(x, 32)
+    assert same_bits(q0, q32) and same_bits(s0, s32)
+    qn, sn = oracle.quantize_int4(x, -3)
+    assert same_bits(qn, q32)
+    assert s32.size == 3  # ceil(70/32); the last group has 6 elements
+    assert s32[2] == np.float32(70.0) / np.float32(7.0)
+
+
+def test_rank1_is_per_tensor(oracle):
+    x = np.linspace(-3, 5, 17, dtype=np.float32)
+    q_pc, s_pc = oracle.quantize_int8(x, 1)
+    q_pt, s_pt = oracle.quantize_int8(x, 0)
+    assert s_pc.size == 1 and same_bits(q_pc, q_pt) and same_bits(s_pc, s_pt)
+
+
+@pytest.mark.parametrize("bits_", [8, 4])
+def test_roundtrip_error_bound(oracle, synth, bits_):
+    # |x - q*s| <= s/2 (+ rounding of the products) for every element that is
+    # not clamped; codes stay in [-hi, hi] and hit +-hi at the group maximum.
+    x = synth.normal((64, 96), 9, 0)
+    if bits_ == 8:
+        q, s = oracle.quantize_int8(x, 1)
+        sc = np.repeat(s, 96).reshape(64, 96)
+        hi = 127
+    else:
+        q, s = oracle.quantize_int4(x, 32)
+        sc = np.repeat(s, 32).reshape(64, 96)
+        hi = 7
+    d = q.astype(np.float64) * sc
+    assert np.all(np.abs(q) <= hi) and np.all(q == np.round(q))
+    err = np.abs(x.astype(np.float64) - d)
+    assert np.all(err <= sc * 0.5 * (1 + 1e-5) + 1e-30)
+    amax = np.abs(x.reshape(-1, 96 if bits_ == 8 else 32)).argmax(axis=1)
+    qq = np.abs(q.reshape(-1, 96 if bits_ == 8 else 32))
+    assert np.all(qq[np.arange(qq.shape[0]), amax] == hi)
+
+
+def test_matmul_fp64_bound_identity_linearity(oracle, synth):
+    K, N, M = 257, 65, 11
+    a = synth.normal((M, K), 3, 1)
+    b = synth.normal((K, N), 3, 0, 0.0, 0.02)
+    y = oracle.matmul(a, b)
+    y64, yabs = oracle.matmul_f64(a, b)
+    gamma = K * 2.0 ** -24 / (1 - K * 2.0 ** -24)
+    assert np.all(np.abs(y - y64) <= gamma * yabs + 1e-30)
+    # identity weight returns x exactly
+    eye = np.eye(K, dtype=np.float32)
+    assert same_bits(oracle.matmul(a, eye), a)
+    # linearity within rounding
+    a2 = synth.normal((M, K), 4, 1)
+    lhs = oracle.matmul(a + a2, b).astype(np.float64)
+    rhs = oracle.matmul(a, b).astype(np.float64) + oracle.matmul(a2, b)
+    assert np.max(np.abs(lhs - rhs)) <= 4 * gamma * (np.abs(a) + np.abs(a2)).sum(axis=1).max() * np.abs(b).max()
+
+
+def test_per_tensor_factorisation(oracle, synth):
+    # For per-tensor scales y = s * (x . q) up to rounding.
+    W = synth.normal((128, 48), 11, 0, 0.0, 0.02)
+    x = synth.normal((5, 128), 11, 1)
+    q, s = oracle.quantize_int8(W, 0)
+    y = oracle.quantized_matmul_int8(x, q, s, 0)
+    yq = (x.astype(np.float64) @ q.astype(np.float64)) * float(s[0])
+    assert np.max(np.abs(y - yq)) <= 1e-5 * np.max(np.abs(yq))
+
+
+def test_bias_broadcast(oracle, synth):
+    W = synth.normal((32, 16), 12, 0, 0.0, 0.02)
+    x = synth.normal((6, 32), 12, 1)
+    b = synth.normal((1, 16), 12, 2)
+    q, s = oracle.quantize_int8(W, 1)
+    y0 = oracle.quantized_matmul_int8(x, q, s, 1)
+    y1 = oracle.quantized_matmul_int8(x, q, s, 1, b)
+    assert same_bits(y1, (y0 + b).astype(np.float32))
