@@ -18,6 +18,8 @@
  *   - Reentrant: no mutable global state; safe to call concurrently from
  *     several host threads as long as each concurrent call has its own
  *     workspace.
+ *   - Alignment: packed buffers, devscales and per-channel INT8 scales must be
+ *     16-byte aligned (hipMalloc gives 256); x may have any 4-byte alignment.
  *
  * Weight shape convention: W is [K, N] row-major ([in_features,
  * out_features], include/sovereigngrad/nn.hpp:938) and the forward is
@@ -85,8 +87,10 @@ int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size);
 int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size);
 
 /* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
- * The workspace must be zero-filled once before its first use (for example
- * with sgq_workspace_init); every call leaves it ready for the next one. */
+ * Currently 0 for every shape: each workgroup of the forward kernels owns
+ * whole output columns, so no scratch memory is used; the workspace
+ * arguments are reserved and may be NULL/0.  A caller that does allocate one
+ * zero-fills it once (sgq_workspace_init). */
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
 
 /* Zero-fills a workspace with a kernel (no hipMemset), on `stream`. */
@@ -125,7 +129,7 @@ int sgq_quantize_int4(const float* x, int64_t rows, int64_t cols, int64_t group_
 /* Packs reference-layout fp32 codes (as stored in a QuantizedTensor's qdata,
  * or loaded by load_state_dict, src/module.cpp:114-134) into the device layout.
  * Returns SGQ_ERR_CODES (after synchronising `stream`) when a code is not an
- * integer in [-127,127] (INT8) or [-8,7] (INT4). */
+ * integer in [-128,127] (INT8) or [-8,7] (INT4). */
 int sgq_pack_int8(const float* qdata_f32, int64_t K, int64_t N, void* packed, void* workspace,
                   int64_t workspace_bytes, void* stream);
 int sgq_pack_int4(const float* qdata_f32, const float* scales, int64_t K, int64_t N, int64_t group_size,

@@ -120,22 +120,27 @@ def _dev_f32(t: torch.Tensor) -> torch.Tensor:
 
 
 class _Workspaces:
-    """One zero-initialised linear workspace per (device, stream, thread)."""
+    """One zero-initialised linear workspace per (device, stream, thread), for
+    the sizes sgq_linear_workspace_bytes asks for (currently none)."""
 
     def __init__(self):
         self._local = threading.local()
 
-    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+    def get(self, nbytes: int, device: torch.device):
+        if nbytes < 0:
+            raise SGQError(1, "bad shape for the workspace query")
+        if nbytes == 0:
+            return None, 0
         cache = getattr(self._local, "cache", None)
         if cache is None:
             cache = self._local.cache = {}
         key = (device.index, _stream(device))
         ws = cache.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _check(load_library().sgq_workspace_init(ws.data_ptr(), ws.numel(), _stream(device)))
             cache[key] = ws
-        return ws
+        return ws.data_ptr(), ws.numel()
 
 
 _linear_ws = _Workspaces()
@@ -159,24 +164,22 @@ class QuantizedTensor:
 
     @property
     def rows(self) -> int:
-        return int(self.original_shape[0]) if len(self.original_shape) >= 2 else 1
+        return _view2d(self.original_shape)[0]
 
     @property
     def cols(self) -> int:
-        n = 1
-        for d in self.original_shape:
-            n *= int(d)
-        return n // self.rows if self.rows else 0
+        return _view2d(self.original_shape)[1]
 
 
 def _view2d(shape) -> tuple:
-    numel = 1
-    for d in shape:
-        numel *= int(d)
+    """[rows, cols] view of a weight: rows = shape[0] (src/quantization.cpp:44-45),
+    rank-1 tensors are one row."""
     if len(shape) >= 2:
-        rows = int(shape[0])
-        return rows, (numel // rows if rows else 0)
-    return 1, numel
+        cols = 1
+        for d in shape[1:]:
+            cols *= int(d)
+        return int(shape[0]), cols
+    return 1, (int(shape[0]) if len(shape) == 1 else 1)
 
 
 def quantize_int8(x: torch.Tensor, scheme: int = PER_CHANNEL, keep_qdata: bool = True) -> QuantizedTensor:
@@ -312,10 +315,9 @@ def quantized_matmul_int8(x: torch.Tensor, qw: QuantizedTensor, bias: Optional[t
     M = x.shape[0]
     dev = x.device
     y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
-    nbytes = lib.sgq_linear_workspace_bytes(8, M, K, N)
-    ws = _linear_ws.get(nbytes, dev)
+    ws, nws = _linear_ws.get(lib.sgq_linear_workspace_bytes(8, M, K, N), dev)
     _check(lib.sgq_linear_int8(_ptr(x), M, K, N, _ptr(qw.packed), _ptr(qw.scales), _int8_branch(qw), _ptr(b),
-                               _ptr(y), _ptr(ws), ws.numel(), _stream(dev)))
+                               _ptr(y), ws, nws, _stream(dev)))
     return y
 
 
@@ -326,10 +328,9 @@ def quantized_matmul_int4(x: torch.Tensor, qw: QuantizedTensor, bias: Optional[t
     M = x.shape[0]
     dev = x.device
     y = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
-    nbytes = lib.sgq_linear_workspace_bytes(4, M, K, N)
-    ws = _linear_ws.get(nbytes, dev)
+    ws, nws = _linear_ws.get(lib.sgq_linear_workspace_bytes(4, M, K, N), dev)
     _check(lib.sgq_linear_int4(_ptr(x), M, K, N, _ptr(qw.packed), _ptr(qw.scales), _ptr(qw.devscales),
-                               qw.group_size, _ptr(b), _ptr(y), _ptr(ws), ws.numel(), _stream(dev)))
+                               qw.group_size, _ptr(b), _ptr(y), ws, nws, _stream(dev)))
     return y
 
 

@@ -58,24 +58,11 @@ QuantWs quant_ws(int64_t ngroups) {
 
 int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 32 : G); }
 
-// Linear workspace: [counters: NCB u32][partials: ksplit * M * Npad floats].
-struct LinWs {
-    int64_t cnt_off, part_off, total;
-};
-LinWs lin_ws(int bits, int64_t M, int64_t K, int64_t N) {
-    const int64_t KT = ceil_div(K, kTileK);
-    const int64_t tn = bits == 8 ? kI8TileN : kI4TileN;
-    const int64_t Npad = round_up(N, tn), NCB = Npad / tn;
-    LinWs w;
-    w.cnt_off = 0;
-    w.part_off = align_up((NCB > 0 ? NCB : 1) * 4);
-    w.total = w.part_off;
-    if (M >= 1 && M <= kGemvMaxM) {
-        const GemvPlan p = gemv_plan(KT, NCB);
-        w.total += align_up((int64_t)p.ksplit * M * Npad * 4);
-    }
-    return w;
-}
+// The forward kernels need no workspace: every workgroup owns whole output
+// columns.  The workspace arguments of sgq_linear_* are reserved.
+int64_t linear_ws_bytes(int, int64_t, int64_t, int64_t) { return 0; }
+
+bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 bool bad_dims(int64_t a, int64_t b) { return a < 0 || b < 0 || a > kMaxDim || b > kMaxDim || a * b > ((int64_t)1 << 40); }
 
@@ -132,7 +119,7 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
 
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N) {
     if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4)) return -1;
-    return lin_ws(bits, M, K, N).total;
+    return linear_ws_bytes(bits, M, K, N);
 }
 
 int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
@@ -152,6 +139,8 @@ int sgq_quantize_int8(const float* x, int64_t rows, int64_t cols, int scheme, fl
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: per-channel needs rows > 0");
     const int64_t total = rows * cols;
     if (!scales || (total > 0 && !x)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: null pointer");
+    if (packed && !aligned16(packed))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int8: packed must be 16-byte aligned");
     const QuantWs w = quant_ws(rows);
     if (!workspace || workspace_bytes < w.total)
         return fail(SGQ_ERR_WORKSPACE, "sgq_quantize_int8: workspace needs %lld bytes", (long long)w.total);
@@ -184,6 +173,8 @@ int sgq_quantize_int4(const float* x, int64_t rows, int64_t cols, int64_t group_
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: null pointer");
     if (packed && g.tiled && !devscales)
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: tiled layout needs devscales");
+    if (packed && g.tiled && !aligned16(packed))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_quantize_int4: packed must be 16-byte aligned");
     const QuantWs w = quant_ws(ngroups);
     if (!workspace || workspace_bytes < w.total)
         return fail(SGQ_ERR_WORKSPACE, "sgq_quantize_int4: workspace needs %lld bytes", (long long)w.total);
@@ -208,6 +199,7 @@ int sgq_pack_int8(const float* qdata_f32, int64_t K, int64_t N, void* packed, vo
     hipStream_t s = (hipStream_t)stream;
     if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int8: bad shape");
     if (!packed || (K * N > 0 && !qdata_f32)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int8: null pointer");
+    if (!aligned16(packed)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int8: packed must be 16-byte aligned");
     const QuantWs w = quant_ws(K);
     if (!workspace || workspace_bytes < w.total)
         return fail(SGQ_ERR_WORKSPACE, "sgq_pack_int8: workspace needs %lld bytes", (long long)w.total);
@@ -224,6 +216,8 @@ int sgq_pack_int4(const float* qdata_f32, const float* scales, int64_t K, int64_
     const I4Geom g(K, N, group_size);
     if (!packed || (K * N > 0 && (!qdata_f32 || !scales)) || (g.tiled && !devscales))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int4: null pointer");
+    if (g.tiled && !aligned16(packed))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_pack_int4: packed must be 16-byte aligned");
     const QuantWs w = quant_ws(int4_groups(K * N, g.G));
     if (!workspace || workspace_bytes < w.total)
         return fail(SGQ_ERR_WORKSPACE, "sgq_pack_int4: workspace needs %lld bytes", (long long)w.total);
@@ -241,6 +235,7 @@ int sgq_pack_int4(const float* qdata_f32, const float* scales, int64_t K, int64_
 int sgq_unpack_int8(const void* packed, int64_t K, int64_t N, float* qdata_f32, void* stream) {
     if (bad_dims(K, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int8: bad shape");
     if (K * N > 0 && (!packed || !qdata_f32)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int8: null pointer");
+    if (!aligned16(packed)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_unpack_int8: packed must be 16-byte aligned");
     SGQ_HIP(launch_unpack_i8_tiled(packed, K, N, nullptr, false, qdata_f32, (hipStream_t)stream), "unpack_i8");
     return ok();
 }
@@ -300,14 +295,12 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     }
     if (!x || !packed || !scales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: null pointer");
     const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
+    if (!aligned16(packed) || (!per_tensor && !aligned16(scales)))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: packed and per-channel scales must be 16-byte aligned");
+    (void)workspace;
+    (void)workspace_bytes;
     if (M <= kGemvMaxM) {
-        const LinWs w = lin_ws(8, M, K, N);
-        if (!workspace || workspace_bytes < w.total)
-            return fail(SGQ_ERR_WORKSPACE, "sgq_linear_int8: workspace needs %lld bytes", (long long)w.total);
-        char* ws = (char*)workspace;
-        SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, (float*)(ws + w.part_off),
-                               (unsigned*)(ws + w.cnt_off), s),
-                "gemv_i8");
+        SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
         SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemm_i8");
     }
@@ -334,14 +327,12 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return ok();
     }
     if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
+    if (!aligned16(packed) || !aligned16(devscales))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: packed and devscales must be 16-byte aligned");
+    (void)workspace;
+    (void)workspace_bytes;
     if (M <= kGemvMaxM) {
-        const LinWs w = lin_ws(4, M, K, N);
-        if (!workspace || workspace_bytes < w.total)
-            return fail(SGQ_ERR_WORKSPACE, "sgq_linear_int4: workspace needs %lld bytes", (long long)w.total);
-        char* ws = (char*)workspace;
-        SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, (float*)(ws + w.part_off),
-                               (unsigned*)(ws + w.cnt_off), s),
-                "gemv_i4");
+        SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
         SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemm_i4");
     }

@@ -4,13 +4,15 @@
 // matmul, then a bias add (src/quantization.cpp:189-206, src/ops.cpp:378-455,
 // src/ops.cpp:132-171).
 //
-// Decode path (M <= 16): one wavefront streams one 1 KiB super-tile per
-// 128-bit load (lane = chunk), unpacks codes in registers, folds the scale
-// into the activation (xs = x * s, one multiply per row and lane) and
-// accumulates code * xs with FMAs.  Lanes of the four bands are combined with
-// cross-lane shuffles, the four waves of a workgroup through LDS, and the
-// split-K workgroups of one column block by the last one to finish, which sums
-// the partials in a fixed order (deterministic; no output pre-fill needed).
+// Decode path (M <= 16): a workgroup owns S strips (whole columns over all of
+// K), so no workgroup ever needs another's result.  Its four wavefronts split
+// K; within a wavefront 64/S lanes take consecutive row quads of one strip, so
+// every 128-bit load of packed codes is part of a contiguous run.  All loads
+// of a batch of row quads are issued before any is consumed.  Codes are
+// unpacked in registers, the scale is folded into the activation (xs = x * s,
+// one multiply per row and lane) and code * xs is accumulated with FMAs.  Lanes
+// of a strip are combined by a butterfly that halves the values each lane
+// carries at every step, the four wavefronts through LDS.
 //
 // Prefill path (M > 16): 128x128 output tiles, K staged through LDS 16 rows at
 // a time; codes are dequantized on the way into LDS (code * scale, the
@@ -31,7 +33,7 @@ __device__ __forceinline__ uint4 load_stream(const uint4* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// Byte b of w read as a signed int8 and converted to fp32 in one VALU op
+// Byte B of w read as a signed int8 and converted to fp32 in one VALU op
 // (v_cvt_f32_i32 with an SDWA sign-extended byte select).  For INT4, a byte
 // holding a code in its high nibble and zero below reads as 16*q exactly.
 template <int B>
@@ -52,58 +54,10 @@ __device__ __forceinline__ float i8_byte(uint32_t w, int b) {
     return b == 0 ? cvt_sbyte<0>(w) : (b == 1 ? cvt_sbyte<1>(w) : (b == 2 ? cvt_sbyte<2>(w) : cvt_sbyte<3>(w)));
 }
 
-// ---------------------------------------------------------------------------
-// Shared epilogue of the GEMV kernels: wave results are in red[wave][m][col].
-// Sums the four waves, then either writes y (ksplit == 1) or stores a partial
-// and lets the last workgroup of the column block reduce all partials.
-// ---------------------------------------------------------------------------
-template <int MT, int TN>
-__device__ __forceinline__ void gemv_finish(float (*red)[MT][TN], int M, int N, int n_base, int Npad, float post,
-                                            const float* __restrict__ bias, float* __restrict__ y,
-                                            float* __restrict__ part, unsigned* __restrict__ cnt, int cb, int ks,
-                                            int ksplit, unsigned* s_last) {
-    const int tid = threadIdx.x;
-    if (ksplit == 1) {
-        for (int o = tid; o < MT * TN; o += kThreads) {
-            const int m = o / TN, i = o - m * TN;
-            const int n = n_base + i;
-            if (m < M && n < N) {
-                float v = (red[0][m][i] + red[1][m][i]) + (red[2][m][i] + red[3][m][i]);
-                v = v * post;
-                if (bias) v = v + bias[n];
-                y[(int64_t)m * N + n] = v;
-            }
-        }
-        return;
-    }
-    for (int o = tid; o < MT * TN; o += kThreads) {
-        const int m = o / TN, i = o - m * TN;
-        if (m < M) {
-            const float v = (red[0][m][i] + red[1][m][i]) + (red[2][m][i] + red[3][m][i]);
-            part[((int64_t)ks * M + m) * Npad + n_base + i] = v;
-        }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(&cnt[cb], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        *s_last = (prev == (unsigned)(ksplit - 1)) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (*s_last == 0u) return;
-    __threadfence();
-    for (int o = tid; o < MT * TN; o += kThreads) {
-        const int m = o / TN, i = o - m * TN;
-        const int n = n_base + i;
-        if (m < M && n < N) {
-            float v = 0.0f;
-            for (int s = 0; s < ksplit; ++s) v += part[((int64_t)s * M + m) * Npad + n];
-            v = v * post;
-            if (bias) v = v + bias[n];
-            y[(int64_t)m * N + n] = v;
-        }
-    }
-    if (tid == 0) __hip_atomic_store(&cnt[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float nibble(uint32_t w, int e) { return (float)(((int)(w << (28 - 4 * e))) >> 28); }
+
+__device__ __forceinline__ float f4get(const float4& v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
 // Loads x[m][k0..k0+3] (zero past K and past M).
@@ -123,169 +77,160 @@ __device__ __forceinline__ float4 load_x4(const float* __restrict__ x, int m, in
     return r;
 }
 
-__device__ __forceinline__ float f4get(const float4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
+// Sum of v[0..H) over the lanes of an aligned group whose lane bits below O*2
+// differ.  Each step halves the values a lane carries: the lane with bit O set
+// keeps the upper half and adds its partner's upper half, the other keeps the
+// lower half.  When one value is left the remaining steps are plain
+// butterflies.  On return v[0..H>>steps) holds totals for indices base + i.
+template <int H, int O>
+struct StripReduce {
+    static __device__ __forceinline__ void run(float* v, int lane, int& base) {
+        if constexpr (O == 0) {
+            return;
+        } else if constexpr (H > 1) {
+            constexpr int h = H / 2;
+            const bool upper = (lane & O) != 0;
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                const float send = upper ? v[i] : v[i + h];
+                const float keep = upper ? v[i + h] : v[i];
+                v[i] = keep + __shfl_xor(send, O);
+            }
+            if (upper) base += h;
+            StripReduce<h, O / 2>::run(v, lane, base);
+        } else {
+            v[0] += __shfl_xor(v[0], O);
+            StripReduce<1, O / 2>::run(v, lane, base);
+        }
+    }
+};
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
 // ---------------------------------------------------------------------------
-// INT4 GEMV / skinny GEMM.  grid = NCB * ksplit workgroups of 256 threads.
+// GEMV / skinny GEMM for M <= 16.  BITS 4: strips of 8 columns, scales from
+// devscales[j / spc][k]; BITS 8: strips of 4 columns, scales[0] (per-tensor)
+// or scales[k] (per-row).  Grid: ceil(NS / S) workgroups of 256 threads.
 // ---------------------------------------------------------------------------
-template <int MT, bool KALIGN4>
-__global__ __launch_bounds__(kThreads) void k_gemv_i4(const float* __restrict__ x, int M, int K, int N,
-                                                      const uint4* __restrict__ W, const float* __restrict__ S,
-                                                      int spc, int Kpad, int KT, const float* __restrict__ bias,
-                                                      float* __restrict__ y, float* __restrict__ part,
-                                                      unsigned* __restrict__ cnt, int ksplit, int tps) {
-    __shared__ float red[4][MT][128];
-    __shared__ unsigned s_last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cb = blockIdx.x / ksplit, ks = blockIdx.x - cb * ksplit;
-    const int band = lane >> 4, strip = lane & 15;
-    const int t0 = ks * tps;
-    const int t1 = min(KT, t0 + tps);
-    const float* __restrict__ Sc = S + (int64_t)((cb * 16 + strip) / spc) * Kpad;
-    const uint4* __restrict__ Wb = W + (int64_t)cb * KT * 64 + lane;
+template <int BITS, int MT, int S, bool KALIGN4>
+__global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, int M, int K, int N,
+                                                   const uint4* __restrict__ W, const float* __restrict__ SC,
+                                                   int mode, int Kpad, int RQ, int NS,
+                                                   const float* __restrict__ bias, float* __restrict__ y) {
+    constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
+    constexpr int LPS = 64 / S;              // lanes per strip
+    constexpr int RQ_IT = 4 * LPS;           // row quads per strip per workgroup iteration
+    constexpr int V = MT * SW;               // accumulators per lane
+    constexpr int U = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);  // row quads in flight per lane (register budget)
+    __shared__ float red[4][S][V];
 
-    float acc[MT][8];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sl = lane / LPS, lq = lane - sl * LPS;
+    const int j = blockIdx.x * S + sl;
+    const int jc = j < NS ? j : NS - 1;  // keep addresses in bounds; results of j >= NS are dropped
+    const uint4* __restrict__ Wj = W + (int64_t)jc * RQ;
+    const float* __restrict__ Sc = SC;
+    float s_all = 0.0f;
+    if constexpr (BITS == 4) {
+        Sc = SC + (int64_t)(jc / mode) * Kpad;
+    } else {
+        if (mode) s_all = SC[0];
+    }
 
-    constexpr int U = (MT <= 2) ? 4 : 2;
-    for (int tb = t0 + wave; tb < t1; tb += 4 * U) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+
+    const int nit = (RQ + RQ_IT - 1) / RQ_IT;
+    for (int it0 = 0; it0 < nit; it0 += U) {
         uint4 w[U];
-        float4 s4[U];
+        float4 sv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int t = tb + 4 * u;
-            if (t < t1) {
-                w[u] = load_stream(Wb + (int64_t)t * 64);
-                s4[u] = *(const float4*)(Sc + t * 16 + band * 4);
+            const int rq = (it0 + u) * RQ_IT + wave * LPS + lq;
+            const bool ok = rq < RQ;
+            w[u] = ok ? load_stream(Wj + rq) : make_uint4(0u, 0u, 0u, 0u);
+            if constexpr (BITS == 4) {
+                sv[u] = ok ? *(const float4*)(Sc + 4 * rq) : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
-                w[u] = make_uint4(0u, 0u, 0u, 0u);
-                s4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                const int k0 = 4 * rq;
+                if (mode) {
+                    sv[u] = make_float4(s_all, s_all, s_all, s_all);
+                } else if (k0 + 3 < K) {
+                    sv[u] = *(const float4*)(Sc + k0);
+                } else {
+                    sv[u].x = (k0 + 0 < K) ? Sc[k0 + 0] : 0.0f;
+                    sv[u].y = (k0 + 1 < K) ? Sc[k0 + 1] : 0.0f;
+                    sv[u].z = (k0 + 2 < K) ? Sc[k0 + 2] : 0.0f;
+                    sv[u].w = (k0 + 3 < K) ? Sc[k0 + 3] : 0.0f;
+                }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int t = tb + 4 * u;
-            if (t >= t1) break;
-            const int k0 = t * 16 + band * 4;
+            const int rq = (it0 + u) * RQ_IT + wave * LPS + lq;
+            const int k0 = 4 * rq;
             const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const float4 xv = load_x4<KALIGN4>(x, m, M, K, k0);
+                float xs[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float xs = f4get(xv, r) * f4get(s4[u], r);
-                    const uint32_t hi = dw[r] & 0xF0F0F0F0u;
-                    const uint32_t lo = (dw[r] << 4) & 0xF0F0F0F0u;
+                    // Rows past K contribute exactly zero: INT4 padding rows have
+                    // zero scales; INT8 ones are masked (no 0 * inf from a per-tensor scale).
+                    if constexpr (BITS == 4)
+                        xs[r] = f4get(xv, r) * f4get(sv[u], r);
+                    else
+                        xs[r] = (k0 + r < K) ? f4get(xv, r) * f4get(sv[u], r) : 0.0f;
+                }
+                if constexpr (BITS == 4) {
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        acc[m][2 * b] = fmaf(i8_byte(lo, b), xs, acc[m][2 * b]);
-                        acc[m][2 * b + 1] = fmaf(i8_byte(hi, b), xs, acc[m][2 * b + 1]);
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t hi = dw[r] & 0xF0F0F0F0u;         // columns 2b+1, as 16*q
+                        const uint32_t lo = (dw[r] << 4) & 0xF0F0F0F0u;  // columns 2b, as 16*q
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) {
+                            acc[m * 8 + 2 * b] = fmaf(i8_byte(lo, b), xs[r], acc[m * 8 + 2 * b]);
+                            acc[m * 8 + 2 * b + 1] = fmaf(i8_byte(hi, b), xs[r], acc[m * 8 + 2 * b + 1]);
+                        }
                     }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) acc[m * 4 + d] = fmaf(i8_byte(dw[d], r), xs[r], acc[m * 4 + d]);
                 }
             }
         }
     }
 
-    // Combine the four bands (lanes l, l^16, l^32, l^48 share columns).
+    // Combine the LPS lanes of each strip.
+    int base = 0;
+    StripReduce<V, LPS / 2>::run(acc, lane, base);
+    constexpr int steps_t = ilog2(LPS) < ilog2(V) ? ilog2(LPS) : ilog2(V);
+    constexpr int left = V >> steps_t;              // values a lane holds now
+    constexpr int dup_mask = (LPS >> steps_t) - 1;  // lanes holding identical totals
+    if ((lq & dup_mask) == 0) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[m][e];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[m][e] = v;
-        }
-    if (band == 0) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) red[wave][m][strip * 8 + e] = acc[m][e];
+        for (int i = 0; i < left; ++i) red[wave][sl][base + i] = acc[i];
     }
     __syncthreads();
-    // Codes were read as 16*q: scale the sum back by 1/16 (exact).
-    gemv_finish<MT, 128>(red, M, N, cb * 128, (int)round_up(N, kI4TileN), 0.0625f, bias, y, part, cnt, cb, ks,
-                         ksplit, &s_last);
-}
 
-// ---------------------------------------------------------------------------
-// INT8 GEMV / skinny GEMM.  Scales: per-tensor scales[0] or per-row scales[k].
-// ---------------------------------------------------------------------------
-template <int MT, bool KALIGN4>
-__global__ __launch_bounds__(kThreads) void k_gemv_i8(const float* __restrict__ x, int M, int K, int N,
-                                                      const uint4* __restrict__ W, const float* __restrict__ S,
-                                                      int per_tensor, int KT, const float* __restrict__ bias,
-                                                      float* __restrict__ y, float* __restrict__ part,
-                                                      unsigned* __restrict__ cnt, int ksplit, int tps) {
-    __shared__ float red[4][MT][64];
-    __shared__ unsigned s_last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cb = blockIdx.x / ksplit, ks = blockIdx.x - cb * ksplit;
-    const int band = lane >> 4, strip = lane & 15;
-    const int t0 = ks * tps;
-    const int t1 = min(KT, t0 + tps);
-    const uint4* __restrict__ Wb = W + (int64_t)cb * KT * 64 + lane;
-    const float s_all = per_tensor ? S[0] : 0.0f;
-
-    float acc[MT][4];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int d = 0; d < 4; ++d) acc[m][d] = 0.0f;
-
-    constexpr int U = (MT <= 2) ? 4 : 2;
-    for (int tb = t0 + wave; tb < t1; tb += 4 * U) {
-        uint4 w[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = tb + 4 * u;
-            w[u] = (t < t1) ? load_stream(Wb + (int64_t)t * 64) : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = tb + 4 * u;
-            if (t >= t1) break;
-            const int k0 = t * 16 + band * 4;
-            float s[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) s[r] = per_tensor ? s_all : ((k0 + r < K) ? S[k0 + r] : 0.0f);
-            const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                const float4 xv = load_x4<KALIGN4>(x, m, M, K, k0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float xs = f4get(xv, r) * s[r];
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) acc[m][d] = fmaf(i8_byte(dw[d], r), xs, acc[m][d]);
-                }
-            }
+    // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
+    const float post = (BITS == 4) ? 0.0625f : 1.0f;
+    for (int o = threadIdx.x; o < S * V; o += kThreads) {
+        const int s_idx = o / V, v = o - s_idx * V;
+        const int m = v / SW, e = v - m * SW;
+        const int jj = blockIdx.x * S + s_idx;
+        const int n = jj * SW + e;
+        if (jj < NS && m < M && n < N) {
+            float r = (red[0][s_idx][v] + red[1][s_idx][v]) + (red[2][s_idx][v] + red[3][s_idx][v]);
+            r = r * post;
+            if (bias) r = r + bias[n];
+            y[(int64_t)m * N + n] = r;
         }
     }
-
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            float v = acc[m][d];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[m][d] = v;
-        }
-    if (band == 0) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int d = 0; d < 4; ++d) red[wave][m][strip * 4 + d] = acc[m][d];
-    }
-    __syncthreads();
-    gemv_finish<MT, 64>(red, M, N, cb * 64, (int)round_up(N, kI8TileN), 1.0f, bias, y, part, cnt, cb, ks, ksplit,
-                        &s_last);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,8 +246,8 @@ constexpr int kBM = 128, kBN = 128, kBK = 16, kLdsStride = kBK + 4;
 template <int BITS, bool KALIGN4>
 __global__ __launch_bounds__(kThreads) void k_gemm(const float* __restrict__ x, int M, int K, int N,
                                                    const uint4* __restrict__ W, const float* __restrict__ S,
-                                                   int mode, int Kpad, int KT, const float* __restrict__ bias,
-                                                   float* __restrict__ y) {
+                                                   int mode, int Kpad, int RQ, int NS,
+                                                   const float* __restrict__ bias, float* __restrict__ y) {
     // mode: INT8 -> per_tensor flag; INT4 -> strips per scale column (spc).
     __shared__ __attribute__((aligned(16))) float As[2][kBM][kLdsStride];
     __shared__ __attribute__((aligned(16))) float Bs[2][kBN][kLdsStride];
@@ -311,10 +256,17 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const float* __restrict__ x, 
     const int ntn = (N + kBN - 1) / kBN;
     const int tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
     const int m0 = tm * kBM, n0 = tn * kBN;
+    const int KT = Kpad / kBK;
 
-    // ---- global -> register staging -------------------------------------
+    constexpr int SW = (BITS == 4) ? 8 : 4;
+    constexpr int kStrips = kBN / SW;      // strips per tile: 16 (INT4) or 32 (INT8)
+    constexpr int kBChunks = kStrips * 4;  // 4 row quads per strip per stage
+    // chunk t of a stage: strip n0/SW + (t >> 2), row quad 4*kt + (t & 3)
+    const int bj = n0 / SW + (tid >> 2);
+    const bool b_ok = tid < kBChunks && bj < NS;
+
     float4 ra[2];
-    uint4 rb;
+    uint4 rb = make_uint4(0u, 0u, 0u, 0u);
     auto load_a = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -336,16 +288,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const float* __restrict__ x, 
             ra[i] = v;
         }
     };
-    // INT8: 128 columns = two 64-column blocks -> threads 0..127 take one chunk each.
-    // INT4: 128 columns = one 128-column block -> threads 0..63 take one chunk each.
-    constexpr int kBChunks = (BITS == 8) ? 128 : 64;
     auto load_b = [&](int kt) {
-        if (tid < kBChunks) {
-            const int cbl = tid >> 6, ch = tid & 63;
-            const int64_t cb = (BITS == 8) ? (int64_t)(n0 / 64 + cbl) : (int64_t)(n0 / 128);
-            // INT8 pads N to 64 only: the second half of the last tile may not exist.
-            rb = (BITS == 4 || cb < (N + 63) / 64) ? W[(cb * KT + kt) * 64 + ch] : make_uint4(0u, 0u, 0u, 0u);
-        }
+        if (b_ok) rb = W[(int64_t)bj * RQ + kt * 4 + (tid & 3)];
     };
     auto store_a = [&](int buf) {
 #pragma unroll
@@ -357,35 +301,34 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const float* __restrict__ x, 
     };
     auto store_b = [&](int buf, int kt) {
         if (tid >= kBChunks) return;
-        const int ch = tid & 63, band = ch >> 4, strip = ch & 15;
-        const int kl = band * 4;
+        const int jl = tid >> 2, kl = (tid & 3) * 4;
         const int k = kt * kBK + kl;
         const uint32_t dw[4] = {rb.x, rb.y, rb.z, rb.w};
         if (BITS == 8) {
             float s[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) s[r] = mode ? S[0] : ((k + r < K) ? S[k + r] : 0.0f);
-            const int nl = (tid >> 6) * 64 + strip * 4;
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
+                // Rows past K are exactly zero (no 0 * inf from a per-tensor scale).
                 float4 v;
-                v.x = i8_byte(dw[d], 0) * s[0];
-                v.y = i8_byte(dw[d], 1) * s[1];
-                v.z = i8_byte(dw[d], 2) * s[2];
-                v.w = i8_byte(dw[d], 3) * s[3];
-                *(float4*)&Bs[buf][nl + d][kl] = v;
+                v.x = (k + 0 < K) ? i8_byte(dw[d], 0) * s[0] : 0.0f;
+                v.y = (k + 1 < K) ? i8_byte(dw[d], 1) * s[1] : 0.0f;
+                v.z = (k + 2 < K) ? i8_byte(dw[d], 2) * s[2] : 0.0f;
+                v.w = (k + 3 < K) ? i8_byte(dw[d], 3) * s[3] : 0.0f;
+                *(float4*)&Bs[buf][jl * 4 + d][kl] = v;
             }
         } else {
-            const float4 s = *(const float4*)(S + (int64_t)((n0 / 8 + strip) / mode) * Kpad + k);
-            const int nl = strip * 8;
+            const int jc = bj < NS ? bj : NS - 1;
+            const float4 s = *(const float4*)(S + (int64_t)(jc / mode) * Kpad + k);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float4 v;
-                v.x = (float)(((int)(dw[0] << (28 - 4 * e))) >> 28) * s.x;
-                v.y = (float)(((int)(dw[1] << (28 - 4 * e))) >> 28) * s.y;
-                v.z = (float)(((int)(dw[2] << (28 - 4 * e))) >> 28) * s.z;
-                v.w = (float)(((int)(dw[3] << (28 - 4 * e))) >> 28) * s.w;
-                *(float4*)&Bs[buf][nl + e][kl] = v;
+                v.x = nibble(dw[0], e) * s.x;
+                v.y = nibble(dw[1], e) * s.y;
+                v.z = nibble(dw[2], e) * s.z;
+                v.w = nibble(dw[3], e) * s.w;
+                *(float4*)&Bs[buf][jl * 8 + e][kl] = v;
             }
         }
     };
@@ -450,7 +393,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(const float* __restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// Generic INT4 forward over the flat layout (shapes the tiled layout cannot
+// Generic INT4 forward over the flat layout (shapes the strip layout cannot
 // hold).  One thread per output; per-element scale index, the reference's own
 // product code*scale, FMA accumulation in k order.
 // ---------------------------------------------------------------------------
@@ -472,99 +415,97 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
     }
 }
 
-template <int MT>
-hipError_t gemv_i4_dispatch(const float* x, int M, int K, int N, const void* packed, const float* devscales,
-                            const I4Geom& g, const float* bias, float* y, float* partial, unsigned* counters,
-                            hipStream_t s) {
-    const GemvPlan p = gemv_plan(g.KT, g.NCB);
-    const dim3 grid((unsigned)(g.NCB * p.ksplit));
-    if (K % 4 == 0 && (((uintptr_t)x) & 15) == 0)
-        k_gemv_i4<MT, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, devscales, (int)g.spc,
-                                                      (int)g.Kpad, (int)g.KT, bias, y, partial, counters, p.ksplit,
-                                                      p.tps);
+bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
+
+// Strips per workgroup: enough workgroups to fill the GPU, wider strips when
+// there are plenty.
+int pick_strips(int64_t NS) {
+    if (NS >= 2048) return 4;
+    if (NS >= 512) return 2;
+    return 1;
+}
+
+template <int BITS, int MT, int S>
+hipError_t gemv_launch(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
+                       int RQ, int NS, const float* bias, float* y, hipStream_t s) {
+    const dim3 grid((unsigned)ceil_div(NS, S));
+    if (x_aligned4(x, K))
+        k_gemv<BITS, MT, S, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, NS,
+                                                           bias, y);
     else
-        k_gemv_i4<MT, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, devscales, (int)g.spc,
-                                                       (int)g.Kpad, (int)g.KT, bias, y, partial, counters,
-                                                       p.ksplit, p.tps);
+        k_gemv<BITS, MT, S, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
+                                                            NS, bias, y);
     return hipGetLastError();
 }
 
-template <int MT>
-hipError_t gemv_i8_dispatch(const float* x, int M, int K, int N, const void* packed, const float* scales,
-                            bool per_tensor, const float* bias, float* y, float* partial, unsigned* counters,
-                            hipStream_t s) {
-    I8Geom g(K, N);
-    const GemvPlan p = gemv_plan(g.KT, g.NCB);
-    const dim3 grid((unsigned)(g.NCB * p.ksplit));
-    if (K % 4 == 0 && (((uintptr_t)x) & 15) == 0)
-        k_gemv_i8<MT, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, scales, per_tensor ? 1 : 0,
-                                                      (int)g.KT, bias, y, partial, counters, p.ksplit, p.tps);
-    else
-        k_gemv_i8<MT, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, scales,
-                                                       per_tensor ? 1 : 0, (int)g.KT, bias, y, partial, counters,
-                                                       p.ksplit, p.tps);
-    return hipGetLastError();
+template <int BITS, int MT>
+hipError_t gemv_strips(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
+                       int RQ, int NS, const float* bias, float* y, hipStream_t s) {
+    switch (pick_strips(NS)) {
+        case 4: return gemv_launch<BITS, MT, 4>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
+        case 2: return gemv_launch<BITS, MT, 2>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
+        default: return gemv_launch<BITS, MT, 1>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
+    }
+}
+
+// Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
+template <int BITS>
+hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc,
+                         int mode, int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, hipStream_t s) {
+    const int k = (int)K, n = (int)N, kp = (int)Kpad, rq = (int)RQ, ns = (int)NS;
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int m = (int)((M - m0) < 8 ? (M - m0) : 8);
+        const float* xm = x + m0 * K;
+        float* ym = y + m0 * N;
+        hipError_t e;
+        if (m <= 1)
+            e = gemv_strips<BITS, 1>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+        else if (m <= 2)
+            e = gemv_strips<BITS, 2>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+        else if (m <= 4)
+            e = gemv_strips<BITS, 4>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+        else
+            e = gemv_strips<BITS, 8>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace
 
-GemvPlan gemv_plan(int64_t KT, int64_t NCB) {
-    // Aim for ~1024 workgroups (4 per CU) with at least 8 super-tiles
-    // (two per wave) in every k-range.
-    int64_t ksplit = 1024 / (NCB > 0 ? NCB : 1);
-    int64_t max_split = KT / 8;
-    if (ksplit > max_split) ksplit = max_split;
-    if (ksplit < 1) ksplit = 1;
-    int64_t tps = ceil_div(KT, ksplit);
-    ksplit = ceil_div(KT, tps);  // drop empty ranges
-    if (ksplit < 1) ksplit = 1;
-    return GemvPlan{(int)ksplit, (int)tps};
-}
-
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
-                          const float* devscales, const I4Geom& g, const float* bias, float* y, float* partial,
-                          unsigned* counters, hipStream_t s) {
-    const int m = (int)M, k = (int)K, n = (int)N;
-    if (M <= 1) return gemv_i4_dispatch<1>(x, m, k, n, packed, devscales, g, bias, y, partial, counters, s);
-    if (M <= 2) return gemv_i4_dispatch<2>(x, m, k, n, packed, devscales, g, bias, y, partial, counters, s);
-    if (M <= 4) return gemv_i4_dispatch<4>(x, m, k, n, packed, devscales, g, bias, y, partial, counters, s);
-    if (M <= 8) return gemv_i4_dispatch<8>(x, m, k, n, packed, devscales, g, bias, y, partial, counters, s);
-    return gemv_i4_dispatch<16>(x, m, k, n, packed, devscales, g, bias, y, partial, counters, s);
+                          const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
+    return gemv_dispatch<4>(x, M, K, N, packed, devscales, (int)g.spc, g.Kpad, g.RQ, g.NS, bias, y, s);
 }
 
 hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
-                          bool per_tensor, const float* bias, float* y, float* partial, unsigned* counters,
-                          hipStream_t s) {
-    const int m = (int)M, k = (int)K, n = (int)N;
-    if (M <= 1) return gemv_i8_dispatch<1>(x, m, k, n, packed, scales, per_tensor, bias, y, partial, counters, s);
-    if (M <= 2) return gemv_i8_dispatch<2>(x, m, k, n, packed, scales, per_tensor, bias, y, partial, counters, s);
-    if (M <= 4) return gemv_i8_dispatch<4>(x, m, k, n, packed, scales, per_tensor, bias, y, partial, counters, s);
-    if (M <= 8) return gemv_i8_dispatch<8>(x, m, k, n, packed, scales, per_tensor, bias, y, partial, counters, s);
-    return gemv_i8_dispatch<16>(x, m, k, n, packed, scales, per_tensor, bias, y, partial, counters, s);
+                          bool per_tensor, const float* bias, float* y, hipStream_t s) {
+    I8Geom g(K, N);
+    return gemv_dispatch<8>(x, M, K, N, packed, scales, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, bias, y, s);
 }
 
 hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, hipStream_t s) {
     I8Geom g(K, N);
     const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN)));
-    if (K % 4 == 0 && (((uintptr_t)x) & 15) == 0)
+    if (x_aligned4(x, K))
         k_gemm<8, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, scales,
-                                                  per_tensor ? 1 : 0, (int)g.Kpad, (int)g.KT, bias, y);
+                                                  per_tensor ? 1 : 0, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
     else
         k_gemm<8, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, scales,
-                                                   per_tensor ? 1 : 0, (int)g.Kpad, (int)g.KT, bias, y);
+                                                   per_tensor ? 1 : 0, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
     const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN)));
-    if (K % 4 == 0 && (((uintptr_t)x) & 15) == 0)
+    if (x_aligned4(x, K))
         k_gemm<4, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, devscales,
-                                                  (int)g.spc, (int)g.Kpad, (int)g.KT, bias, y);
+                                                  (int)g.spc, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
     else
         k_gemm<4, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, devscales,
-                                                   (int)g.spc, (int)g.Kpad, (int)g.KT, bias, y);
+                                                   (int)g.spc, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
     return hipGetLastError();
 }
 

@@ -83,17 +83,15 @@ __global__ void k_absmax_partial(const float* __restrict__ x, int64_t total, flo
     }
 }
 
-// INT8 tiled pack: one thread per 16-byte chunk (4 columns x 4 rows).
-__global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t KT,
+// INT8 strip-major pack: one thread per 16-byte chunk (4 columns x 4 rows).
+__global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t RQ,
                                 int64_t nchunks, const float* __restrict__ inv, int per_tensor,
                                 uint4* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t st = c >> 6;
-    const int ch = (int)(c & 63);
-    const int64_t cb = st / KT, kt = st - cb * KT;
-    const int64_t k0 = kt * kTileK + (ch >> 4) * 4;
-    const int64_t n0 = cb * kI8TileN + (ch & 15) * 4;
+    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 4;
     uint32_t dw[4];
     int badflag = 0;
 #pragma unroll
@@ -127,17 +125,15 @@ __global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, i
     }
 }
 
-// INT4 tiled pack: one thread per 16-byte chunk (4 rows x 8 columns).
+// INT4 strip-major pack: one thread per 16-byte chunk (4 rows x 8 columns).
 __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t G,
-                                int64_t KT, int64_t nchunks, const float* __restrict__ inv,
+                                int64_t RQ, int64_t nchunks, const float* __restrict__ inv,
                                 uint4* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t st = c >> 6;
-    const int ch = (int)(c & 63);
-    const int64_t cb = st / KT, kt = st - cb * KT;
-    const int64_t k0 = kt * kTileK + (ch >> 4) * 4;
-    const int64_t n0 = cb * kI4TileN + (ch & 15) * 8;
+    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 8;
     uint32_t dw[4];
     int badflag = 0;
 #pragma unroll
@@ -213,16 +209,14 @@ __global__ void k_devscales_i4(const float* __restrict__ scales, int64_t K, int6
     }
 }
 
-__global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t KT,
+__global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t RQ,
                                   int64_t nchunks, const float* __restrict__ scales, int per_tensor,
                                   float* __restrict__ out) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t st = c >> 6;
-    const int ch = (int)(c & 63);
-    const int64_t cb = st / KT, kt = st - cb * KT;
-    const int64_t k0 = kt * kTileK + (ch >> 4) * 4;
-    const int64_t n0 = cb * kI8TileN + (ch & 15) * 4;
+    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 4;
     const uint4 w = packed[c];
     const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -240,15 +234,13 @@ __global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, i
     }
 }
 
-__global__ void k_unpack_i4_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t G, int64_t KT,
+__global__ void k_unpack_i4_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t G, int64_t RQ,
                                   int64_t nchunks, const float* __restrict__ scales, float* __restrict__ out) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t st = c >> 6;
-    const int ch = (int)(c & 63);
-    const int64_t cb = st / KT, kt = st - cb * KT;
-    const int64_t k0 = kt * kTileK + (ch >> 4) * 4;
-    const int64_t n0 = cb * kI4TileN + (ch & 15) * 8;
+    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 8;
     const uint4 w = packed[c];
     const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -325,9 +317,9 @@ hipError_t launch_absmax_partial(const float* x, int64_t total, float* partial, 
 hipError_t launch_pack_i8_tiled(const float* src, bool from_codes, int64_t K, int64_t N, const float* inv,
                                 bool per_tensor, void* packed, float* qdata, int* bad, hipStream_t s) {
     I8Geom g(K, N);
-    const int64_t nchunks = g.NCB * g.KT * 64;
+    const int64_t nchunks = g.chunks();
     if (nchunks <= 0) return hipSuccess;
-    k_pack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.KT, nchunks, inv, per_tensor,
+    k_pack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.RQ, nchunks, inv, per_tensor,
                                                          (uint4*)packed, qdata, bad);
     return hipGetLastError();
 }
@@ -335,9 +327,9 @@ hipError_t launch_pack_i8_tiled(const float* src, bool from_codes, int64_t K, in
 hipError_t launch_pack_i4_tiled(const float* src, bool from_codes, int64_t K, int64_t N, int64_t G,
                                 const float* inv, void* packed, float* qdata, int* bad, hipStream_t s) {
     I4Geom g(K, N, G);
-    const int64_t nchunks = g.NCB * g.KT * 64;
+    const int64_t nchunks = g.chunks();
     if (nchunks <= 0) return hipSuccess;
-    k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.KT, nchunks, inv,
+    k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.RQ, nchunks, inv,
                                                          (uint4*)packed, qdata, bad);
     return hipGetLastError();
 }
@@ -361,9 +353,9 @@ hipError_t launch_devscales_i4(const float* scales, const I4Geom& g, float* devs
 hipError_t launch_unpack_i8_tiled(const void* packed, int64_t K, int64_t N, const float* scales, bool per_tensor,
                                   float* out, hipStream_t s) {
     I8Geom g(K, N);
-    const int64_t nchunks = g.NCB * g.KT * 64;
+    const int64_t nchunks = g.chunks();
     if (nchunks <= 0 || K * N <= 0) return hipSuccess;
-    k_unpack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.KT, nchunks, scales,
+    k_unpack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.RQ, nchunks, scales,
                                                            per_tensor, out);
     return hipGetLastError();
 }
@@ -371,9 +363,9 @@ hipError_t launch_unpack_i8_tiled(const void* packed, int64_t K, int64_t N, cons
 hipError_t launch_unpack_i4_tiled(const void* packed, int64_t K, int64_t N, int64_t G, const float* scales,
                                   float* out, hipStream_t s) {
     I4Geom g(K, N, G);
-    const int64_t nchunks = g.NCB * g.KT * 64;
+    const int64_t nchunks = g.chunks();
     if (nchunks <= 0 || K * N <= 0) return hipSuccess;
-    k_unpack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.G, g.KT, nchunks, scales,
+    k_unpack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.G, g.RQ, nchunks, scales,
                                                            out);
     return hipGetLastError();
 }

@@ -85,41 +85,42 @@ def _ceil(a, b):
 
 
 def i8_geom(K, N):
-    Kpad, Npad = _ceil(K, 16) * 16, _ceil(N, 64) * 64
-    return Kpad, Npad, Kpad // 16, Npad // 64
+    """(Kpad, RQ, NS): rows padded to 16, row quads, strips of 4 columns."""
+    Kpad = _ceil(K, 16) * 16
+    return Kpad, Kpad // 4, _ceil(N, 4)
 
 
 def i4_geom(K, N, G):
     G = G if G > 0 else 32
-    Kpad, Npad = _ceil(K, 16) * 16, _ceil(N, 128) * 128
+    Kpad = _ceil(K, 16) * 16
     tiled = N % 8 == 0 and G % 8 == 0
+    NS = N // 8
     spc = G // 8 if (tiled and N % G == 0) else 1
-    nsc = _ceil(Npad // 128 * 16, spc) if tiled else 0
-    return dict(G=G, Kpad=Kpad, Npad=Npad, KT=Kpad // 16, NCB=Npad // 128, tiled=tiled, spc=spc, nsc=nsc)
+    nsc = _ceil(NS, spc) if tiled else 0
+    return dict(G=G, Kpad=Kpad, RQ=Kpad // 4, NS=NS, tiled=tiled, spc=spc, nsc=nsc)
 
 
 def model_pack_i8(codes: np.ndarray) -> np.ndarray:
-    """INT8 tiled: super-tile (cb, kt) of 16 rows x 64 cols at (cb*KT+kt)*1024;
-    chunk c = (band, strip); dword d = column 4*strip+d; byte r = row 4*band+r."""
+    """INT8 strip-major: chunk (strip j, row quad rq) at (j*RQ + rq)*16;
+    dword d = column 4*j+d; byte r = row 4*rq+r."""
     K, N = codes.shape
-    Kpad, Npad, KT, NCB = i8_geom(K, N)
-    full = np.zeros((Kpad, Npad), np.int8)
+    Kpad, RQ, NS = i8_geom(K, N)
+    full = np.zeros((Kpad, NS * 4), np.int8)
     full[:K, :N] = codes.astype(np.int8)
-    # [NCB][KT][band 4][strip 16][col d 4][row r 4]
-    t = full.reshape(KT, 4, 4, NCB, 16, 4)  # kt, band, r, cb, strip, d
-    t = t.transpose(3, 0, 1, 4, 5, 2)  # cb, kt, band, strip, d, r
+    t = full.reshape(RQ, 4, NS, 4)  # rq, r, j, d
+    t = t.transpose(2, 0, 3, 1)  # j, rq, d, r
     return np.ascontiguousarray(t).view(np.uint8).reshape(-1)
 
 
 def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
-    """INT4 tiled: super-tile of 16 rows x 128 cols; chunk c = (band, strip);
-    dword r = row 4*band+r; nibble e = column 8*strip+e (low nibble first)."""
+    """INT4 strip-major: chunk (strip j, row quad rq) at (j*RQ + rq)*16;
+    dword r = row 4*rq+r; nibble e = column 8*j+e (low nibble first)."""
     K, N = codes.shape
     g = i4_geom(K, N, G)
-    full = np.zeros((g["Kpad"], g["Npad"]), np.int64)
+    full = np.zeros((g["Kpad"], N), np.int64)
     full[:K, :N] = codes.astype(np.int64)
-    t = full.reshape(g["KT"], 4, 4, g["NCB"], 16, 8)  # kt, band, r, cb, strip, e
-    t = t.transpose(3, 0, 1, 4, 2, 5)  # cb, kt, band, strip, r, e
+    t = full.reshape(g["RQ"], 4, g["NS"], 8)  # rq, r, j, e
+    t = t.transpose(2, 0, 1, 3)  # j, rq, r, e
     nib = (t & 0xF).astype(np.uint32)
     shifts = (np.arange(8, dtype=np.uint32) * 4)
     words = np.bitwise_or.reduce(nib << shifts, axis=-1).astype(np.uint32)

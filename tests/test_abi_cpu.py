@@ -31,8 +31,8 @@ def test_abi_version(lib):
 
 @pytest.mark.parametrize("K,N", [(1, 1), (16, 64), (17, 65), (1024, 1024), (4096, 11008), (11008, 4096), (3, 0)])
 def test_int8_sizes(lib, K, N):
-    Kpad, Npad, KT, NCB = helpers.i8_geom(K, N)
-    assert lib.sgq_int8_packed_bytes(K, N) == NCB * KT * 1024
+    Kpad, RQ, NS = helpers.i8_geom(K, N)
+    assert lib.sgq_int8_packed_bytes(K, N) == NS * RQ * 16
     assert lib.sgq_int8_scale_count(K, N, 0) == 1
     assert lib.sgq_int8_scale_count(K, N, 1) == K
 
@@ -42,17 +42,22 @@ def test_int8_sizes(lib, K, N):
 def test_int4_sizes(lib, K, N, G):
     g = helpers.i4_geom(K, N, G)
     assert lib.sgq_int4_layout(K, N, G) == (0 if g["tiled"] else 1)
-    exp_bytes = g["NCB"] * g["KT"] * 1024 if g["tiled"] else (K * N + 1) // 2
+    exp_bytes = g["NS"] * g["RQ"] * 16 if g["tiled"] else (K * N + 1) // 2
     assert lib.sgq_int4_packed_bytes(K, N, G) == exp_bytes
     assert lib.sgq_int4_devscale_count(K, N, G) == (g["nsc"] * g["Kpad"] if g["tiled"] else 0)
     assert lib.sgq_int4_scale_count(K, N, G) == (K * N + g["G"] - 1) // g["G"]
 
 
 def test_workspace_sizes(lib):
-    assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) >= 4096 * 4
-    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) > 0
+    # The forward kernels need no workspace (each workgroup owns whole columns).
+    assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(3, 1, 4, 4) == -1
     assert lib.sgq_quantize_workspace_bytes(4, 4096, 4096, 128) >= 4096 * 4096 // 128 * 4
+    # Regression: K == 0 (and other degenerate shapes) must not divide by zero on the host.
+    for bits_ in (4, 8):
+        for (M, K, N) in [(3, 0, 16), (0, 0, 0), (1, 1, 0), (16, 0, 1), (1, 15, 1)]:
+            assert lib.sgq_linear_workspace_bytes(bits_, M, K, N) >= 0
 
 
 def test_argument_errors_before_gpu(lib, sgq):
@@ -65,8 +70,10 @@ def test_argument_errors_before_gpu(lib, sgq):
     assert lib.sgq_linear_int8(None, 1, 4, 4, None, None, 9, None, None, None, 0, None) == 1
     assert lib.sgq_linear_int4(None, -2, 4, 4, None, None, None, 32, None, None, None, 0, None) == 1
     assert lib.sgq_linear_int4(16, 1, 64, 64, 16, 16, None, 32, None, 16, None, 0, None) == 1  # no devscales
-    assert lib.sgq_linear_int4(16, 1, 64, 64, 16, 16, 16, 32, None, 16, None, 0, None) == 3  # no workspace
-    assert b"workspace" in lib.sgq_last_error()
+    assert lib.sgq_linear_int4(16, 1, 64, 64, 24, 16, 16, 32, None, 16, None, 0, None) == 1  # misaligned packed
+    assert b"aligned" in lib.sgq_last_error()
+    assert lib.sgq_linear_int8(16, 1, 64, 64, 16, 20, 1, None, 16, None, 0, None) == 1  # misaligned scales
+    assert lib.sgq_quantize_int4(16, 4, 64, 32, None, 16, 24, 16, None, 0, None) == 1  # misaligned packed
     # empty outputs are a no-op success
     assert lib.sgq_linear_int8(None, 0, 4, 4, None, None, 0, None, None, None, 0, None) == 0
 
@@ -74,9 +81,9 @@ def test_argument_errors_before_gpu(lib, sgq):
 # ---- numpy layout models -------------------------------------------------
 
 def _unpack_model_i8(buf, K, N):
-    Kpad, Npad, KT, NCB = helpers.i8_geom(K, N)
-    t = buf.view(np.int8).reshape(NCB, KT, 4, 16, 4, 4)  # cb, kt, band, strip, d, r
-    full = t.transpose(1, 2, 5, 0, 3, 4).reshape(Kpad, Npad)
+    Kpad, RQ, NS = helpers.i8_geom(K, N)
+    t = buf.view(np.int8).reshape(NS, RQ, 4, 4)  # j, rq, d, r
+    full = t.transpose(1, 3, 0, 2).reshape(Kpad, NS * 4)
     return full[:K, :N]
 
 
@@ -85,13 +92,12 @@ def test_model_pack_i8_roundtrip():
     for K, N in [(16, 64), (17, 70), (33, 130)]:
         q = rng.integers(-127, 128, size=(K, N))
         buf = helpers.model_pack_i8(q)
-        assert buf.size == helpers.i8_geom(K, N)[2] * helpers.i8_geom(K, N)[3] * 1024
+        Kpad, RQ, NS = helpers.i8_geom(K, N)
+        assert buf.size == NS * RQ * 16
         assert np.array_equal(_unpack_model_i8(buf, K, N), q)
         # element (k, n) sits at the documented byte
         k, n = K - 1, N - 1
-        cb, kt, band, strip, d, r = n // 64, k // 16, (k % 16) // 4, (n % 64) // 4, n % 4, k % 4
-        KT = helpers.i8_geom(K, N)[2]
-        off = (cb * KT + kt) * 1024 + (band * 16 + strip) * 16 + d * 4 + r
+        off = ((n // 4) * RQ + k // 4) * 16 + (n % 4) * 4 + k % 4
         assert buf.view(np.int8)[off] == q[k, n]
 
 
@@ -102,9 +108,8 @@ def test_model_pack_i4_positions():
     buf = helpers.model_pack_i4_tiled(q, 8)
     g = helpers.i4_geom(K, N, 8)
     for (k, n) in [(0, 0), (19, 135), (5, 77), (16, 128)]:
-        cb, kt, band, strip, r, e = n // 128, k // 16, (k % 16) // 4, (n % 128) // 8, k % 4, n % 8
-        off = (cb * g["KT"] + kt) * 1024 + (band * 16 + strip) * 16 + r * 4 + e // 2
-        nib = (int(buf[off]) >> (4 * (e % 2))) & 0xF
+        off = ((n // 8) * g["RQ"] + k // 4) * 16 + (k % 4) * 4 + (n % 8) // 2
+        nib = (int(buf[off]) >> (4 * (n % 2))) & 0xF
         assert ((nib ^ 8) - 8) == q[k, n]
 
 

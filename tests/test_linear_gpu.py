@@ -174,6 +174,30 @@ def test_deterministic_and_workspace_reuse(sgq, dev, synth):
         assert torch.equal(y1, y2)
 
 
+def test_workspace_shared_across_shapes(sgq, dev, oracle, synth):
+    # Regression: one workspace serves calls of different shapes back to back
+    # (the split-K counters must stay at a shape-independent place).
+    lib = sgq.load_library()
+    shapes = [(1, 4096, 4096), (1, 4096, 11008), (3, 512, 640), (1, 11008, 4096), (16, 2048, 2048)]
+    nbytes = max(lib.sgq_linear_workspace_bytes(4, m, k, n) for m, k, n in shapes)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    assert lib.sgq_workspace_init(ws.data_ptr(), ws.numel(), stream) == 0
+    for rep in range(2):
+        for (M, K, N) in shapes:
+            W = synth.normal((K, N), 61 + K + N, 0, 0.0, 0.02)
+            x = synth.normal((M, K), 61 + K + N, 1)
+            qw = sgq.quantize_int4(_to_dev(W, dev), 128)
+            y = torch.empty((M, N), device=dev)
+            xd = _to_dev(x, dev)
+            rc = lib.sgq_linear_int4(xd.data_ptr(), M, K, N, qw.packed.data_ptr(), qw.scales.data_ptr(),
+                                     qw.devscales.data_ptr(), 128, None, y.data_ptr(), ws.data_ptr(), ws.numel(),
+                                     stream)
+            assert rc == 0
+            q, s = oracle.quantize_int4(W, 128)
+            assert rel_err(_np(y), oracle.quantized_matmul_int4(x, q, s, 128)) <= TOL, (rep, M, K, N)
+
+
 def test_nonfinite_propagates(sgq, dev):
     # A NaN activation poisons the outputs it touches, as in the reference.
     W = torch.full((32, 64), 0.01, device=dev)
