@@ -60,33 +60,73 @@ __device__ __forceinline__ float f4get(const float4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// Loads x[m][k0..k0+3] (zero past K and past M).
-template <bool KALIGN4>
-__device__ __forceinline__ float4 load_x4(const float* __restrict__ x, int m, int M, int K, int k0) {
-    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (m >= M) return r;
-    const float* p = x + (int64_t)m * K + k0;
-    if (KALIGN4) {
-        if (k0 < K) r = *(const float4*)p;
-    } else {
-        if (k0 + 0 < K) r.x = p[0];
-        if (k0 + 1 < K) r.y = p[1];
-        if (k0 + 2 < K) r.z = p[2];
-        if (k0 + 3 < K) r.w = p[3];
-    }
-    return r;
+// Raw buffer resource over [p, p + bytes): loads through it take a 32-bit
+// lane offset plus a wave-uniform SGPR offset (no per-load 64-bit address
+// math), and every dword past `bytes` reads as 0 -- which is how rows past K
+// and row quads past the strip end contribute nothing.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// Sum of v[0..H) over the lanes of an aligned group whose lane bits below O*2
-// differ.  Each step halves the values a lane carries: the lane with bit O set
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Four floats at byte offset voff + soff (zero past the end).  ALIGN4: the
+// buffer holds a multiple of four floats, so a quad is entirely in or out and
+// one 128-bit load serves; otherwise four 32-bit loads.
+template <bool ALIGN4>
+__device__ __forceinline__ float4 buf_load4f(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    if (ALIGN4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+        return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+    } else {
+        return make_float4(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 0, soff, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 4, soff, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 8, soff, 0)),
+                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 12, soff, 0)));
+    }
+}
+
+// Value of `v` held by the lane whose index differs from this lane's in bit O,
+// with VALU-latency cross-lane ops where gfx950 has them: DPP quad_perm for
+// bits 0-1, ds_swizzle (xor mode) for bits 2-3, v_permlane16/32_swap for bits
+// 4-5.  All lanes of the wavefront must be active.
+template <int O>
+__device__ __forceinline__ float xor_lane(float v, int lane) {
+    const int iv = __float_as_int(v);
+    if constexpr (O == 1) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+    } else if constexpr (O == 2) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+    } else if constexpr (O == 4 || O == 8) {
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(iv, (O << 10) | 0x1F));  // xor O within 32 lanes
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        return __int_as_float((lane & 16) ? r[0] : r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        return __int_as_float((lane & 32) ? r[0] : r[1]);
+    }
+}
+
+// Lane bits in the order the reduction consumes them: cheapest exchanges
+// first, because the first steps move the most values.
+constexpr int red_bit(int i) { return i == 0 ? 1 : i == 1 ? 2 : i == 2 ? 16 : i == 3 ? 32 : i == 4 ? 4 : 8; }
+
+// Sums v[0..H) over the LPS lanes of an aligned lane group.  While a lane
+// carries more than one value, each step halves them: the lane with bit O set
 // keeps the upper half and adds its partner's upper half, the other keeps the
-// lower half.  When one value is left the remaining steps are plain
-// butterflies.  On return v[0..H>>steps) holds totals for indices base + i.
-template <int H, int O>
-struct StripReduce {
-    static __device__ __forceinline__ void run(float* v, int lane, int& base) {
-        if constexpr (O == 0) {
-            return;
+// lower half (so every value is exchanged once).  With one value left, the
+// remaining bits are plain butterflies.  On return v[0..red_left) holds the
+// totals of indices base + i.
+template <int H, int I, int LPS>
+__device__ __forceinline__ void lane_reduce(float* v, int lane, int& base) {
+    if constexpr (I < 6) {
+        constexpr int O = red_bit(I);
+        if constexpr (O >= LPS) {
+            lane_reduce<H, I + 1, LPS>(v, lane, base);
         } else if constexpr (H > 1) {
             constexpr int h = H / 2;
             const bool upper = (lane & O) != 0;
@@ -94,48 +134,72 @@ struct StripReduce {
             for (int i = 0; i < h; ++i) {
                 const float send = upper ? v[i] : v[i + h];
                 const float keep = upper ? v[i + h] : v[i];
-                v[i] = keep + __shfl_xor(send, O);
+                v[i] = keep + xor_lane<O>(send, lane);
             }
             if (upper) base += h;
-            StripReduce<h, O / 2>::run(v, lane, base);
+            lane_reduce<h, I + 1, LPS>(v, lane, base);
         } else {
-            v[0] += __shfl_xor(v[0], O);
-            StripReduce<1, O / 2>::run(v, lane, base);
+            v[0] += xor_lane<O>(v[0], lane);
+            lane_reduce<1, I + 1, LPS>(v, lane, base);
         }
     }
-};
+}
 
-constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+// Values a lane holds after lane_reduce, and the lane bits whose lanes then
+// hold identical totals.
+constexpr int red_left(int H, int LPS) {
+    for (int i = 0; i < 6; ++i)
+        if (red_bit(i) < LPS && H > 1) H /= 2;
+    return H;
+}
+constexpr int red_dup_mask(int H, int LPS) {
+    int m = 0;
+    for (int i = 0; i < 6; ++i) {
+        if (red_bit(i) >= LPS) continue;
+        if (H > 1)
+            H /= 2;
+        else
+            m |= red_bit(i);
+    }
+    return m;
+}
 
 // ---------------------------------------------------------------------------
-// GEMV / skinny GEMM for M <= 16.  BITS 4: strips of 8 columns, scales from
-// devscales[j / spc][k]; BITS 8: strips of 4 columns, scales[0] (per-tensor)
-// or scales[k] (per-row).  Grid: ceil(NS / S) workgroups of 256 threads.
+// GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup per strip (all
+// K rows of SW columns): BITS 4 -> 8 columns, scales devscales[j / spc][k];
+// BITS 8 -> 4 columns, scales[0] (per-tensor) or scales[k] (per-row).
+// Lane l of wave w takes row quads rq = 256*it + 64*w + l.  The codes, the
+// scales and x of one row quad all sit at byte 16*rq of their buffers, so the
+// four loads share one lane offset and one SGPR iteration offset.
 // ---------------------------------------------------------------------------
-template <int BITS, int MT, int S, bool KALIGN4>
+template <int BITS, int MT, bool KALIGN4>
 __global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, int M, int K, int N,
                                                    const uint4* __restrict__ W, const float* __restrict__ SC,
-                                                   int mode, int Kpad, int RQ, int NS,
-                                                   const float* __restrict__ bias, float* __restrict__ y) {
+                                                   int mode, int Kpad, int RQ, const float* __restrict__ bias,
+                                                   float* __restrict__ y) {
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
-    constexpr int LPS = 64 / S;              // lanes per strip
-    constexpr int RQ_IT = 4 * LPS;           // row quads per strip per workgroup iteration
+    constexpr int RQ_IT = 256;               // row quads per workgroup iteration
     constexpr int V = MT * SW;               // accumulators per lane
     constexpr int U = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);  // row quads in flight per lane (register budget)
-    __shared__ float red[4][S][V];
+    constexpr bool kPreloadX = MT <= 2;
+    __shared__ float red[4][V];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sl = lane / LPS, lq = lane - sl * LPS;
-    const int j = blockIdx.x * S + sl;
-    const int jc = j < NS ? j : NS - 1;  // keep addresses in bounds; results of j >= NS are dropped
-    const uint4* __restrict__ Wj = W + (int64_t)jc * RQ;
-    const float* __restrict__ Sc = SC;
+    const int j = blockIdx.x;
+    const int voff = threadIdx.x * 16;  // (64*wave + lane) * 16
+
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)j * RQ, (uint32_t)RQ * 16u);
+    __amdgpu_buffer_rsrc_t rS;
     float s_all = 0.0f;
     if constexpr (BITS == 4) {
-        Sc = SC + (int64_t)(jc / mode) * Kpad;
+        rS = make_rsrc(SC + (int64_t)(j / mode) * Kpad, (uint32_t)Kpad * 4u);
     } else {
+        rS = make_rsrc(SC, mode ? 4u : (uint32_t)K * 4u);
         if (mode) s_all = SC[0];
     }
+    __amdgpu_buffer_rsrc_t rX[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) rX[m] = make_rsrc(x + (int64_t)m * K, m < M ? (uint32_t)K * 4u : 0u);
 
     float acc[V];
 #pragma unroll
@@ -145,45 +209,44 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, 
     for (int it0 = 0; it0 < nit; it0 += U) {
         uint4 w[U];
         float4 sv[U];
+        float4 xv[U][kPreloadX ? MT : 1];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int rq = (it0 + u) * RQ_IT + wave * LPS + lq;
-            const bool ok = rq < RQ;
-            w[u] = ok ? load_stream(Wj + rq) : make_uint4(0u, 0u, 0u, 0u);
+            const int soff = (it0 + u) * RQ_IT * 16;
+            w[u] = buf_load16(rW, voff, soff);
             if constexpr (BITS == 4) {
-                sv[u] = ok ? *(const float4*)(Sc + 4 * rq) : make_float4(0.f, 0.f, 0.f, 0.f);
-            } else {
-                const int k0 = 4 * rq;
-                if (mode) {
-                    sv[u] = make_float4(s_all, s_all, s_all, s_all);
-                } else if (k0 + 3 < K) {
-                    sv[u] = *(const float4*)(Sc + k0);
-                } else {
-                    sv[u].x = (k0 + 0 < K) ? Sc[k0 + 0] : 0.0f;
-                    sv[u].y = (k0 + 1 < K) ? Sc[k0 + 1] : 0.0f;
-                    sv[u].z = (k0 + 2 < K) ? Sc[k0 + 2] : 0.0f;
-                    sv[u].w = (k0 + 3 < K) ? Sc[k0 + 3] : 0.0f;
-                }
+                sv[u] = buf_load4f<true>(rS, voff, soff);  // devscales rows are padded to 16
+            } else if (!mode) {
+                sv[u] = buf_load4f<KALIGN4>(rS, voff, soff);
+            }
+            if constexpr (kPreloadX) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) xv[u][m] = buf_load4f<KALIGN4>(rX[m], voff, soff);
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int rq = (it0 + u) * RQ_IT + wave * LPS + lq;
-            const int k0 = 4 * rq;
+            const int k0 = 4 * ((it0 + u) * RQ_IT) + 4 * threadIdx.x;
+            if constexpr (BITS == 8) {
+                if (mode) {
+                    // Rows past K must give exactly zero, also for a non-finite per-tensor scale.
+                    sv[u].x = (k0 + 0 < K) ? s_all : 0.0f;
+                    sv[u].y = (k0 + 1 < K) ? s_all : 0.0f;
+                    sv[u].z = (k0 + 2 < K) ? s_all : 0.0f;
+                    sv[u].w = (k0 + 3 < K) ? s_all : 0.0f;
+                }
+            }
             const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const float4 xv = load_x4<KALIGN4>(x, m, M, K, k0);
+                float4 xm;
+                if constexpr (kPreloadX)
+                    xm = xv[u][m];
+                else
+                    xm = buf_load4f<KALIGN4>(rX[m], voff, (it0 + u) * RQ_IT * 16);
                 float xs[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // Rows past K contribute exactly zero: INT4 padding rows have
-                    // zero scales; INT8 ones are masked (no 0 * inf from a per-tensor scale).
-                    if constexpr (BITS == 4)
-                        xs[r] = f4get(xv, r) * f4get(sv[u], r);
-                    else
-                        xs[r] = (k0 + r < K) ? f4get(xv, r) * f4get(sv[u], r) : 0.0f;
-                }
+                for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
                 if constexpr (BITS == 4) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
@@ -205,27 +268,24 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, 
         }
     }
 
-    // Combine the LPS lanes of each strip.
+    // Combine the 64 lanes of the wavefront, then the four wavefronts.
     int base = 0;
-    StripReduce<V, LPS / 2>::run(acc, lane, base);
-    constexpr int steps_t = ilog2(LPS) < ilog2(V) ? ilog2(LPS) : ilog2(V);
-    constexpr int left = V >> steps_t;              // values a lane holds now
-    constexpr int dup_mask = (LPS >> steps_t) - 1;  // lanes holding identical totals
-    if ((lq & dup_mask) == 0) {
+    lane_reduce<V, 0, 64>(acc, lane, base);
+    constexpr int left = red_left(V, 64);
+    constexpr int dup_mask = red_dup_mask(V, 64);
+    if ((lane & dup_mask) == 0) {
 #pragma unroll
-        for (int i = 0; i < left; ++i) red[wave][sl][base + i] = acc[i];
+        for (int i = 0; i < left; ++i) red[wave][base + i] = acc[i];
     }
     __syncthreads();
 
     // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
     const float post = (BITS == 4) ? 0.0625f : 1.0f;
-    for (int o = threadIdx.x; o < S * V; o += kThreads) {
-        const int s_idx = o / V, v = o - s_idx * V;
+    for (int v = threadIdx.x; v < V; v += kThreads) {
         const int m = v / SW, e = v - m * SW;
-        const int jj = blockIdx.x * S + s_idx;
-        const int n = jj * SW + e;
-        if (jj < NS && m < M && n < N) {
-            float r = (red[0][s_idx][v] + red[1][s_idx][v]) + (red[2][s_idx][v] + red[3][s_idx][v]);
+        const int n = j * SW + e;
+        if (m < M && n < N) {
+            float r = (red[0][v] + red[1][v]) + (red[2][v] + red[3][v]);
             r = r * post;
             if (bias) r = r + bias[n];
             y[(int64_t)m * N + n] = r;
@@ -417,35 +477,16 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
 
 bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
 
-// Strips per workgroup: enough workgroups to fill the GPU, wider strips when
-// there are plenty.
-int pick_strips(int64_t NS) {
-    if (NS >= 2048) return 4;
-    if (NS >= 512) return 2;
-    return 1;
-}
-
-template <int BITS, int MT, int S>
+template <int BITS, int MT>
 hipError_t gemv_launch(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
                        int RQ, int NS, const float* bias, float* y, hipStream_t s) {
-    const dim3 grid((unsigned)ceil_div(NS, S));
-    if (x_aligned4(x, K))
-        k_gemv<BITS, MT, S, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, NS,
-                                                           bias, y);
+    const dim3 grid((unsigned)NS);
+    if (K % 4 == 0)
+        k_gemv<BITS, MT, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, bias, y);
     else
-        k_gemv<BITS, MT, S, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
-                                                            NS, bias, y);
+        k_gemv<BITS, MT, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, bias,
+                                                         y);
     return hipGetLastError();
-}
-
-template <int BITS, int MT>
-hipError_t gemv_strips(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
-                       int RQ, int NS, const float* bias, float* y, hipStream_t s) {
-    switch (pick_strips(NS)) {
-        case 4: return gemv_launch<BITS, MT, 4>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
-        case 2: return gemv_launch<BITS, MT, 2>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
-        default: return gemv_launch<BITS, MT, 1>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
-    }
 }
 
 // Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
@@ -459,13 +500,13 @@ hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, const 
         float* ym = y + m0 * N;
         hipError_t e;
         if (m <= 1)
-            e = gemv_strips<BITS, 1>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 1>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
         else if (m <= 2)
-            e = gemv_strips<BITS, 2>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 2>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
         else if (m <= 4)
-            e = gemv_strips<BITS, 4>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 4>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
         else
-            e = gemv_strips<BITS, 8>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 8>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
