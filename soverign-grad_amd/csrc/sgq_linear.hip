@@ -165,28 +165,28 @@ constexpr int red_dup_mask(int H, int LPS) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup per strip (all
-// K rows of SW columns): BITS 4 -> 8 columns, scales devscales[j / spc][k];
-// BITS 8 -> 4 columns, scales[0] (per-tensor) or scales[k] (per-row).
-// Lane l of wave w takes row quads rq = 256*it + 64*w + l.  The codes, the
+// GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup of NW
+// wavefronts per strip (all K rows of SW columns): BITS 4 -> 8 columns,
+// scales devscales[j / spc][k]; BITS 8 -> 4 columns, scales[0] (per-tensor)
+// or scales[k] (per-row).  Thread t takes row quads rq = 64*NW*it + t, U of
+// them in flight at once.  The codes, the
 // scales and x of one row quad all sit at byte 16*rq of their buffers, so the
 // four loads share one lane offset and one SGPR iteration offset.
 // ---------------------------------------------------------------------------
-template <int BITS, int MT, bool KALIGN4>
-__global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, int M, int K, int N,
-                                                   const uint4* __restrict__ W, const float* __restrict__ SC,
-                                                   int mode, int Kpad, int RQ, const float* __restrict__ bias,
-                                                   float* __restrict__ y) {
+template <int BITS, int MT, int NW, int U, bool KALIGN4>
+__global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, int M, int K, int N,
+                                                  const uint4* __restrict__ W, const float* __restrict__ SC,
+                                                  int mode, int Kpad, int RQ, const float* __restrict__ bias,
+                                                  float* __restrict__ y) {
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
-    constexpr int RQ_IT = 256;               // row quads per workgroup iteration
+    constexpr int RQ_IT = NW * 64;           // row quads per workgroup iteration
     constexpr int V = MT * SW;               // accumulators per lane
-    constexpr int U = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);  // row quads in flight per lane (register budget)
     constexpr bool kPreloadX = MT <= 2;
-    __shared__ float red[4][V];
+    __shared__ float red[NW][V];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = blockIdx.x;
-    const int voff = threadIdx.x * 16;  // (64*wave + lane) * 16
+    const int voff = threadIdx.x * 16;
 
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)j * RQ, (uint32_t)RQ * 16u);
     __amdgpu_buffer_rsrc_t rS;
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, 
         }
     }
 
-    // Combine the 64 lanes of the wavefront, then the four wavefronts.
+    // Combine the 64 lanes of each wavefront, then the NW wavefronts.
     int base = 0;
     lane_reduce<V, 0, 64>(acc, lane, base);
     constexpr int left = red_left(V, 64);
@@ -281,11 +281,13 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const float* __restrict__ x, 
 
     // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
     const float post = (BITS == 4) ? 0.0625f : 1.0f;
-    for (int v = threadIdx.x; v < V; v += kThreads) {
+    for (int v = threadIdx.x; v < V; v += NW * 64) {
         const int m = v / SW, e = v - m * SW;
         const int n = j * SW + e;
         if (m < M && n < N) {
-            float r = (red[0][v] + red[1][v]) + (red[2][v] + red[3][v]);
+            float r = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) r += red[w][v];
             r = r * post;
             if (bias) r = r + bias[n];
             y[(int64_t)m * N + n] = r;
@@ -477,16 +479,40 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
 
 bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
 
+template <int BITS, int MT, int NW, int U>
+hipError_t gemv_launch_nu(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
+                          int RQ, int NS, const float* bias, float* y, hipStream_t s) {
+    const dim3 grid((unsigned)NS);
+    if (K % 4 == 0)
+        k_gemv<BITS, MT, NW, U, true><<<grid, NW * 64, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
+                                                               bias, y);
+    else
+        k_gemv<BITS, MT, NW, U, false><<<grid, NW * 64, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
+                                                                bias, y);
+    return hipGetLastError();
+}
+
+// Wavefronts per workgroup (each workgroup owns one strip).  Measured on
+// MI355X for K in 2048..11008 and M in 1..8, 4, 8 and 16 wavefronts per strip
+// are within a few percent of each other; 4 keeps the cross-wave LDS
+// reduction short.
+constexpr int kGemvWaves = 4;
+
 template <int BITS, int MT>
 hipError_t gemv_launch(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
                        int RQ, int NS, const float* bias, float* y, hipStream_t s) {
-    const dim3 grid((unsigned)NS);
-    if (K % 4 == 0)
-        k_gemv<BITS, MT, true><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, bias, y);
-    else
-        k_gemv<BITS, MT, false><<<grid, kThreads, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ, bias,
-                                                         y);
-    return hipGetLastError();
+    // Register budget: row quads in flight per lane shrink as the batch grows.
+    constexpr int UMAX = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);
+    const int per_lane = (RQ + kGemvWaves * 64 - 1) / (kGemvWaves * 64);
+    const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
+#define SGQ_GEMV_NU(U_)                                                                                      \
+    if ((u >= U_ || U_ == 1) && U_ <= UMAX)                                                                \
+        return gemv_launch_nu<BITS, MT, kGemvWaves, U_>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
+    SGQ_GEMV_NU(4)
+    SGQ_GEMV_NU(2)
+    SGQ_GEMV_NU(1)
+#undef SGQ_GEMV_NU
+    return hipErrorInvalidValue;
 }
 
 // Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
