@@ -179,6 +179,29 @@ class Case:
         return float(np.max(np.abs(yg.astype(np.float64) - yref)) / max(np.max(np.abs(yref)), 1e-30))
 
 
+def calibration_copy(dev, mib: int = 64) -> None:
+    """One device-to-device copy of a known size (64 MiB read + 64 MiB written),
+    run before the timed region so that a `rocprofv3 --pmc FETCH_SIZE` /
+    `WRITE_SIZE` pass over this program can scale the GEMV's counter readings
+    by what the counters report for a copy of known size."""
+    import torch
+
+    a = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
+def measured_traffic(config: str):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 PMC summary for this workload (None if there is none)."""
+    path = ROOT / "profiles" / f"traffic_{config}.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+
+
 def cpu_baseline(c, budget_s: float):
     """The reference forward (dequantize + matmul + bias) on this host's cores."""
     from oracle.oracle import Oracle, Reference, reference_available
@@ -256,6 +279,7 @@ def main() -> int:
     copies = args.copies or max(1, min(64, -(-300_000_000 // nbytes)))
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; config {args.config}; steps={args.steps} "
         f"warmup={args.warmup} copies={copies}")
+    calibration_copy(dev)
     case = Case(pkg, c, dev, copies)
     ms_eager = case.time_eager(min(args.steps, 500), args.warmup)
     ms = ms_eager if args.eager else case.time_graph(args.steps, args.warmup)
@@ -268,7 +292,7 @@ def main() -> int:
     hbm_bound = c["M"] <= 4
     roofline = (
         {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config)}
         if hbm_bound else
         {"bound": "mfma", "achieved": round(tfl, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
          "frac": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}

@@ -154,6 +154,14 @@ int sgq_dequantize_int8(const void* packed, const float* scales, int scheme, int
 int sgq_dequantize_int4(const void* packed, const float* scales, int64_t K, int64_t N, int64_t group_size,
                         float* out, void* stream);
 
+/* Replaces dequantize_int8 / dequantize_int4 bit for bit from the
+ * reference-layout fp32 codes (qdata [rows*cols]): out[i] = qdata[i] * s(i),
+ * one IEEE multiply, with s(i) = scales[0] (bits 8, per-tensor),
+ * scales[i / cols] (bits 8, per-channel) or scales[i / group_size] (bits 4;
+ * group_size <= 0 means 32), following src/quantization.cpp:90-107,173-184. */
+int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, int scheme, int64_t rows,
+                         int64_t cols, int64_t group_size, float* out, void* stream);
+
 /* ---- forward ---------------------------------------------------------- */
 
 /* Replaces quantization::quantized_matmul_int8 (src/quantization.cpp:189-197)

@@ -60,6 +60,7 @@ SIGNATURES = {
     "sgq_unpack_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "sgq_dequantize_int8": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _vp]),
     "sgq_dequantize_int4": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "sgq_dequantize_codes": (_int, [_vp, _vp, _int, _int, _i64, _i64, _i64, _vp, _vp]),
     "sgq_linear_int8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp, _vp, _i64, _vp]),
     "sgq_linear_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
 }
@@ -290,6 +291,19 @@ def dequantize_int4(qx: QuantizedTensor) -> torch.Tensor:
     out = torch.empty(qx.original_shape, dtype=torch.float32, device=dev)
     _check(lib.sgq_dequantize_int4(_ptr(qx.packed), _ptr(qx.scales), qx.rows, qx.cols, qx.group_size, _ptr(out),
                                    _stream(dev)))
+    return out
+
+
+def dequantize_codes(qx: QuantizedTensor) -> torch.Tensor:
+    """dequantize_int8/int4 from the reference-layout fp32 codes (bit-exact,
+    -0.0 codes included)."""
+    lib = load_library()
+    q = _dev_f32(qx.qdata)
+    dev = q.device
+    out = torch.empty(qx.original_shape, dtype=torch.float32, device=dev)
+    branch = _int8_branch(qx) if qx.bits == 8 else 0
+    _check(lib.sgq_dequantize_codes(_ptr(q), _ptr(_dev_f32(qx.scales)), qx.bits, branch, qx.rows, qx.cols,
+                                    qx.group_size, _ptr(out), _stream(dev)))
     return out
 
 

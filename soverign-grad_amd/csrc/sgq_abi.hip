@@ -279,6 +279,27 @@ int sgq_dequantize_int4(const void* packed, const float* scales, int64_t K, int6
     return ok();
 }
 
+int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, int scheme, int64_t rows,
+                         int64_t cols, int64_t group_size, float* out, void* stream) {
+    if (bad_dims(rows, cols)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_codes: bad shape");
+    if (bits != 8 && bits != 4) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_codes: bits must be 8 or 4");
+    if (bits == 8 && scheme != SGQ_PER_TENSOR_SYMMETRIC && scheme != SGQ_PER_CHANNEL_SYMMETRIC)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_codes: bad scheme");
+    const int64_t total = rows * cols;
+    if (total == 0) return ok();
+    if (!qdata_f32 || !scales || !out) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_codes: null pointer");
+    int mode = 1;
+    int64_t div = 1;
+    if (bits == 8) {
+        mode = scheme == SGQ_PER_TENSOR_SYMMETRIC ? 0 : 1;
+        div = cols;
+    } else {
+        div = group_size <= 0 ? 32 : group_size;
+    }
+    SGQ_HIP(launch_dequant_codes(qdata_f32, scales, total, mode, div, out, (hipStream_t)stream), "dequant_codes");
+    return ok();
+}
+
 int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     int scheme, const float* bias, float* y, void* workspace, int64_t workspace_bytes,
                     void* stream) {

@@ -92,6 +92,10 @@ hipError_t launch_unpack_i4_tiled(const void* packed, int64_t K, int64_t N, int6
 hipError_t launch_unpack_i4_flat(const void* packed, int64_t total, int64_t G, const float* scales, float* out,
                                  hipStream_t s);
 
+// out[i] = q[i] * scales[idx(i)]: idx = 0 (mode 0), i / div (mode 1).
+hipError_t launch_dequant_codes(const float* q, const float* scales, int64_t total, int mode, int64_t div, float* out,
+                                hipStream_t s);
+
 // Forward kernels.
 hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, hipStream_t s);

@@ -164,6 +164,19 @@ constexpr int red_dup_mask(int H, int LPS) {
     return m;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
+// XCD b % 8), and each XCD has its own L2.  Strips that share a scale column
+// (and, for the MFMA GEMM, tiles that share operands) should run on the same
+// XCD, so the first 8*(n/8) workgroup ids are permuted to give XCD x the
+// contiguous range [x*(n/8), (x+1)*(n/8)); the remaining ids map to themselves.
+// A bijection on [0, n).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_swizzle(int b, int n) {
+    const int per = n / kXcds;
+    if (b >= per * kXcds) return b;
+    return (b % kXcds) * per + b / kXcds;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup of NW
 // wavefronts per strip (all K rows of SW columns): BITS 4 -> 8 columns,
@@ -185,7 +198,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, i
     __shared__ float red[NW][V];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int j = blockIdx.x;
+    const int j = xcd_swizzle(blockIdx.x, gridDim.x);  // strips of a scale column share an XCD's L2
     const int voff = threadIdx.x * 16;
 
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)j * RQ, (uint32_t)RQ * 16u);

@@ -269,6 +269,13 @@ __global__ void k_unpack_i4_flat(const unsigned char* __restrict__ packed, int64
     }
 }
 
+__global__ void k_dequant_codes(const float* __restrict__ q, const float* __restrict__ scales, int64_t total,
+                                int mode, int64_t div, float* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = q[i] * (mode == 0 ? scales[0] : scales[i / div]);
+}
+
 inline unsigned grid_for(int64_t n, int64_t cap = 1 << 16) {
     int64_t g = ceil_div(n, kBlock);
     if (g < 1) g = 1;
@@ -374,6 +381,13 @@ hipError_t launch_unpack_i4_flat(const void* packed, int64_t total, int64_t G, c
                                  hipStream_t s) {
     if (total <= 0) return hipSuccess;
     k_unpack_i4_flat<<<grid_for(total), kBlock, 0, s>>>((const unsigned char*)packed, total, G, scales, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_codes(const float* q, const float* scales, int64_t total, int mode, int64_t div, float* out,
+                                hipStream_t s) {
+    if (total <= 0) return hipSuccess;
+    k_dequant_codes<<<grid_for(total), kBlock, 0, s>>>(q, scales, total, mode, div, out);
     return hipGetLastError();
 }
 

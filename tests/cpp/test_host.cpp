@@ -1,0 +1,431 @@
+// test_host.cpp -- tests of the C++ host layer (soverign-grad_amd/host),
+// written against the same API the reference's test suite uses
+// (src/test_suite.cpp:672-726 for quantization).
+//
+//   test_host cpu    host-only tests (allocator, tensors, modules, file formats)
+//   test_host gpu    tests that run the gfx950 kernels through libsgq.so
+//
+// Exit status 0 when every check passes.
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <iostream>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "sovereigngrad/allocator.hpp"
+#include "sovereigngrad/nn.hpp"
+#include "sovereigngrad/quantization.hpp"
+#include "sovereigngrad/safetensors.hpp"
+#include "sovereigngrad/serialization.hpp"
+#include "sovereigngrad/tensor.hpp"
+
+using namespace sovereigngrad;
+using quantization::QuantizationScheme;
+
+static int g_failures = 0;
+
+#define CHECK(cond)                                                                          \
+    do {                                                                                     \
+        if (!(cond)) {                                                                       \
+            std::cerr << "  CHECK FAILED: " #cond " at " << __FILE__ << ":" << __LINE__ << "\n"; \
+            ++g_failures;                                                                    \
+        }                                                                                    \
+    } while (0)
+
+template <typename F>
+static bool throws(F&& f) {
+    try {
+        f();
+    } catch (const std::exception&) {
+        return true;
+    }
+    return false;
+}
+
+static std::vector<float> host(const Tensor& t) {
+    Tensor c = t.cpu();
+    return std::vector<float>(c.data(), c.data() + c.numel());
+}
+
+static bool same_bits(const std::vector<float>& a, const std::vector<float>& b) {
+    return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
+}
+
+static double rel_err(const std::vector<float>& y, const std::vector<float>& ref) {
+    double num = 0.0, den = 0.0;
+    for (size_t i = 0; i < y.size(); ++i) {
+        num = std::max(num, std::fabs((double)y[i] - (double)ref[i]));
+        den = std::max(den, std::fabs((double)ref[i]));
+    }
+    return den > 0 ? num / den : num;
+}
+
+static std::string tmp_path(const std::string& name) { return "/tmp/sgq_test_" + name; }
+
+// ---------------------------------------------------------------- host-only
+
+static void test_allocator_cpu() {
+    std::cout << "--- allocator (CPU pool)\n";
+    auto& A = MemoryAllocator::instance();
+    const size_t active0 = A.active_allocations(Device::CPU);
+    void* a = A.allocate(1000, Device::CPU);
+    void* b = A.allocate(3000, Device::CPU);
+    CHECK(a && b && a != b);
+    CHECK(((uintptr_t)a % 256) == 0 && ((uintptr_t)b % 256) == 0);
+    CHECK(A.active_allocations(Device::CPU) == active0 + 2);
+    A.free(a, Device::CPU);
+    void* c = A.allocate(900, Device::CPU);  // best fit reuses the freed 1000-byte block
+    CHECK(c == a);
+    A.free(b, Device::CPU);
+    A.free(c, Device::CPU);
+    A.free(c, Device::CPU);  // double free is ignored
+    CHECK(A.active_allocations(Device::CPU) == active0);
+    CHECK(A.total_memory_allocated(Device::CPU) >= 4096);
+    const std::string s = A.get_memory_summary(Device::CPU);
+    CHECK(s.find("CPU Memory Summary") != std::string::npos);
+    // Neighbouring free blocks merge: a freed segment is one cached block again.
+    void* p1 = A.allocate(64 << 10, Device::CPU);
+    void* p2 = A.allocate(64 << 10, Device::CPU);
+    A.free(p1, Device::CPU);
+    A.free(p2, Device::CPU);
+    void* big = A.allocate(128 << 10, Device::CPU);
+    CHECK(big != nullptr);
+    A.free(big, Device::CPU);
+    A.release_all();
+    CHECK(A.allocate(0, Device::CPU) == nullptr);
+    // An impossible host request throws instead of hanging on the allocator lock.
+    CHECK(throws([&] { A.allocate((size_t)1 << 62, Device::CPU); }));
+    CHECK(A.active_allocations(Device::CPU) == active0);
+    std::cout << "  * best fit, alignment, merge, stats, OOM error: PASSED\n";
+}
+
+static void test_tensor_basics() {
+    std::cout << "--- tensor basics\n";
+    Tensor z = Tensor::zeros({2, 3});
+    CHECK(z.numel() == 6 && z.shape() == std::vector<int64_t>({2, 3}));
+    for (float v : host(z)) CHECK(v == 0.0f);
+    Tensor a({1, 2, 3, 4, 5, 6}, {2, 3});
+    Tensor b({1, 0, 0, 1, 1, 1}, {3, 2});
+    std::vector<float> y = host(a.matmul(b));
+    CHECK(y == std::vector<float>({4, 5, 10, 11}));
+    Tensor bias({10, 20}, {1, 2});
+    CHECK(host(a.matmul(b) + bias) == std::vector<float>({14, 25, 20, 31}));
+    Tensor c = a.clone();
+    const uint64_t v0 = c.version();
+    c.copy_from(Tensor::full({2, 3}, 7.0f));
+    CHECK(c.version() == v0 + 1 && host(c)[5] == 7.0f && host(a)[5] == 6.0f);
+    CHECK(throws([&] { a.matmul(a); }));
+    CHECK(a.get_element({1, 2}) == 6.0f);
+    Tensor::manual_seed(42);
+    auto r1 = host(Tensor::randn({64}));
+    Tensor::manual_seed(42);
+    auto r2 = host(Tensor::randn({64}));
+    CHECK(same_bits(r1, r2));
+    std::cout << "  * factories, matmul, broadcast add, copy/version, seeding: PASSED\n";
+}
+
+static void test_module_state_dict() {
+    std::cout << "--- module state_dict\n";
+    nn::Linear lin(8, 4);
+    auto sd = lin.state_dict();
+    CHECK(sd.size() == 2 && sd.count("weight") && sd.count("bias"));
+    CHECK(sd["weight"].shape() == std::vector<int64_t>({8, 4}));
+    // state_dict clones: writing the clone leaves the module alone.
+    sd["bias"].copy_from(Tensor::full({1, 4}, 3.0f));
+    CHECK(host(lin.b)[0] == 0.0f);
+    nn::Linear other(8, 4);
+    other.load_state_dict(sd);
+    CHECK(same_bits(host(other.W), host(lin.W)) && host(other.b)[0] == 3.0f);
+    auto bad = sd;
+    bad["weight"] = Tensor::zeros({4, 8});
+    CHECK(throws([&] { other.load_state_dict(bad); }));
+    auto missing = sd;
+    missing.erase("bias");
+    CHECK(throws([&] { other.load_state_dict(missing, true); }));
+    other.load_state_dict(missing, false);
+    std::cout << "  * names, clones, strict shape check, missing keys: PASSED\n";
+}
+
+static void test_sgrd_format() {
+    std::cout << "--- .sgrd checkpoints\n";
+    nn::Linear lin(5, 3);
+    const std::string path = tmp_path("lin.sgrd");
+    serialization::save_module(lin, path);
+    auto sd = serialization::load_checkpoint(path);
+    CHECK(same_bits(host(sd["weight"]), host(lin.W)));
+    // Byte layout: "SGRD", u32 version 1, u32 count.
+    std::ifstream in(path, std::ios::binary);
+    char hdr[12];
+    in.read(hdr, 12);
+    uint32_t version, count;
+    std::memcpy(&version, hdr + 4, 4);
+    std::memcpy(&count, hdr + 8, 4);
+    CHECK(std::memcmp(hdr, "SGRD", 4) == 0 && version == 1 && count == 2);
+    in.close();
+    const std::string badp = tmp_path("bad.sgrd");
+    {
+        std::ofstream o(badp, std::ios::binary);
+        o.write("XXXX", 4);
+    }
+    CHECK(throws([&] { serialization::load_checkpoint(badp); }));
+    {
+        std::ofstream o(badp, std::ios::binary);
+        const uint32_t v = 7;
+        o.write("SGRD", 4);
+        o.write(reinterpret_cast<const char*>(&v), 4);
+    }
+    CHECK(throws([&] { serialization::load_checkpoint(badp); }));
+    {
+        std::ifstream src(path, std::ios::binary);
+        std::string all((std::istreambuf_iterator<char>(src)), std::istreambuf_iterator<char>());
+        std::ofstream o(badp, std::ios::binary);
+        o.write(all.data(), (std::streamsize)all.size() - 5);  // truncated payload
+    }
+    CHECK(throws([&] { serialization::load_checkpoint(badp); }));
+    std::cout << "  * round trip, header bytes, bad magic/version, truncation: PASSED\n";
+}
+
+static void test_safetensors_format() {
+    std::cout << "--- .safetensors\n";
+    nn::Linear lin(6, 2);
+    const std::string path = tmp_path("lin.safetensors");
+    safetensors::save_module(lin, path);
+    auto meta = safetensors::inspect_file(path);
+    CHECK(meta.count("weight") && meta["weight"].dtype == "F32" && meta["weight"].shape == std::vector<int64_t>({6, 2}));
+    nn::Linear other(6, 2);
+    safetensors::load_module(other, path);
+    CHECK(same_bits(host(other.W), host(lin.W)));
+    // A hand-written file with F16 / I32 payloads and metadata.
+    const std::string hp = tmp_path("mixed.safetensors");
+    {
+        std::string js =
+            "{\"__metadata__\":{\"format\":\"pt\"},\"a\":{\"dtype\":\"F16\",\"shape\":[2],\"data_offsets\":[0,4]},"
+            "\"b\":{\"dtype\":\"I32\",\"shape\":[1,2],\"data_offsets\":[4,12]}}";
+        const uint64_t len = js.size();
+        std::ofstream o(hp, std::ios::binary);
+        o.write(reinterpret_cast<const char*>(&len), 8);
+        o.write(js.data(), (std::streamsize)js.size());
+        const uint16_t h[2] = {0x3C00, 0xC100};  // 1.0, -2.5
+        const int32_t i[2] = {-7, 9};
+        o.write(reinterpret_cast<const char*>(h), 4);
+        o.write(reinterpret_cast<const char*>(i), 8);
+    }
+    auto sd = safetensors::load_file(hp);
+    CHECK(host(sd["a"]) == std::vector<float>({1.0f, -2.5f}));
+    CHECK(host(sd["b"]) == std::vector<float>({-7.0f, 9.0f}));
+    std::cout << "  * round trip, inspect, F16/I32 payloads, metadata: PASSED\n";
+}
+
+// --------------------------------------------------------------------- GPU
+
+static void test_quantization(Device dev) {
+    std::cout << "--- quantization on " << device_to_string(dev) << " (reference checks, src/test_suite.cpp:672-726)\n";
+    Tensor::manual_seed(1234);
+    {
+        Tensor x = Tensor::randn({16, 32}, 0.0f, 1.0f, dev);
+        auto q = quantization::quantize_int8(x, QuantizationScheme::PerTensorSymmetric);
+        Tensor d = quantization::dequantize_int8(q);
+        float max_err = 0.0f;
+        auto dx = host(x - d);
+        for (float e : dx) max_err = std::max(max_err, std::fabs(e));
+        CHECK(max_err < 0.05f);
+        auto qc = quantization::quantize_int8(x, QuantizationScheme::PerChannelSymmetric);
+        Tensor dc = quantization::dequantize_int8(qc);
+        CHECK(host(x - dc)[0] < 0.05f);
+        CHECK(q.qdata.device() == dev && q.scales.numel() == 1 && qc.scales.numel() == 16);
+        std::cout << "  * INT8 per-tensor (max err " << max_err << ") and per-channel: PASSED\n";
+    }
+    {
+        Tensor x = Tensor::randn({16, 32}, 0.0f, 1.0f, dev);
+        auto q4 = quantization::quantize_int4(x, 32);
+        Tensor d4 = quantization::dequantize_int4(q4);
+        CHECK(d4.shape() == x.shape());
+        CHECK(q4.scales.numel() == 16 && q4.bits == 4 && q4.group_size == 32);
+        std::cout << "  * INT4 grouped (G=32) quantization & dequantization: PASSED\n";
+    }
+    {
+        nn::Linear float_linear(32, 16, dev);
+        auto ql8 = nn::QuantizedLinear::from_float(float_linear);
+        auto ql4 = nn::QuantizedLinear4Bit::from_float(float_linear, 16);
+        Tensor input = Tensor::randn({4, 32}, 0.0f, 1.0f, dev);
+        Tensor float_out = float_linear.forward(input);
+        Tensor q8_out = ql8->forward(input);
+        Tensor q4_out = ql4->forward(input);
+        CHECK(q8_out.shape() == float_out.shape() && q4_out.shape() == float_out.shape());
+        CHECK(q8_out.device() == dev && q4_out.device() == dev);
+        const float diff8 = std::fabs(host(float_out - q8_out)[0]);
+        const float diff4 = std::fabs(host(float_out - q4_out)[0]);
+        CHECK(diff8 < 0.15f);
+        CHECK(diff4 < 0.35f);
+        std::cout << "  * QuantizedLinear INT8 (diff " << diff8 << ") and INT4 (diff " << diff4 << "): PASSED\n";
+    }
+}
+
+// The fused forward equals the reference composition dequantize -> matmul -> +bias.
+static void test_forward_matches_composition() {
+    std::cout << "--- fused forward vs dequantize + matmul + bias\n";
+    Tensor::manual_seed(7);
+    for (int bits : {8, 4}) {
+        for (int64_t M : {1, 3, 8, 17, 40}) {
+            const int64_t K = 96, N = 72;
+            Tensor W = Tensor::randn({K, N}, 0.0f, 0.02f, Device::CUDA);
+            Tensor x = Tensor::randn({M, K}, 0.0f, 1.0f, Device::CUDA);
+            Tensor b = Tensor::randn({1, N}, 0.0f, 0.02f, Device::CUDA);
+            Tensor y, ref;
+            if (bits == 8) {
+                auto q = quantization::quantize_int8(W, QuantizationScheme::PerChannelSymmetric);
+                y = quantization::quantized_matmul_int8(x, q, b);
+                ref = x.matmul(quantization::dequantize_int8(q)) + b;
+            } else {
+                auto q = quantization::quantize_int4(W, 24);
+                y = quantization::quantized_matmul_int4(x, q, b);
+                ref = x.matmul(quantization::dequantize_int4(q)) + b;
+            }
+            const double e = rel_err(host(y), host(ref));
+            CHECK(e <= 1e-5);
+        }
+    }
+    // The same weight quantized from the host and from the device gives the same bits.
+    Tensor W = Tensor::randn({33, 40}, 0.0f, 0.02f, Device::CPU);
+    auto qc = quantization::quantize_int4(W, 8);
+    auto qg = quantization::quantize_int4(W.to(Device::CUDA), 8);
+    CHECK(same_bits(host(qc.qdata), host(qg.qdata)) && same_bits(host(qc.scales), host(qg.scales)));
+    // dequantize is one IEEE multiply of the stored code and scale, -0.0 codes included.
+    auto dq = host(quantization::dequantize_int4(qc));
+    auto qh = host(qc.qdata), sh = host(qc.scales);
+    std::vector<float> expect(qh.size());
+    for (size_t i = 0; i < qh.size(); ++i) expect[i] = qh[i] * sh[i / 8];
+    CHECK(same_bits(dq, expect));
+    std::cout << "  * INT8/INT4, M in {1,3,8,17,40}, host vs device codes, dequantize bits: PASSED\n";
+}
+
+// load_state_dict / .sgrd / .safetensors rebuild the device form of the weights.
+static void test_persistence_bridge() {
+    std::cout << "--- persistence bridge\n";
+    Tensor::manual_seed(99);
+    for (Device dev : {Device::CPU, Device::CUDA}) {
+        nn::QuantizedLinear4Bit a(64, 48, 16, dev);
+        a.bias.copy_from(Tensor::randn({1, 48}, 0.0f, 0.1f));
+        Tensor x = Tensor::randn({5, 64}, 0.0f, 1.0f, dev);
+        const auto ya = host(a.forward(x));
+        const std::string p1 = tmp_path("q4.sgrd"), p2 = tmp_path("q4.safetensors");
+        serialization::save_module(a, p1);
+        safetensors::save_module(a, p2);
+        auto sd = serialization::load_checkpoint(p1);
+        CHECK(sd.count("qdata") && sd.count("scales") && sd.count("bias"));
+        for (float c : host(sd["qdata"])) CHECK(c == std::round(c) && c >= -8 && c <= 7);  // fp32 codes on disk
+        nn::QuantizedLinear4Bit b(64, 48, 16, dev);  // different random weights
+        CHECK(!same_bits(host(b.forward(x)), ya));
+        serialization::load_module(b, p1);
+        CHECK(same_bits(host(b.forward(x)), ya));
+        nn::QuantizedLinear4Bit c(64, 48, 16, dev);
+        safetensors::load_module(c, p2);
+        CHECK(same_bits(host(c.forward(x)), ya));
+        nn::QuantizedLinear d8(64, 48, dev);
+        nn::QuantizedLinear e8(64, 48, dev);
+        e8.load_state_dict(d8.state_dict());
+        CHECK(same_bits(host(e8.forward(x)), host(d8.forward(x))));
+        // Non-integer codes cannot be packed: a clear error, not a wrong answer.
+        auto broken = d8.state_dict();
+        Tensor q = broken["qdata"].cpu();
+        q.data()[0] = 0.5f;
+        broken["qdata"] = q;
+        e8.load_state_dict(broken);
+        CHECK(throws([&] { e8.forward(x); }));
+    }
+    std::cout << "  * .sgrd, .safetensors and load_state_dict repack (CPU and CUDA modules): PASSED\n";
+}
+
+static void test_module_to_device() {
+    std::cout << "--- Module::to\n";
+    Tensor::manual_seed(5);
+    nn::QuantizedLinear4Bit m(128, 64, 32, Device::CPU);
+    Tensor x = Tensor::randn({2, 128});
+    const auto y_cpu = host(m.forward(x));
+    m.to(Device::CUDA);
+    CHECK(m.q_weight.qdata.device() == Device::CUDA);
+    Tensor yg = m.forward(x.to(Device::CUDA));
+    CHECK(yg.device() == Device::CUDA && same_bits(host(yg), y_cpu));
+    std::cout << "  * parameters move, forward unchanged: PASSED\n";
+}
+
+// Data-parallel style: one module, forwards from several host threads at once
+// (include/sovereigngrad/nn.hpp:1032-1035 runs module->forward in OpenMP threads).
+static void test_concurrent_forward() {
+    std::cout << "--- concurrent forward\n";
+    Tensor::manual_seed(11);
+    nn::QuantizedLinear4Bit m(256, 128, 32, Device::CUDA);
+    std::vector<Tensor> xs;
+    std::vector<std::vector<float>> expect;
+    for (int t = 0; t < 6; ++t) {
+        xs.push_back(Tensor::randn({3, 256}, 0.0f, 1.0f, Device::CUDA));
+        expect.push_back(host(m.forward(xs.back())));
+    }
+    std::atomic<int> bad{0};
+    std::vector<std::thread> threads;
+    for (int t = 0; t < 6; ++t)
+        threads.emplace_back([&, t] {
+            for (int r = 0; r < 20; ++r)
+                if (!same_bits(host(m.forward(xs[t])), expect[t])) ++bad;
+        });
+    for (auto& th : threads) th.join();
+    CHECK(bad.load() == 0);
+    std::cout << "  * 6 threads x 20 forwards, bitwise stable: PASSED\n";
+}
+
+static void test_allocator_gpu() {
+    std::cout << "--- allocator (HIP pool)\n";
+    auto& A = MemoryAllocator::instance();
+    const size_t act0 = A.active_allocations(Device::CUDA);
+    void* a = A.allocate(100, Device::CUDA);
+    void* b = A.allocate(5000, Device::CUDA);
+    CHECK(a && b && ((uintptr_t)a % 256) == 0 && ((uintptr_t)b % 256) == 0);
+    CHECK(A.total_memory_allocated(Device::CUDA) >= (1u << 20));
+    A.free(a, Device::CUDA);
+    void* c = A.allocate(64, Device::CUDA);
+    CHECK(c == a);
+    A.free(b, Device::CUDA);
+    A.free(c, Device::CUDA);
+    CHECK(A.active_allocations(Device::CUDA) == act0);
+    CHECK(A.peak_memory_allocated(Device::CUDA) >= 5000);
+    std::cout << "  * " << A.get_memory_summary(Device::CUDA) << ": PASSED\n";
+}
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "cpu";
+    std::vector<std::pair<std::string, std::function<void()>>> tests;
+    if (mode == "cpu") {
+        tests = {{"allocator_cpu", test_allocator_cpu},
+                 {"tensor_basics", test_tensor_basics},
+                 {"module_state_dict", test_module_state_dict},
+                 {"sgrd_format", test_sgrd_format},
+                 {"safetensors_format", test_safetensors_format}};
+    } else if (mode == "gpu") {
+        tests = {{"allocator_gpu", test_allocator_gpu},
+                 {"quantization_cpu", [] { test_quantization(Device::CPU); }},
+                 {"quantization_cuda", [] { test_quantization(Device::CUDA); }},
+                 {"forward_composition", test_forward_matches_composition},
+                 {"persistence_bridge", test_persistence_bridge},
+                 {"module_to_device", test_module_to_device},
+                 {"concurrent_forward", test_concurrent_forward}};
+    } else {
+        std::cerr << "usage: test_host cpu|gpu\n";
+        return 2;
+    }
+    for (auto& t : tests) {
+        std::cout << "[test] " << t.first << std::endl;
+        try {
+            t.second();
+        } catch (const std::exception& e) {
+            std::cerr << "  EXCEPTION in " << t.first << ": " << e.what() << "\n";
+            ++g_failures;
+        }
+    }
+    std::cout << (g_failures ? "FAILED" : "ALL PASSED") << " (" << g_failures << " failed checks)" << std::endl;
+    return g_failures ? 1 : 0;
+}

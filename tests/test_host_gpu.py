@@ -1,0 +1,21 @@
+"""Runs the C++ host layer's GPU tests (tests/cpp/test_host.cpp, `gpu` mode):
+the reference's quantization checks on CPU and CUDA devices, fused forward vs
+dequantize+matmul+bias, the persistence bridge (.sgrd/.safetensors/
+load_state_dict repack), Module::to, concurrent forwards, the HIP pool."""
+import subprocess
+
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+
+BIN = helpers.PKG_DIR / "host" / "test_host"
+
+
+def test_host_layer_gpu(dev):
+    assert BIN.exists(), f"{BIN} is not built"
+    r = subprocess.run([str(BIN), "gpu"], capture_output=True, text=True, timeout=300)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "ALL PASSED" in r.stdout

@@ -41,6 +41,7 @@ def test_golden_quantize_int8(sgq, dev, golden):
             assert same_value_allow_zero_sign(_np(sgq.unpack_codes(qx)).reshape(-1), c["q"].reshape(-1))
         if "deq" in c and c["x"].size:
             assert same_value_allow_zero_sign(_np(sgq.dequantize_int8(qx)), c["deq"]), p
+            assert same_bits(_np(sgq.dequantize_codes(qx)), c["deq"]), p  # -0.0 included
         n += 1
     assert n >= 20
 
@@ -67,6 +68,7 @@ def test_golden_quantize_int4(sgq, dev, golden):
         assert same_value_allow_zero_sign(_np(sgq.unpack_codes(qx)), c["q"])
         if "deq" in c:
             assert same_value_allow_zero_sign(_np(sgq.dequantize_int4(qx)), c["deq"]), p
+            assert same_bits(_np(sgq.dequantize_codes(qx)), c["deq"]), p  # -0.0 included
 
 
 BENCH_SHAPES_INT8 = [(1024, 1024, 0), (4096, 4096, 0), (4096, 4096, 1), (2048, 6144, 1)]
