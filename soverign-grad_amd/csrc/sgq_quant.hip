@@ -85,11 +85,13 @@ __global__ void k_absmax_partial(const float* __restrict__ x, int64_t total, flo
 
 // INT8 strip-major pack: one thread per 16-byte chunk (4 columns x 4 rows).
 __global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t RQ,
-                                int64_t nchunks, const float* __restrict__ inv, int per_tensor,
+                                int64_t NS, int64_t nchunks, const float* __restrict__ inv, int per_tensor,
                                 uint4* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t j = c / RQ, rq = c - j * RQ;
+    // Consecutive threads take consecutive strips of the same rows, so the
+    // reads of x (or qdata) are coalesced; each thread writes chunk j*RQ + rq.
+    const int64_t rq = c / NS, j = c - rq * NS;
     const int64_t k0 = rq * 4;
     const int64_t n0 = j * 4;
     uint32_t dw[4];
@@ -120,18 +122,18 @@ __global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, i
         }
         dw[d] = word;
     }
-    if (packed) packed[c] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    if (packed) packed[j * RQ + rq] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
     if (badflag) atomicOr(bad, 1);
     }
 }
 
 // INT4 strip-major pack: one thread per 16-byte chunk (4 rows x 8 columns).
 __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t G,
-                                int64_t RQ, int64_t nchunks, const float* __restrict__ inv,
+                                int64_t RQ, int64_t NS, int64_t nchunks, const float* __restrict__ inv,
                                 uint4* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t rq = c / NS, j = c - rq * NS;
     const int64_t k0 = rq * 4;
     const int64_t n0 = j * 8;
     uint32_t dw[4];
@@ -140,12 +142,14 @@ __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, i
     for (int r = 0; r < 4; ++r) {
         const int64_t k = k0 + r;
         uint32_t word = 0;
+        if (k < K) {
+            // The strip layout requires N % 8 == 0 and G % 8 == 0, so the 8
+            // columns of this row of the strip lie in one group.
+            const int64_t i0 = k * N + n0;
+            const float iv = from_codes ? 0.0f : inv[i0 / G];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int64_t n = n0 + e;
-            int code = 0;
-            if (k < K && n < N) {
-                const int64_t i = k * N + n;
+            for (int e = 0; e < 8; ++e) {
+                const int64_t i = i0 + e;
                 float v;
                 if (from_codes) {
                     v = src[i];
@@ -154,16 +158,15 @@ __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, i
                         v = 0.0f;
                     }
                 } else {
-                    v = ref_code(src[i], inv[i / G], -8.0f, 7.0f);
+                    v = ref_code(src[i], iv, -8.0f, 7.0f);
                     if (qdata) qdata[i] = v;
                 }
-                code = (int)v;
+                word |= ((uint32_t)(int)v & 0xFu) << (4 * e);
             }
-            word |= ((uint32_t)code & 0xFu) << (4 * e);
         }
         dw[r] = word;
     }
-    if (packed) packed[c] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    if (packed) packed[j * RQ + rq] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
     if (badflag) atomicOr(bad, 1);
     }
 }
@@ -210,14 +213,14 @@ __global__ void k_devscales_i4(const float* __restrict__ scales, int64_t K, int6
 }
 
 __global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t RQ,
-                                  int64_t nchunks, const float* __restrict__ scales, int per_tensor,
+                                  int64_t NS, int64_t nchunks, const float* __restrict__ scales, int per_tensor,
                                   float* __restrict__ out) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t rq = c / NS, j = c - rq * NS;  // strip fastest: coalesced writes of out
     const int64_t k0 = rq * 4;
     const int64_t n0 = j * 4;
-    const uint4 w = packed[c];
+    const uint4 w = packed[j * RQ + rq];
     const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -235,25 +238,25 @@ __global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, i
 }
 
 __global__ void k_unpack_i4_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t G, int64_t RQ,
-                                  int64_t nchunks, const float* __restrict__ scales, float* __restrict__ out) {
+                                  int64_t NS, int64_t nchunks, const float* __restrict__ scales,
+                                  float* __restrict__ out) {
     for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
          c += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t j = c / RQ, rq = c - j * RQ;
+    const int64_t rq = c / NS, j = c - rq * NS;  // strip fastest: coalesced writes of out
     const int64_t k0 = rq * 4;
     const int64_t n0 = j * 8;
-    const uint4 w = packed[c];
+    const uint4 w = packed[j * RQ + rq];
     const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int64_t k = k0 + r;
+        if (k >= K) continue;
+        const int64_t i0 = k * N + n0;
+        const float s = scales ? scales[i0 / G] : 1.0f;  // one group per strip row (N % 8 == 0, G % 8 == 0)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int64_t n = n0 + e;
-            if (k < K && n < N) {
-                const int64_t i = k * N + n;
-                const float q = (float)(((int)(dw[r] << (28 - 4 * e))) >> 28);
-                out[i] = scales ? q * scales[i / G] : q;
-            }
+            const float q = (float)(((int)(dw[r] << (28 - 4 * e))) >> 28);
+            out[i0 + e] = scales ? q * s : q;
         }
     }
     }
@@ -326,7 +329,7 @@ hipError_t launch_pack_i8_tiled(const float* src, bool from_codes, int64_t K, in
     I8Geom g(K, N);
     const int64_t nchunks = g.chunks();
     if (nchunks <= 0) return hipSuccess;
-    k_pack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.RQ, nchunks, inv, per_tensor,
+    k_pack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.RQ, g.NS, nchunks, inv, per_tensor,
                                                          (uint4*)packed, qdata, bad);
     return hipGetLastError();
 }
@@ -336,7 +339,7 @@ hipError_t launch_pack_i4_tiled(const float* src, bool from_codes, int64_t K, in
     I4Geom g(K, N, G);
     const int64_t nchunks = g.chunks();
     if (nchunks <= 0) return hipSuccess;
-    k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.RQ, nchunks, inv,
+    k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.RQ, g.NS, nchunks, inv,
                                                          (uint4*)packed, qdata, bad);
     return hipGetLastError();
 }
@@ -362,7 +365,7 @@ hipError_t launch_unpack_i8_tiled(const void* packed, int64_t K, int64_t N, cons
     I8Geom g(K, N);
     const int64_t nchunks = g.chunks();
     if (nchunks <= 0 || K * N <= 0) return hipSuccess;
-    k_unpack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.RQ, nchunks, scales,
+    k_unpack_i8_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.RQ, g.NS, nchunks, scales,
                                                            per_tensor, out);
     return hipGetLastError();
 }
@@ -372,7 +375,7 @@ hipError_t launch_unpack_i4_tiled(const void* packed, int64_t K, int64_t N, int6
     I4Geom g(K, N, G);
     const int64_t nchunks = g.chunks();
     if (nchunks <= 0 || K * N <= 0) return hipSuccess;
-    k_unpack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.G, g.RQ, nchunks, scales,
+    k_unpack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.G, g.RQ, g.NS, nchunks, scales,
                                                            out);
     return hipGetLastError();
 }
