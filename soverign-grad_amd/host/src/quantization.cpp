@@ -192,8 +192,12 @@ Tensor quantized_matmul_int8(const Tensor& x, const QuantizedTensor& q_weight, c
     Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
     const int64_t M = x.shape()[0];
     Tensor y = Tensor::empty({M, v.cols}, Device::CUDA);
+    // The workspace the library asks for (none for the current kernels), from
+    // the device pool; stream order keeps a later reuse behind this launch.
+    const int64_t wsb = sgq_linear_workspace_bytes(8, M, v.rows, v.cols);
+    const std::shared_ptr<Storage> ws = wsb > 0 ? gpu_bytes(wsb) : nullptr;
     SG_SGQ_CHECK(sgq_linear_int8(xg.data(), M, v.rows, v.cols, p.codes->ptr, p.scales_dev.data(), int8_branch(q_weight),
-                                 bg.defined() ? bg.data() : nullptr, y.data(), nullptr, 0, nullptr));
+                                 bg.defined() ? bg.data() : nullptr, y.data(), ws ? ws->ptr : nullptr, wsb, nullptr));
     return to_device(y, x.device());
 }
 
@@ -205,9 +209,11 @@ Tensor quantized_matmul_int4(const Tensor& x, const QuantizedTensor& q_weight, c
     Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
     const int64_t M = x.shape()[0];
     Tensor y = Tensor::empty({M, v.cols}, Device::CUDA);
+    const int64_t wsb = sgq_linear_workspace_bytes(4, M, v.rows, v.cols);
+    const std::shared_ptr<Storage> ws = wsb > 0 ? gpu_bytes(wsb) : nullptr;
     SG_SGQ_CHECK(sgq_linear_int4(xg.data(), M, v.rows, v.cols, p.codes->ptr, p.scales_dev.data(),
                                  p.devscales.defined() ? p.devscales.data() : nullptr, q_weight.group_size,
-                                 bg.defined() ? bg.data() : nullptr, y.data(), nullptr, 0, nullptr));
+                                 bg.defined() ? bg.data() : nullptr, y.data(), ws ? ws->ptr : nullptr, wsb, nullptr));
     return to_device(y, x.device());
 }
 

@@ -51,6 +51,7 @@ def test_int4_sizes(lib, K, N, G):
 def test_workspace_sizes(lib):
     # The forward kernels need no workspace (each workgroup owns whole columns).
     assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(4, 8, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(3, 1, 4, 4) == -1
     assert lib.sgq_quantize_workspace_bytes(4, 4096, 4096, 128) >= 4096 * 4096 // 128 * 4

@@ -131,6 +131,52 @@ def test_ragged_int8(sgq, dev, oracle, synth, M, K, N, scheme):
     assert rel_err(y, yref) <= TOL
 
 
+# Small batches (2 <= M <= 16, the decode kernel's multi-row passes): K ragged
+# against the 4-row chunk and the 256-row-quad iteration, long and short K,
+# several group sizes.
+@pytest.mark.parametrize("M", [2, 4, 6, 8, 11, 16])
+@pytest.mark.parametrize("K,N,G", [(1000, 256, 128), (1001, 96, 32), (5000, 384, 64), (300, 512, 256),
+                                   (4096, 128, 128)])
+def test_small_batch_int4(sgq, dev, oracle, synth, M, K, N, G):
+    y, yref = _case(sgq, dev, oracle, synth, 4, M, K, N, G, 0, M % 2 == 0, 10)
+    assert rel_err(y, yref) <= TOL
+
+
+# INT8 strips ragged (N % 4 != 0), per-tensor and per-channel scales.
+@pytest.mark.parametrize("M", [2, 7, 13, 16])
+@pytest.mark.parametrize("K,N,scheme", [(1000, 70, 1), (4099, 30, 0), (333, 1000, 1), (64, 17, 0), (6000, 256, 1)])
+def test_small_batch_int8(sgq, dev, oracle, synth, M, K, N, scheme):
+    y, yref = _case(sgq, dev, oracle, synth, 8, M, K, N, 0, scheme, M % 2 == 1, 11)
+    assert rel_err(y, yref) <= TOL
+
+
+@pytest.mark.parametrize("bits_,M", [(4, 8), (8, 5), (4, 16), (8, 2)])
+def test_batch_rows_are_independent(sgq, dev, synth, bits_, M):
+    # Batch row r of x feeds output row r only: a NaN in x[r] poisons y[r] and
+    # nothing else.
+    W = _to_dev(synth.normal((4096, 256), 71, 0, 0.0, 0.02), dev)
+    qw = sgq.quantize_int8(W, 1) if bits_ == 8 else sgq.quantize_int4(W, 128)
+    x = _to_dev(synth.normal((M, 4096), 71, 1), dev)
+    for r in sorted({0, 2 % M, M - 1}):
+        xx = x.clone()
+        xx[r, 1234] = float("nan")
+        y = sgq.quantized_matmul(xx, qw)
+        torch.cuda.synchronize()
+        others = [i for i in range(M) if i != r]
+        assert torch.isnan(y[r]).all(), r
+        assert torch.isfinite(y[others]).all(), r
+
+
+def test_small_batch_deterministic(sgq, dev, synth):
+    # Lanes and wavefronts are summed in a fixed order: identical bits every call.
+    W = _to_dev(synth.normal((4096, 1024), 81, 0, 0.0, 0.02), dev)
+    x = _to_dev(synth.normal((8, 4096), 81, 1), dev)
+    for qw in (sgq.quantize_int4(W, 128), sgq.quantize_int8(W, 0)):
+        y1 = sgq.quantized_matmul(x, qw).clone()
+        for _ in range(3):
+            assert torch.equal(sgq.quantized_matmul(x, qw), y1)
+
+
 def test_unaligned_x_pointer(sgq, dev, oracle, synth):
     # x offset by one float: the kernels must not assume 16-byte alignment.
     W = synth.normal((64, 128), 31, 0, 0.0, 0.02)
@@ -159,7 +205,7 @@ def test_empty_shapes(sgq, dev):
 
 
 def test_deterministic_and_workspace_reuse(sgq, dev, synth):
-    # The split-K reduction sums partials in a fixed order: repeated calls give
+    # Lanes and wavefronts are summed in a fixed order: repeated calls give
     # identical bits, also after the workspace served other shapes.
     W = _to_dev(synth.normal((4096, 4096), 41, 0, 0.0, 0.02), dev)
     x = _to_dev(synth.normal((1, 4096), 41, 1), dev)
@@ -175,8 +221,8 @@ def test_deterministic_and_workspace_reuse(sgq, dev, synth):
 
 
 def test_workspace_shared_across_shapes(sgq, dev, oracle, synth):
-    # Regression: one workspace serves calls of different shapes back to back
-    # (the split-K counters must stay at a shape-independent place).
+    # One caller-owned workspace serves calls of different shapes back to back
+    # (regression: state kept in a shared workspace must not depend on the shape).
     lib = sgq.load_library()
     shapes = [(1, 4096, 4096), (1, 4096, 11008), (3, 512, 640), (1, 11008, 4096), (16, 2048, 2048)]
     nbytes = max(lib.sgq_linear_workspace_bytes(4, m, k, n) for m, k, n in shapes)
