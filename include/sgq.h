@@ -87,10 +87,13 @@ int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size);
 int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size);
 
 /* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
- * Currently 0 for every shape: each workgroup of the forward kernels owns
- * whole output columns, so no scratch memory is used; the workspace
- * arguments are reserved and may be NULL/0.  A caller that does allocate one
- * zero-fills it once (sgq_workspace_init). */
+ * Nonzero only for the GEMM (M > 16) when its grid of 128x128 output tiles
+ * is smaller than the GPU: K is then split over workgroups, whose partial
+ * tiles (KS * M * N floats) are summed by a second kernel in fixed order.
+ * 0 otherwise (the GEMV and large GEMMs own whole outputs per workgroup), and
+ * the workspace arguments may then be NULL/0.  The contents need no
+ * initialisation and are overwritten by each call; calls that overlap in
+ * time must not share one workspace.  16-byte alignment required. */
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
 
 /* Zero-fills a workspace with a kernel (no hipMemset), on `stream`. */
@@ -168,8 +171,9 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  * and with it nn::QuantizedLinear::forward (include/sovereigngrad/nn.hpp:956-958):
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
- * Dispatch: M <= 16 runs the wavefront GEMV/skinny kernel, larger M the
- * LDS-staged fp32-MFMA GEMM.  workspace: sgq_linear_workspace_bytes(8, M, K, N). */
+ * Dispatch: M <= 16 runs the wavefront GEMV, larger M the LDS-staged
+ * fp32-MFMA GEMM.  workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes,
+ * else SGQ_ERR_WORKSPACE. */
 int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     int scheme, const float* bias, float* y, void* workspace, int64_t workspace_bytes,
                     void* stream);

@@ -58,9 +58,20 @@ QuantWs quant_ws(int64_t ngroups) {
 
 int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 32 : G); }
 
-// The forward kernels need no workspace: every workgroup owns whole output
-// columns.  The workspace arguments of sgq_linear_* are reserved.
-int64_t linear_ws_bytes(int, int64_t, int64_t, int64_t) { return 0; }
+// Only the GEMM uses a workspace, for split-K partial tiles when its tile
+// grid is smaller than the GPU (see gemm_plan); the GEMV owns whole columns.
+int64_t linear_ws_bytes(int, int64_t M, int64_t K, int64_t N) {
+    return M > kGemvMaxM ? gemm_workspace_bytes(M, K, N) : 0;
+}
+
+int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void* workspace, int64_t workspace_bytes) {
+    const int64_t need = linear_ws_bytes(0, M, K, N);
+    if (need == 0) return ok();
+    if (!workspace || workspace_bytes < need)
+        return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes", fn, (long long)need);
+    if ((((uintptr_t)workspace) & 15) != 0) return fail(SGQ_ERR_WORKSPACE, "%s: workspace must be 16-byte aligned", fn);
+    return ok();
+}
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
@@ -318,12 +329,12 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
     if (!aligned16(packed) || (!per_tensor && !aligned16(scales)))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: packed and per-channel scales must be 16-byte aligned");
-    (void)workspace;
-    (void)workspace_bytes;
     if (M <= kGemvMaxM) {
         SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
-        SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemm_i8");
+        const int st = check_linear_ws("sgq_linear_int8", M, K, N, workspace, workspace_bytes);
+        if (st != SGQ_OK) return st;
+        SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, workspace, s), "gemm_i8");
     }
     return ok();
 }
@@ -350,12 +361,12 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
     if (!aligned16(packed) || !aligned16(devscales))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: packed and devscales must be 16-byte aligned");
-    (void)workspace;
-    (void)workspace_bytes;
     if (M <= kGemvMaxM) {
         SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
-        SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemm_i4");
+        const int st = check_linear_ws("sgq_linear_int4", M, K, N, workspace, workspace_bytes);
+        if (st != SGQ_OK) return st;
+        SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
     }
     return ok();
 }

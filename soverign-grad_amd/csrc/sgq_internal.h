@@ -101,10 +101,20 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
                           bool per_tensor, const float* bias, float* y, hipStream_t s);
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
+// MFMA GEMM (M > kGemvMaxM).  Grids with fewer 128x128 tiles than CUs split K
+// over workgroups; their partial tiles go to ws (gemm_workspace_bytes(M, K, N)
+// bytes, 0 when K is not split) and a second kernel adds them in fixed order.
+struct GemmPlan {
+    int KS, sps;  // splits of K, 32-row stages per split
+};
+constexpr int64_t kCus = 256;  // MI355X compute units
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N);
+int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
-                          bool per_tensor, const float* bias, float* y, hipStream_t s);
+                          bool per_tensor, const float* bias, float* y, void* ws, hipStream_t s);
 hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
-                          const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
+                          const float* devscales, const I4Geom& g, const float* bias, float* y, void* ws,
+                          hipStream_t s);
 hipError_t launch_linear_i4_flat(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                                  const float* scales, int64_t G, const float* bias, float* y, hipStream_t s);
 

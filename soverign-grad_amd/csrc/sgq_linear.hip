@@ -27,12 +27,6 @@ constexpr int kThreads = 256;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// Streaming 128-bit load of packed codes (read once; non-temporal hint).
-__device__ __forceinline__ uint4 load_stream(const uint4* p) {
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 // Byte B of w read as a signed int8 and converted to fp32: the compiler emits
 // one v_cvt_f32_i32 with an SDWA sign-extended byte select.  For INT4, a byte
 // holding a code in its high nibble and zero below reads as 16*q exactly.
@@ -49,8 +43,6 @@ __device__ __forceinline__ float i8_byte(uint32_t w, int b) {
     return b == 0 ? cvt_sbyte<0>(w) : (b == 1 ? cvt_sbyte<1>(w) : (b == 2 ? cvt_sbyte<2>(w) : cvt_sbyte<3>(w)));
 }
 
-__device__ __forceinline__ float nibble(uint32_t w, int e) { return (float)(((int)(w << (28 - 4 * e))) >> 28); }
-
 __device__ __forceinline__ float f4get(const float4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -62,6 +54,8 @@ __device__ __forceinline__ float f4get(const float4& v, int i) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
+
+constexpr int kOobOff = 0x40000000;  // a lane offset past every buffer the forward kernels read
 
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
@@ -322,17 +316,27 @@ static_assert(kBK % 16 == 0 && kBK <= 64, "stage depth is a multiple of 16");
 template <int BITS, bool KALIGN4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(const float* __restrict__ x, int M, int K, int N,
                                                    const uint4* __restrict__ W, const float* __restrict__ S,
-                                                   int mode, int Kpad, int RQ, int NS,
-                                                   const float* __restrict__ bias, float* __restrict__ y) {
+                                                   int mode, int Kpad, int RQ, int NS, int KS, int sps,
+                                                   const float* __restrict__ bias, float* __restrict__ y,
+                                                   float* __restrict__ part) {
     // mode: INT8 -> per_tensor flag; INT4 -> strips per scale column (spc).
+    // Workgroup b computes split b % KS (stages [kt0, kt1) of sps each) of
+    // tile b / KS; with KS > 1 it writes part[split][M][N] instead of y.
     __shared__ __attribute__((aligned(16))) float As[2][kBM][kLdsStride];
     __shared__ __attribute__((aligned(16))) float Bs[2][kBN][kLdsStride];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int ntn = (N + kBN - 1) / kBN;
-    const int tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
+    const int tile = blockIdx.x / KS, split = blockIdx.x - tile * KS;
+    const int tm = tile / ntn, tn = tile - tm * ntn;
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int KT = (Kpad + kBK - 1) / kBK;  // the last stage may reach past Kpad: masked below
+    const int kt0 = split * sps, kt1 = (kt0 + sps) < KT ? (kt0 + sps) : KT;
+    // Scales: INT8 per-channel scales[k] (zero past K), per-tensor scales[0];
+    // INT4 devscales[sc][Kpad].
+    const __amdgpu_buffer_rsrc_t rS =
+        make_rsrc(S, BITS == 8 ? (mode ? 4u : (uint32_t)K * 4u) : (uint32_t)(((NS + mode - 1) / mode) * Kpad) * 4u);
+    const float s_all = (BITS == 8 && mode) ? S[0] : 0.0f;
 
     constexpr int SW = (BITS == 4) ? 8 : 4;
     constexpr int KQ = kBK / 4;                 // row quads per stage
@@ -350,31 +354,38 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         float4 a[kAVec];
         uint4 b[kBPer];
     };
+    // Buffer resources over this tile's rows of x and strips of W: rows past
+    // M and strips past NS read as zero; k past K and row quads past RQ (which
+    // would read the next row or strip) get an out-of-range lane offset.
+    const int mrows = (M - m0) < kBM ? (M - m0) : kBM;
+    const int nstr = (NS - n0 / SW) < kStrips ? (NS - n0 / SW) : kStrips;
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
     auto load = [&](Regs& rg, int kt) {
+        const int soffA = kt * kBK * 4, soffB = kt * KQ * 16;
 #pragma unroll
         for (int i = 0; i < kAVec; ++i) {
             const int idx = tid + kThreads * i;
             const int row = idx / KQ, kq = idx % KQ;
-            const int m = m0 + row, k = kt * kBK + kq * 4;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m < M) {
-                const float* p = x + (int64_t)m * K + k;
-                if (KALIGN4) {
-                    if (k < K) v = *(const float4*)p;
-                } else {
-                    if (k + 0 < K) v.x = p[0];
-                    if (k + 1 < K) v.y = p[1];
-                    if (k + 2 < K) v.z = p[2];
-                    if (k + 3 < K) v.w = p[3];
-                }
+            const int k = kt * kBK + kq * 4;
+            const int vo = (row * K + kq * 4) * 4;
+            if (KALIGN4) {
+                rg.a[i] = buf_load4f<true>(rX, k < K ? vo : kOobOff, soffA);
+            } else {
+                float t[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    t[r] = __uint_as_float(
+                        __builtin_amdgcn_raw_buffer_load_b32(rX, k + r < K ? vo + 4 * r : kOobOff, soffA, 0));
+                rg.a[i] = make_float4(t[0], t[1], t[2], t[3]);
             }
-            rg.a[i] = v;
         }
 #pragma unroll
         for (int i = 0; i < kBPer; ++i) {
             const int t = tid + kThreads * i;
-            const int bj = n0 / SW + t / KQ, rq = kt * KQ + t % KQ;
-            rg.b[i] = (t < kBChunks && bj < NS && rq < RQ) ? W[(int64_t)bj * RQ + rq] : make_uint4(0u, 0u, 0u, 0u);
+            const int rq = kt * KQ + t % KQ;
+            const int vo = ((t / KQ) * RQ + t % KQ) * 16;
+            rg.b[i] = buf_load16(rW, (t < kBChunks && rq < RQ) ? vo : kOobOff, soffB);
         }
     };
     auto store = [&](const Regs& rg, int buf, int kt) {
@@ -392,33 +403,46 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             const int k = kt * kBK + kl;
             const uint32_t dw[4] = {rg.b[i].x, rg.b[i].y, rg.b[i].z, rg.b[i].w};
             if (BITS == 8) {
-                float s[4];
+                float sc[4];
+                if (mode) {
+                    // Rows past K must be exactly zero, also for a non-finite per-tensor scale.
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s[r] = mode ? S[0] : ((k + r < K) ? S[k + r] : 0.0f);
+                    for (int r = 0; r < 4; ++r) sc[r] = (k + r < K) ? s_all : 0.0f;
+                } else {
+                    const float4 s4 = buf_load4f<KALIGN4>(rS, kl * 4, kt * kBK * 4);  // zero past K
+                    sc[0] = s4.x, sc[1] = s4.y, sc[2] = s4.z, sc[3] = s4.w;
+                }
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    // Rows past K are exactly zero (no 0 * inf from a per-tensor scale).
                     float4 v;
-                    v.x = (k + 0 < K) ? i8_byte(dw[d], 0) * s[0] : 0.0f;
-                    v.y = (k + 1 < K) ? i8_byte(dw[d], 1) * s[1] : 0.0f;
-                    v.z = (k + 2 < K) ? i8_byte(dw[d], 2) * s[2] : 0.0f;
-                    v.w = (k + 3 < K) ? i8_byte(dw[d], 3) * s[3] : 0.0f;
+                    v.x = i8_byte(dw[d], 0) * sc[0];
+                    v.y = i8_byte(dw[d], 1) * sc[1];
+                    v.z = i8_byte(dw[d], 2) * sc[2];
+                    v.w = i8_byte(dw[d], 3) * sc[3];
                     *(float4*)&Bs[buf][jl * 4 + d][kl] = v;
                 }
             } else {
                 const int bj = n0 / SW + jl;
                 const int jc = bj < NS ? bj : NS - 1;
-                // devscales rows stop at Kpad; codes there are zero anyway
-                const float4 s = k < Kpad ? *(const float4*)(S + (int64_t)(jc / mode) * Kpad + k)
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+                // devscales rows stop at Kpad (codes there are zero); the
+                // 1/16 turns the 16*q read of a high nibble back into q (exact)
+                const float4 s4 = buf_load4f<true>(rS, k < Kpad ? ((jc / mode) * Kpad + kl) * 4 : kOobOff,
+                                                   kt * kBK * 4);
+                const float sc[4] = {s4.x * 0.0625f, s4.y * 0.0625f, s4.z * 0.0625f, s4.w * 0.0625f};
+                uint32_t lo[4], hi[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    float4 v;
-                    v.x = nibble(dw[0], e) * s.x;
-                    v.y = nibble(dw[1], e) * s.y;
-                    v.z = nibble(dw[2], e) * s.z;
-                    v.w = nibble(dw[3], e) * s.w;
-                    *(float4*)&Bs[buf][jl * 8 + e][kl] = v;
+                for (int r = 0; r < 4; ++r) {
+                    hi[r] = dw[r] & 0xF0F0F0F0u;         // byte c: column 2c+1 of row r, as 16*q
+                    lo[r] = (dw[r] << 4) & 0xF0F0F0F0u;  // byte c: column 2c
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    *(float4*)&Bs[buf][jl * 8 + 2 * c][kl] =
+                        make_float4(i8_byte(lo[0], c) * sc[0], i8_byte(lo[1], c) * sc[1], i8_byte(lo[2], c) * sc[2],
+                                    i8_byte(lo[3], c) * sc[3]);
+                    *(float4*)&Bs[buf][jl * 8 + 2 * c + 1][kl] =
+                        make_float4(i8_byte(hi[0], c) * sc[0], i8_byte(hi[1], c) * sc[1], i8_byte(hi[2], c) * sc[2],
+                                    i8_byte(hi[3], c) * sc[3]);
                 }
             }
         }
@@ -435,10 +459,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // the MFMAs), `fill` is free and receives the loads of stage kt+2.
     auto stage = [&](int kt, const Regs& next, Regs& fill) {
         const int buf = kt & 1;
-        if (kt + 2 < KT) load(fill, kt + 2);
+        if (kt + 2 < kt1) load(fill, kt + 2);
 #pragma unroll
         for (int sb = 0; sb < kBK / 16; ++sb) {
-            if (sb == kStoreBlock && kt + 1 < KT) store(next, buf ^ 1, kt + 1);
+            if (sb == kStoreBlock && kt + 1 < kt1) store(next, buf ^ 1, kt + 1);
             const int lk = sb * 16 + (lane >> 4) * 4;
             float4 a[4], b[4];
 #pragma unroll
@@ -458,13 +482,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     };
 
     Regs r0, r1;
-    load(r0, 0);
-    if (KT > 1) load(r1, 1);
-    store(r0, 0, 0);
+    load(r0, kt0);
+    if (kt0 + 1 < kt1) load(r1, kt0 + 1);
+    store(r0, kt0 & 1, kt0);
     __syncthreads();
-    for (int kt = 0; kt < KT; kt += 2) {
+    for (int kt = kt0; kt < kt1; kt += 2) {
         stage(kt, r1, r0);
-        if (kt + 1 < KT) stage(kt + 1, r0, r1);
+        if (kt + 1 < kt1) stage(kt + 1, r0, r1);
     }
 
     // D layout of 16x16x4: lane l, element r -> row 4*(l/16) + r, column l%16.
@@ -474,16 +498,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int j = 0; j < 4; ++j) {
             const int n = n0 + wn * 64 + j * 16 + lr;
             if (n >= N) continue;
-            const float bv = bias ? bias[n] : 0.0f;
+            const float bv = (bias && KS == 1) ? bias[n] : 0.0f;
+            float* out = KS == 1 ? y : part + (int64_t)split * M * N;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
                 if (m < M) {
                     const float v = acc[i][j][r];
-                    y[(int64_t)m * N + n] = bias ? v + bv : v;
+                    out[(int64_t)m * N + n] = (bias && KS == 1) ? v + bv : v;
                 }
             }
         }
+}
+
+// y[m][n] = sum over splits s = 0..KS-1, in that order, of part[s][m][n] (+ bias[n]).
+constexpr int kMaxSplits = 16;
+__global__ __launch_bounds__(kThreads) void k_splitk_reduce(const float* __restrict__ part, int KS, int64_t MN, int N,
+                                                            const float* __restrict__ bias, float* __restrict__ y) {
+    for (int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; o < MN; o += (int64_t)gridDim.x * blockDim.x) {
+        float t[kMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplits; ++sp) t[sp] = sp < KS ? part[sp * MN + o] : 0.0f;  // all loads first
+        float r = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplits; ++sp)
+            if (sp < KS) r += t[sp];
+        if (bias) r = r + bias[o % N];
+        y[o] = r;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -583,29 +625,62 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
     return gemv_dispatch<8>(x, M, K, N, packed, scales, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, bias, y, s);
 }
 
-hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
-                          bool per_tensor, const float* bias, float* y, hipStream_t s) {
-    I8Geom g(K, N);
-    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN)));
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N) {
+    const int64_t tiles = ceil_div(M, kBM) * ceil_div(N, kBN);
+    const int64_t KT = ceil_div(round_up(K, kPadK), kBK);
+    GemmPlan p{1, (int)KT};
+    if (tiles < kCus && KT >= 4) {
+        int64_t ks = ceil_div(2 * kCus, tiles);  // about two workgroups per CU
+        if (ks > KT / 2) ks = KT / 2;             // at least two stages per split
+        if (ks > kMaxSplits) ks = kMaxSplits;
+        if (ks > 1) {
+            p.sps = (int)ceil_div(KT, ks);
+            p.KS = (int)ceil_div(KT, p.sps);  // no split without stages
+        }
+    }
+    return p;
+}
+
+int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    const GemmPlan p = gemm_plan(M, K, N);
+    return p.KS > 1 ? (int64_t)p.KS * M * N * 4 : 0;
+}
+
+namespace {
+template <int BITS>
+hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc, int mode,
+                       int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, void* ws, hipStream_t s) {
+    const GemmPlan p = gemm_plan(M, K, N);
+    float* part = p.KS > 1 ? (float*)ws : nullptr;
+    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN) * p.KS));
     if (x_aligned4(x, K))
-        k_gemm<8, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, scales,
-                                                  per_tensor ? 1 : 0, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
+        k_gemm<BITS, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
+                                                     (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
     else
-        k_gemm<8, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, scales,
-                                                   per_tensor ? 1 : 0, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
+        k_gemm<BITS, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
+                                                      (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
+    if (p.KS > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t MN = M * N;
+        int64_t blocks = ceil_div(MN, kThreads);
+        if (blocks > 4096) blocks = 4096;
+        k_splitk_reduce<<<(unsigned)blocks, kThreads, 0, s>>>(part, p.KS, MN, (int)N, bias, y);
+    }
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                          bool per_tensor, const float* bias, float* y, void* ws, hipStream_t s) {
+    I8Geom g(K, N);
+    return gemm_launch<8>(x, M, K, N, packed, scales, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, bias, y, ws, s);
 }
 
 hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
-                          const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
-    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN)));
-    if (x_aligned4(x, K))
-        k_gemm<4, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, devscales,
-                                                  (int)g.spc, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
-    else
-        k_gemm<4, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, devscales,
-                                                   (int)g.spc, (int)g.Kpad, (int)g.RQ, (int)g.NS, bias, y);
-    return hipGetLastError();
+                          const float* devscales, const I4Geom& g, const float* bias, float* y, void* ws,
+                          hipStream_t s) {
+    return gemm_launch<4>(x, M, K, N, packed, devscales, (int)g.spc, g.Kpad, g.RQ, g.NS, bias, y, ws, s);
 }
 
 hipError_t launch_linear_i4_flat(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,

@@ -49,10 +49,14 @@ def test_int4_sizes(lib, K, N, G):
 
 
 def test_workspace_sizes(lib):
-    # The forward kernels need no workspace (each workgroup owns whole columns).
+    # The GEMV (M <= 16) and GEMMs with at least one 128x128 tile per CU need no
+    # workspace; smaller GEMM grids split K and keep KS * M * N fp32 partials.
     assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) == 0
-    assert lib.sgq_linear_workspace_bytes(4, 8, 4096, 4096) == 0
-    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(4, 16, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0  # 512 tiles
+    ws = lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)  # 8 tiles: split K
+    assert ws > 0 and ws % (128 * 1024 * 4) == 0 and 2 <= ws // (128 * 1024 * 4) <= 16
+    assert lib.sgq_linear_workspace_bytes(4, 64, 96, 512) == 0  # three 32-row stages: too short to split
     assert lib.sgq_linear_workspace_bytes(3, 1, 4, 4) == -1
     assert lib.sgq_quantize_workspace_bytes(4, 4096, 4096, 128) >= 4096 * 4096 // 128 * 4
     # Regression: K == 0 (and other degenerate shapes) must not divide by zero on the host.
@@ -75,6 +79,12 @@ def test_argument_errors_before_gpu(lib, sgq):
     assert b"aligned" in lib.sgq_last_error()
     assert lib.sgq_linear_int8(16, 1, 64, 64, 16, 20, 1, None, 16, None, 0, None) == 1  # misaligned scales
     assert lib.sgq_quantize_int4(16, 4, 64, 32, None, 16, 24, 16, None, 0, None) == 1  # misaligned packed
+    # A split-K GEMM checks its workspace before any launch.
+    need = lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)
+    assert lib.sgq_linear_int8(16, 128, 1024, 1024, 16, 16, 0, None, 16, None, 0, None) == 3
+    assert str(need).encode() in lib.sgq_last_error()
+    assert lib.sgq_linear_int8(16, 128, 1024, 1024, 16, 16, 0, None, 16, 256, need - 4, None) == 3
+    assert lib.sgq_linear_int4(16, 128, 1024, 1024, 16, 16, 16, 128, None, 16, 260, need, None) == 3  # misaligned
     # empty outputs are a no-op success
     assert lib.sgq_linear_int8(None, 0, 4, 4, None, None, 0, None, None, None, 0, None) == 0
 

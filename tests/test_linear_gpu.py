@@ -224,7 +224,8 @@ def test_workspace_shared_across_shapes(sgq, dev, oracle, synth):
     # One caller-owned workspace serves calls of different shapes back to back
     # (regression: state kept in a shared workspace must not depend on the shape).
     lib = sgq.load_library()
-    shapes = [(1, 4096, 4096), (1, 4096, 11008), (3, 512, 640), (1, 11008, 4096), (16, 2048, 2048)]
+    shapes = [(1, 4096, 4096), (1, 4096, 11008), (3, 512, 640), (1, 11008, 4096), (16, 2048, 2048),
+              (128, 1024, 1024), (40, 2048, 640), (200, 640, 256)]  # the last three split K over workgroups
     nbytes = max(lib.sgq_linear_workspace_bytes(4, m, k, n) for m, k, n in shapes)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
