@@ -52,6 +52,10 @@ CONFIGS = {
                        scheme=2, bias=False, seed=2),
     "c3_down_m16": dict(name="C3: INT4 g128 down 11008->4096, M=16", bits=4, M=16, K=11008, N=4096, G=128,
                         scheme=2, bias=False, seed=2),
+    "c3_down_m4": dict(name="C3: INT4 g128 down 11008->4096, M=4", bits=4, M=4, K=11008, N=4096, G=128,
+                       scheme=2, bias=False, seed=2),
+    "c3_down_m8": dict(name="C3: INT4 g128 down 11008->4096, M=8", bits=4, M=8, K=11008, N=4096, G=128,
+                       scheme=2, bias=False, seed=2),
     "c4": dict(name="C4: INT8 per-tensor QuantizedLinear 4096->4096, prefill M=2048", bits=8, M=2048, K=4096,
                N=4096, G=0, scheme=0, bias=False, seed=3),
 }
@@ -75,6 +79,19 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+_SYNTH_CACHE = {}
+
+
+def synth_normal(shape, seed, stream, mean, std):
+    """synth.normal, memoized: the C3 configs share their weights across M."""
+    from soverign_grad_amd import synth
+
+    key = (tuple(shape), seed, stream, mean, std)
+    if key not in _SYNTH_CACHE:
+        _SYNTH_CACHE[key] = synth.normal(shape, seed, stream, mean, std)
+    return _SYNTH_CACHE[key]
+
+
 class Case:
     """One quantized weight (with `copies` device copies), its input and output."""
 
@@ -86,9 +103,9 @@ class Case:
         self.lib = pkg.load_library()
         seed = synth.config_seed(c["seed"])
         t0 = time.time()
-        self.W = synth.normal((c["K"], c["N"]), seed, synth.STREAM_W, 0.0, 0.02)
-        self.x = synth.normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
-        self.b = synth.normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
+        self.W = synth_normal((c["K"], c["N"]), seed, synth.STREAM_W, 0.0, 0.02)
+        self.x = synth_normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
+        self.b = synth_normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
         Wd = torch.from_numpy(self.W).to(dev)
         if c["bits"] == 4:
             self.qw = pkg.quantize_int4(Wd, c["G"], keep_qdata=False)
@@ -248,6 +265,93 @@ def cpu_baseline(c, budget_s: float):
     }
 
 
+OTHER_CONFIGS = ["c1", "c3_gate_m1", "c3_gate_m4", "c3_gate_m8", "c3_gate_m16", "c3_down_m1", "c3_down_m4",
+                 "c3_down_m8", "c3_down_m16"]
+
+# every QuantizedLinear call of one NanoLLaMA decode step.
+C5_LAYERS, C5_M, C5_G = 22, 8, 128
+C5_MATS = [("qkv", 2048, 6144), ("o", 2048, 2048), ("gate", 2048, 5632), ("up", 2048, 5632), ("down", 5632, 2048)]
+
+
+def other_config(pkg, key, dev, oracle, steps):
+    """Graph-timed forward of one BASELINE config with its parity check."""
+    c = CONFIGS[key]
+    nbytes = alg_bytes(c)
+    copies = max(1, min(64, -(-300_000_000 // nbytes)))
+    case = Case(pkg, c, dev, copies)
+    ms = case.time_graph(steps, 20)
+    err = case.check(oracle)
+    del case
+    return {"workload": c["name"], "us_per_call": round(ms * 1e3, 3), "GB_s": round(nbytes / ms / 1e6, 1),
+            "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "weight_copies": copies, "rel_err_vs_oracle": err}
+
+
+def decode_step(pkg, dev, oracle, steps):
+    """C5: the 110 INT4 g128 QuantizedLinear calls of one 22-layer NanoLLaMA
+    decode step at batch M=8, in sequence, each layer on its own weight memory
+    (one seeded layer quantized once, its packed form copied per layer).  One
+    hipGraph holds `steps` decode steps."""
+    import torch
+    from soverign_grad_amd import synth
+
+    lib = pkg.load_library()
+    seed = synth.config_seed(4)
+    mats = []
+    t0 = time.time()
+    for i, (name, K, N) in enumerate(C5_MATS):
+        W = synth.normal((K, N), seed, 3 * i + synth.STREAM_W, 0.0, 0.02)
+        x = synth.normal((C5_M, K), seed, 3 * i + synth.STREAM_X, 0.0, 1.0)
+        qw = pkg.quantize_int4(torch.from_numpy(W).to(dev), C5_G)
+        layers = [(qw.packed, qw.devscales)] + [(qw.packed.clone(), qw.devscales.clone())
+                                                for _ in range(C5_LAYERS - 1)]
+        y = torch.empty((C5_M, N), dtype=torch.float32, device=dev)
+        mats.append(dict(name=name, K=K, N=N, x=x, xd=torch.from_numpy(x).to(dev), qw=qw, layers=layers, y=y))
+    torch.cuda.synchronize()
+    log(f"[bench] c5: set up {len(C5_MATS)} x {C5_LAYERS} weights in {time.time() - t0:.1f}s")
+
+    def step():
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for layer in range(C5_LAYERS):
+            for m in mats:
+                packed, ds = m["layers"][layer]
+                rc = lib.sgq_linear_int4(m["xd"].data_ptr(), C5_M, m["K"], m["N"], packed.data_ptr(),
+                                         m["qw"].scales.data_ptr(), ds.data_ptr(), C5_G, None, m["y"].data_ptr(),
+                                         None, 0, stream)
+                if rc != 0:
+                    raise RuntimeError(lib.sgq_last_error().decode())
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=torch.cuda.Stream(dev)):
+        for _ in range(steps):
+            step()
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    err = 0.0
+    for m in mats:
+        q = pkg.unpack_codes(m["qw"]).cpu().numpy()
+        sc = m["qw"].scales.cpu().numpy()
+        yref = oracle.quantized_matmul_int4(m["x"], q, sc, C5_G)
+        yg = m["y"].cpu().numpy().astype(np.float64)
+        err = max(err, float(np.max(np.abs(yg - yref)) / max(np.max(np.abs(yref)), 1e-30)))
+    nbytes = C5_LAYERS * sum(K * N // 2 + 4 * (K * N // C5_G) + 4 * C5_M * (K + N) for _, K, N in C5_MATS)
+    flops = C5_LAYERS * sum(2 * C5_M * K * N for _, K, N in C5_MATS)
+    del g, mats
+    return {"workload": "C5: NanoLLaMA decode step, 22 layers x {QKV 2048->6144, O 2048->2048, gate/up "
+                        "2048->5632, down 5632->2048}, INT4 g128, M=8 (110 calls in sequence)",
+            "us_per_step": round(ms * 1e3, 2), "us_per_call": round(ms * 1e3 / (C5_LAYERS * len(C5_MATS)), 3),
+            "GB_s": round(nbytes / ms / 1e6, 1), "TFLOP_s": round(flops / ms / 1e9, 3),
+            "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "rel_err_vs_oracle": err}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +360,7 @@ def main() -> int:
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--copies", type=int, default=0, help="rotating weight copies (default: > 256 MB)")
     ap.add_argument("--no-secondary", action="store_true", help="skip the M=2048 GEMM line")
+    ap.add_argument("--no-others", action="store_true", help="skip the C1, C3 and C5 lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
@@ -338,6 +443,23 @@ def main() -> int:
         }
         del case4
         torch.cuda.empty_cache()
+
+    if not args.no_others and args.config == "c2":
+        oracle = Oracle()
+        others = {}
+        for key in OTHER_CONFIGS:
+            others[key] = other_config(pkg, key, dev, oracle, max(20, min(400, args.steps // 5)))
+            log(f"[bench] {key}: {others[key]['us_per_call']} us/call, {others[key]['GB_s']} GB/s, "
+                f"{others[key]['TFLOP_s']} TFLOP/s, rel_err {others[key]['rel_err_vs_oracle']:.2e}")
+            if others[key]["rel_err_vs_oracle"] > 1e-5:
+                raise SystemExit(f"parity failure in bench ({key})")
+            torch.cuda.empty_cache()
+        others["c5"] = decode_step(pkg, dev, oracle, max(2, min(20, args.steps // 100)))
+        log(f"[bench] c5: {others['c5']['us_per_step']} us/step, rel_err {others['c5']['rel_err_vs_oracle']:.2e}")
+        if others["c5"]["rel_err_vs_oracle"] > 1e-5:
+            raise SystemExit("parity failure in bench (c5)")
+        torch.cuda.empty_cache()
+        out["other_configs"] = others
 
     if not args.no_cpu:
         t0 = time.time()
