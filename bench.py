@@ -286,11 +286,77 @@ def other_config(pkg, key, dev, oracle, steps):
             "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "weight_copies": copies, "rel_err_vs_oracle": err}
 
 
-def decode_step(pkg, dev, oracle, steps):
+def _graph_ms(dev, body, steps):
+    """`steps` calls of body(i) captured into one hipGraph; ms per call of one timed replay."""
+    import torch
+
+    for i in range(3):
+        body(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=torch.cuda.Stream(dev)):
+        for i in range(steps):
+            body(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    del g
+    return ms
+
+
+def swiglu_pair(pkg, dev, oracle, steps, M):
+    """C3's gate and up projections (INT4 g128 4096->11008) as one gated-MLP
+    call h = silu(x.Wg) * (x.Wu), graph-timed over rotating weight copies, with
+    its parity check against the oracle."""
+    import torch
+    from soverign_grad_amd import synth
+
+    lib = pkg.load_library()
+    K, N, G = 4096, 11008, 128
+    seed = synth.config_seed(2)
+    x = synth_normal((M, K), seed, synth.STREAM_X, 0.0, 1.0)
+    W = [synth_normal((K, N), seed, synth.STREAM_W, 0.0, 0.02), synth_normal((K, N), seed, synth.STREAM_W2, 0.0, 0.02)]
+    qw = [pkg.quantize_int4(torch.from_numpy(w).to(dev), G) for w in W]
+    nbytes = 2 * (K * N // 2 + 4 * (K * N // G)) + 4 * M * (K + N)
+    copies = max(1, min(64, -(-300_000_000 // nbytes)))
+    sets = [[(q.packed, q.devscales) for q in qw]]
+    sets += [[(q.packed.clone(), q.devscales.clone()) for q in qw] for _ in range(copies - 1)]
+    xd = torch.from_numpy(x).to(dev)
+    h = torch.empty((M, N), dtype=torch.float32, device=dev)
+    nws = lib.sgq_swiglu_workspace_bytes(4, M, K, N, G)
+    ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        (pg, dg), (pu, du) = sets[i % copies]
+        rc = lib.sgq_swiglu_int4(xd.data_ptr(), M, K, N, pg.data_ptr(), qw[0].scales.data_ptr(), dg.data_ptr(), None,
+                                 pu.data_ptr(), qw[1].scales.data_ptr(), du.data_ptr(), None, G, h.data_ptr(),
+                                 ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+        if rc != 0:
+            raise RuntimeError(lib.sgq_last_error().decode())
+
+    ms = _graph_ms(dev, call, steps)
+    q = [pkg.unpack_codes(w).cpu().numpy() for w in qw]
+    sc = [w.scales.cpu().numpy() for w in qw]
+    href = oracle.swiglu_int4(x, q[0], sc[0], q[1], sc[1], G)
+    hg = h.cpu().numpy().astype(np.float64)
+    err = float(np.max(np.abs(hg - href)) / max(np.max(np.abs(href)), 1e-30))
+    del sets, qw
+    return {"workload": f"C3: INT4 g128 gate+up 4096->11008 fused (silu(x.Wg) * x.Wu), M={M}",
+            "us_per_call": round(ms * 1e3, 3), "GB_s": round(nbytes / ms / 1e6, 1),
+            "TFLOP_s": round(2 * 2 * M * K * N / ms / 1e9, 3), "weight_copies": copies, "rel_err_vs_oracle": err}
+
+
+def decode_step(pkg, dev, oracle, steps, fused=False):
     """C5: the 110 INT4 g128 QuantizedLinear calls of one 22-layer NanoLLaMA
     decode step at batch M=8, in sequence, each layer on its own weight memory
     (one seeded layer quantized once, its packed form copied per layer).  One
-    hipGraph holds `steps` decode steps."""
+    hipGraph holds `steps` decode steps.  fused: each layer's gate and up
+    projections run as one gated-MLP call on the gate's input (88 calls)."""
     import torch
     from soverign_grad_amd import synth
 
@@ -309,45 +375,61 @@ def decode_step(pkg, dev, oracle, steps):
     torch.cuda.synchronize()
     log(f"[bench] c5: set up {len(C5_MATS)} x {C5_LAYERS} weights in {time.time() - t0:.1f}s")
 
-    def step():
+    by = {m["name"]: m for m in mats}
+    gate, up = by["gate"], by["up"]
+    nws = lib.sgq_swiglu_workspace_bytes(4, C5_M, gate["K"], gate["N"], C5_G)
+    assert nws == 0  # M=8: the one-launch GEMV
+    h = torch.empty((C5_M, gate["N"]), dtype=torch.float32, device=dev)
+
+    def linear(m, layer, stream):
+        packed, ds = m["layers"][layer]
+        rc = lib.sgq_linear_int4(m["xd"].data_ptr(), C5_M, m["K"], m["N"], packed.data_ptr(),
+                                 m["qw"].scales.data_ptr(), ds.data_ptr(), C5_G, None, m["y"].data_ptr(),
+                                 None, 0, stream)
+        if rc != 0:
+            raise RuntimeError(lib.sgq_last_error().decode())
+
+    def step(_i):
         stream = torch.cuda.current_stream(dev).cuda_stream
         for layer in range(C5_LAYERS):
             for m in mats:
-                packed, ds = m["layers"][layer]
-                rc = lib.sgq_linear_int4(m["xd"].data_ptr(), C5_M, m["K"], m["N"], packed.data_ptr(),
-                                         m["qw"].scales.data_ptr(), ds.data_ptr(), C5_G, None, m["y"].data_ptr(),
-                                         None, 0, stream)
-                if rc != 0:
-                    raise RuntimeError(lib.sgq_last_error().decode())
+                if fused and m is up:
+                    continue
+                if fused and m is gate:
+                    (pg, dg), (pu, du) = gate["layers"][layer], up["layers"][layer]
+                    rc = lib.sgq_swiglu_int4(gate["xd"].data_ptr(), C5_M, gate["K"], gate["N"], pg.data_ptr(),
+                                             gate["qw"].scales.data_ptr(), dg.data_ptr(), None, pu.data_ptr(),
+                                             up["qw"].scales.data_ptr(), du.data_ptr(), None, C5_G, h.data_ptr(),
+                                             None, 0, stream)
+                    if rc != 0:
+                        raise RuntimeError(lib.sgq_last_error().decode())
+                    continue
+                linear(m, layer, stream)
 
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=torch.cuda.Stream(dev)):
-        for _ in range(steps):
-            step()
-    g.replay()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    g.replay()
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / steps
+    ms = _graph_ms(dev, step, steps)
     err = 0.0
+    unp = {m["name"]: (pkg.unpack_codes(m["qw"]).cpu().numpy(), m["qw"].scales.cpu().numpy()) for m in mats}
     for m in mats:
-        q = pkg.unpack_codes(m["qw"]).cpu().numpy()
-        sc = m["qw"].scales.cpu().numpy()
+        if fused and m["name"] in ("gate", "up"):
+            continue
+        q, sc = unp[m["name"]]
         yref = oracle.quantized_matmul_int4(m["x"], q, sc, C5_G)
         yg = m["y"].cpu().numpy().astype(np.float64)
         err = max(err, float(np.max(np.abs(yg - yref)) / max(np.max(np.abs(yref)), 1e-30)))
-    nbytes = C5_LAYERS * sum(K * N // 2 + 4 * (K * N // C5_G) + 4 * C5_M * (K + N) for _, K, N in C5_MATS)
+    if fused:
+        href = oracle.swiglu_int4(gate["x"], *unp["gate"], *unp["up"], C5_G)
+        hg = h.cpu().numpy().astype(np.float64)
+        err = max(err, float(np.max(np.abs(hg - href)) / max(np.max(np.abs(href)), 1e-30)))
+    # Gate and up read one input and write one output when fused.
+    io = 4 * C5_M * (gate["K"] + gate["N"]) if fused else 0
+    nbytes = C5_LAYERS * (sum(K * N // 2 + 4 * (K * N // C5_G) + 4 * C5_M * (K + N) for _, K, N in C5_MATS) - io)
     flops = C5_LAYERS * sum(2 * C5_M * K * N for _, K, N in C5_MATS)
-    del g, mats
-    return {"workload": "C5: NanoLLaMA decode step, 22 layers x {QKV 2048->6144, O 2048->2048, gate/up "
-                        "2048->5632, down 5632->2048}, INT4 g128, M=8 (110 calls in sequence)",
-            "us_per_step": round(ms * 1e3, 2), "us_per_call": round(ms * 1e3 / (C5_LAYERS * len(C5_MATS)), 3),
+    calls = C5_LAYERS * (len(C5_MATS) - (1 if fused else 0))
+    del mats, by, gate, up
+    desc = ("C5: NanoLLaMA decode step, 22 layers x {QKV 2048->6144, O 2048->2048, gate/up 2048->5632, down "
+            "5632->2048}, INT4 g128, M=8 ")
+    desc += "(gate+up as one gated-MLP call: 88 calls in sequence)" if fused else "(110 calls in sequence)"
+    return {"workload": desc, "us_per_step": round(ms * 1e3, 2), "us_per_call": round(ms * 1e3 / calls, 3),
             "GB_s": round(nbytes / ms / 1e6, 1), "TFLOP_s": round(flops / ms / 1e9, 3),
             "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "rel_err_vs_oracle": err}
 
@@ -454,11 +536,20 @@ def main() -> int:
             if others[key]["rel_err_vs_oracle"] > 1e-5:
                 raise SystemExit(f"parity failure in bench ({key})")
             torch.cuda.empty_cache()
-        others["c5"] = decode_step(pkg, dev, oracle, max(2, min(20, args.steps // 100)))
-        log(f"[bench] c5: {others['c5']['us_per_step']} us/step, rel_err {others['c5']['rel_err_vs_oracle']:.2e}")
-        if others["c5"]["rel_err_vs_oracle"] > 1e-5:
-            raise SystemExit("parity failure in bench (c5)")
-        torch.cuda.empty_cache()
+        for M in (1, 8):
+            key = f"c3_swiglu_m{M}"
+            others[key] = swiglu_pair(pkg, dev, oracle, max(20, min(400, args.steps // 5)), M)
+            log(f"[bench] {key}: {others[key]['us_per_call']} us/call, {others[key]['GB_s']} GB/s, "
+                f"rel_err {others[key]['rel_err_vs_oracle']:.2e}")
+            if others[key]["rel_err_vs_oracle"] > 1e-5:
+                raise SystemExit(f"parity failure in bench ({key})")
+            torch.cuda.empty_cache()
+        for key, fused in (("c5", False), ("c5_fused_swiglu", True)):
+            others[key] = decode_step(pkg, dev, oracle, max(2, min(20, args.steps // 100)), fused)
+            log(f"[bench] {key}: {others[key]['us_per_step']} us/step, rel_err {others[key]['rel_err_vs_oracle']:.2e}")
+            if others[key]["rel_err_vs_oracle"] > 1e-5:
+                raise SystemExit(f"parity failure in bench ({key})")
+            torch.cuda.empty_cache()
         out["other_configs"] = others
 
     if not args.no_cpu:

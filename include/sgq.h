@@ -186,6 +186,30 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
                     const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* ---- gated MLP (caller-side fusion) ----------------------------------- */
+
+/* Replaces the first three lines of nn::SwiGLU::forward
+ * (include/sovereigngrad/nn.hpp:151-154) with quantized gate and up
+ * projections:
+ *   h[M,N] = silu(x . Wg + bias_gate) * (x . Wu + bias_up)
+ * silu(v) = v / (1 + exp(-v)) as Tensor::silu (src/ops.cpp:561-575,
+ * include/sovereigngrad/simd.hpp:103-108), * as mul (src/ops.cpp:239-253).
+ * The two weights share K, N, scheme / group_size.  M <= 16 with the tiled
+ * layout runs both GEMVs in one launch (x read once per strip pair, no
+ * intermediate in HBM); otherwise two projections (GEMM or flat INT4) and an
+ * elementwise kernel.  Biases may be NULL.  workspace:
+ * sgq_swiglu_workspace_bytes(bits, M, K, N, group_size) bytes (group_size is
+ * ignored for bits 8), else SGQ_ERR_WORKSPACE. */
+int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size);
+int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_gate,
+                    const float* scales_gate, const float* bias_gate, const void* packed_up, const float* scales_up,
+                    const float* bias_up, int scheme, float* h, void* workspace, int64_t workspace_bytes,
+                    void* stream);
+int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_gate,
+                    const float* scales_gate, const float* devscales_gate, const float* bias_gate,
+                    const void* packed_up, const float* scales_up, const float* devscales_up, const float* bias_up,
+                    int64_t group_size, float* h, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

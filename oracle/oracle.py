@@ -52,6 +52,10 @@ class Oracle:
         L.oracle_quantized_matmul_int8.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp]
         L.oracle_quantized_matmul_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp]
         L.oracle_matmul_f64.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64]
+        L.oracle_silu.argtypes = [_vp, _i64, _vp]
+        L.oracle_mul.argtypes = [_vp, _vp, _i64, _vp]
+        L.oracle_swiglu_int8.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
+        L.oracle_swiglu_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]
 
     # quantize_int8: per-tensor for scheme 0 or rank < 2 (src/quantization.cpp:22)
     def quantize_int8(self, x: np.ndarray, scheme: int) -> Tuple[np.ndarray, np.ndarray]:
@@ -111,6 +115,38 @@ class Oracle:
                                               _p(b), _p(out))
         return out
 
+    def silu(self, x) -> np.ndarray:
+        x = _f32(x)
+        out = np.empty_like(x)
+        self.lib.oracle_silu(_p(x), x.size, _p(out))
+        return out
+
+    def mul(self, a, b) -> np.ndarray:
+        a, b = _f32(a), _f32(b)
+        out = np.empty_like(a)
+        self.lib.oracle_mul(_p(a), _p(b), a.size, _p(out))
+        return out
+
+    def swiglu_int8(self, x, qg, sg, qu, su, scheme: int, bias_gate=None, bias_up=None) -> np.ndarray:
+        """silu(x . deq(Wg) + bg) * (x . deq(Wu) + bu), nn.hpp:151-154 on quantized weights."""
+        x, qg, sg, qu, su = _f32(x), _f32(qg), _f32(sg), _f32(qu), _f32(su)
+        out = np.empty((x.shape[0], qg.shape[1]), np.float32)
+        bg = None if bias_gate is None else _f32(bias_gate).reshape(-1)
+        bu = None if bias_up is None else _f32(bias_up).reshape(-1)
+        per_tensor = 1 if (scheme == 0 or sg.size == 1) else 0
+        self.lib.oracle_swiglu_int8(_p(x), x.shape[0], x.shape[1], qg.shape[1], _p(qg), _p(sg), _p(bg), _p(qu),
+                                    _p(su), _p(bu), per_tensor, _p(out))
+        return out
+
+    def swiglu_int4(self, x, qg, sg, qu, su, group_size: int, bias_gate=None, bias_up=None) -> np.ndarray:
+        x, qg, sg, qu, su = _f32(x), _f32(qg), _f32(sg), _f32(qu), _f32(su)
+        out = np.empty((x.shape[0], qg.shape[1]), np.float32)
+        bg = None if bias_gate is None else _f32(bias_gate).reshape(-1)
+        bu = None if bias_up is None else _f32(bias_up).reshape(-1)
+        self.lib.oracle_swiglu_int4(_p(x), x.shape[0], x.shape[1], qg.shape[1], _p(qg), _p(sg), _p(bg), _p(qu),
+                                    _p(su), _p(bu), group_size, _p(out))
+        return out
+
     def matmul_f64(self, a: np.ndarray, b: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
         a, b = _f32(a), _f32(b)
         c = np.empty((a.shape[0], b.shape[1]), np.float64)
@@ -138,6 +174,8 @@ class Reference:
         L.ref_time_quantized_matmul.argtypes = [_int, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _int, _i64, _vp, _int,
                                                 ctypes.POINTER(_dbl), _vp]
         L.ref_omp_max_threads.restype = _int
+        L.ref_silu.argtypes = [_vp, _i64, _vp]
+        L.ref_mul.argtypes = [_vp, _vp, _i64, _vp]
 
     @staticmethod
     def _rc(x: np.ndarray):
@@ -220,6 +258,20 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference forward raised")
         return list(secs), out
+
+    def silu(self, x):
+        x = _f32(x)
+        out = np.empty_like(x)
+        if self.lib.ref_silu(_p(x), x.size, _p(out)) != 0:
+            raise RuntimeError("reference silu raised")
+        return out
+
+    def mul(self, a, b):
+        a, b = _f32(a), _f32(b)
+        out = np.empty_like(a)
+        if self.lib.ref_mul(_p(a), _p(b), a.size, _p(out)) != 0:
+            raise RuntimeError("reference mul raised")
+        return out
 
     def omp_max_threads(self) -> int:
         return int(self.lib.ref_omp_max_threads())

@@ -14,6 +14,8 @@
 //   ref_quantized_matmul_int8 quantization::quantized_matmul_int8 (src/quantization.cpp:189-197)
 //   ref_quantized_matmul_int4 quantization::quantized_matmul_int4 (src/quantization.cpp:199-206)
 //   ref_matmul                matmul (src/ops.cpp:378-455)
+//   ref_silu                  silu   (src/ops.cpp:561-575)
+//   ref_mul                   mul    (src/ops.cpp:239-253)
 #include "sovereigngrad/quantization.hpp"
 #include "sovereigngrad/ops.hpp"
 
@@ -171,6 +173,24 @@ int ref_time_quantized_matmul(int bits, const float* x, int64_t M, int64_t K, in
             secs[r] = std::chrono::duration<double>(t1 - t0).count();
         }
         if (out) to_host(y, out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_silu(const float* x, int64_t n, float* out) {
+    try {
+        to_host(silu(from_host(x, {n})), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_mul(const float* a, const float* b, int64_t n, float* out) {
+    try {
+        to_host(mul(from_host(a, {n}), from_host(b, {n})), out);
         return 0;
     } catch (const std::exception&) {
         return -1;

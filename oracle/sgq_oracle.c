@@ -18,6 +18,13 @@
  *   oracle_add_row_bias               src/ops.cpp:132-171
  *   oracle_quantized_matmul_int8      src/quantization.cpp:189-197
  *   oracle_quantized_matmul_int4      src/quantization.cpp:199-206
+ *   oracle_silu                       src/ops.cpp:561-575 with
+ *                                     include/sovereigngrad/simd.hpp:103-108
+ *   oracle_mul                        src/ops.cpp:239-253 with
+ *                                     include/sovereigngrad/simd.hpp:31-44
+ *   oracle_swiglu_int8 / _int4        include/sovereigngrad/nn.hpp:151-154 (the
+ *                                     gate/up half of SwiGLU::forward) on
+ *                                     quantized weights
  *
  * Floating-point contract.  The reference is built with GCC -O3 -mavx2 -mfma
  * in gnu++17 mode, where -ffp-contract=fast is the default, so every
@@ -210,6 +217,56 @@ void oracle_quantized_matmul_int4(const float* x, int64_t M, int64_t K, int64_t 
     oracle_matmul(x, w, out, M, K, N);
     if (bias) oracle_add_row_bias(out, bias, M, N);
     free(w);
+}
+
+/* simd::vec_silu (simd.hpp:103-108), the CPU branch of silu (ops.cpp:561-575):
+ * x / (1 + exp(-x)) with std::exp on float, i.e. libm's expf, one element at a
+ * time (the loop calls a library function, so GCC keeps it scalar). */
+void oracle_silu(const float* x, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        out[i] = v / (1.0f + expf(-v));
+    }
+}
+
+/* mul (ops.cpp:239-253) for equal contiguous shapes: simd::vec_mul
+ * (simd.hpp:31-44), one IEEE multiply per element. */
+void oracle_mul(const float* a, const float* b, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] * b[i];
+}
+
+/* SwiGLU::forward up to the down projection (nn.hpp:151-154):
+ *   gate = silu(w_gate(x)); up = w_up(x); hidden = gate * up
+ * with both projections quantized linears (bias may be NULL). */
+static void swiglu_finish(float* gate, const float* up, int64_t n, float* out) {
+    oracle_silu(gate, n, gate);
+    oracle_mul(gate, up, n, out);
+}
+
+void oracle_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const float* qg, const float* sg,
+                        const float* bg, const float* qu, const float* su, const float* bu, int per_tensor,
+                        float* out) {
+    const size_t n = (size_t)(M * N > 0 ? M * N : 1);
+    float* gate = (float*)malloc(n * sizeof(float));
+    float* up = (float*)malloc(n * sizeof(float));
+    oracle_quantized_matmul_int8(x, M, K, N, qg, sg, per_tensor, bg, gate);
+    oracle_quantized_matmul_int8(x, M, K, N, qu, su, per_tensor, bu, up);
+    swiglu_finish(gate, up, M * N, out);
+    free(gate);
+    free(up);
+}
+
+void oracle_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const float* qg, const float* sg,
+                        const float* bg, const float* qu, const float* su, const float* bu, int64_t group_size,
+                        float* out) {
+    const size_t n = (size_t)(M * N > 0 ? M * N : 1);
+    float* gate = (float*)malloc(n * sizeof(float));
+    float* up = (float*)malloc(n * sizeof(float));
+    oracle_quantized_matmul_int4(x, M, K, N, qg, sg, group_size, bg, gate);
+    oracle_quantized_matmul_int4(x, M, K, N, qu, su, group_size, bu, up);
+    swiglu_finish(gate, up, M * N, out);
+    free(gate);
+    free(up);
 }
 
 /* fp64 reference dot products for tolerance pinning: out[m,n] = sum_k x[m,k]*w[k,n]

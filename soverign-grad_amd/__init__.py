@@ -63,6 +63,10 @@ SIGNATURES = {
     "sgq_dequantize_codes": (_int, [_vp, _vp, _int, _int, _i64, _i64, _i64, _vp, _vp]),
     "sgq_linear_int8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp, _vp, _i64, _vp]),
     "sgq_linear_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "sgq_swiglu_workspace_bytes": (_i64, [_int, _i64, _i64, _i64, _i64]),
+    "sgq_swiglu_int8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp, _vp, _i64, _vp]),
+    "sgq_swiglu_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,
+                               _vp]),
 }
 
 _lib = None
@@ -121,8 +125,9 @@ def _dev_f32(t: torch.Tensor) -> torch.Tensor:
 
 
 class _Workspaces:
-    """One zero-initialised linear workspace per (device, stream, thread), for
-    the sizes sgq_linear_workspace_bytes asks for (currently none)."""
+    """One zero-initialised workspace per (device, stream, thread), grown to the
+    largest size sgq_linear_workspace_bytes / sgq_swiglu_workspace_bytes has
+    asked for on it (split-K partials, the gated MLP's up projection)."""
 
     def __init__(self):
         self._local = threading.local()
@@ -346,6 +351,37 @@ def quantized_matmul_int4(x: torch.Tensor, qw: QuantizedTensor, bias: Optional[t
     _check(lib.sgq_linear_int4(_ptr(x), M, K, N, _ptr(qw.packed), _ptr(qw.scales), _ptr(qw.devscales),
                                qw.group_size, _ptr(b), _ptr(y), ws, nws, _stream(dev)))
     return y
+
+
+def quantized_swiglu(x: torch.Tensor, w_gate: QuantizedTensor, w_up: QuantizedTensor,
+                     bias_gate: Optional[torch.Tensor] = None, bias_up: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """silu(x . w_gate + bias_gate) * (x . w_up + bias_up): the gated half of
+    SwiGLU::forward (include/sovereigngrad/nn.hpp:151-154) with quantized
+    projections, in one library call."""
+    lib = load_library()
+    if w_gate.bits != w_up.bits or (w_gate.rows, w_gate.cols) != (w_up.rows, w_up.cols):
+        raise ValueError("gate and up weights must have the same shape and bit width")
+    if w_gate.bits == 8 and _int8_branch(w_gate) != _int8_branch(w_up):
+        raise ValueError("gate and up weights must use the same INT8 scheme")
+    if w_gate.bits == 4 and w_gate.group_size != w_up.group_size:
+        raise ValueError("gate and up weights must use the same group size")
+    x, K, N, bg = _linear_args(x, w_gate, bias_gate)
+    _, _, _, bu = _linear_args(x, w_up, bias_up)
+    M = x.shape[0]
+    dev = x.device
+    h = out if out is not None else torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws, nws = _linear_ws.get(lib.sgq_swiglu_workspace_bytes(w_gate.bits, M, K, N, w_gate.group_size), dev)
+    if w_gate.bits == 8:
+        _check(lib.sgq_swiglu_int8(_ptr(x), M, K, N, _ptr(w_gate.packed), _ptr(w_gate.scales), _ptr(bg),
+                                   _ptr(w_up.packed), _ptr(w_up.scales), _ptr(bu), _int8_branch(w_gate), _ptr(h),
+                                   ws, nws, _stream(dev)))
+    else:
+        _check(lib.sgq_swiglu_int4(_ptr(x), M, K, N, _ptr(w_gate.packed), _ptr(w_gate.scales),
+                                   _ptr(w_gate.devscales), _ptr(bg), _ptr(w_up.packed), _ptr(w_up.scales),
+                                   _ptr(w_up.devscales), _ptr(bu), w_gate.group_size, _ptr(h), ws, nws,
+                                   _stream(dev)))
+    return h
 
 
 def quantized_matmul(x: torch.Tensor, qw: QuantizedTensor, bias: Optional[torch.Tensor] = None,

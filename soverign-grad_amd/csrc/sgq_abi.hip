@@ -73,6 +73,15 @@ int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void*
     return ok();
 }
 
+// Gated MLP workspace: nothing for the one-launch GEMV; otherwise
+// [up projection: M*N floats, 256-byte aligned][split-K partials of either GEMM].
+// The flat INT4 layout always takes the two-projection form.
+int64_t swiglu_ws_bytes(bool flat, int64_t M, int64_t K, int64_t N) {
+    if (!flat && M <= kGemvMaxM && K > 0) return 0;
+    const int64_t split = (!flat && M > kGemvMaxM) ? gemm_workspace_bytes(M, K, N) : 0;
+    return align_up(M * N * 4) + split;
+}
+
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 bool bad_dims(int64_t a, int64_t b) { return a < 0 || b < 0 || a > kMaxDim || b > kMaxDim || a * b > ((int64_t)1 << 40); }
@@ -131,6 +140,12 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N) {
     if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4)) return -1;
     return linear_ws_bytes(bits, M, K, N);
+}
+
+int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size) {
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N) || (bits != 8 && bits != 4)) return -1;
+    if (M == 0 || N == 0) return 0;
+    return swiglu_ws_bytes(bits == 4 && !I4Geom(K, N, group_size).tiled, M, K, N);
 }
 
 int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
@@ -368,6 +383,91 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         if (st != SGQ_OK) return st;
         SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
     }
+    return ok();
+}
+
+int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_gate,
+                    const float* scales_gate, const float* bias_gate, const void* packed_up, const float* scales_up,
+                    const float* bias_up, int scheme, float* h, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    const char* fn = "sgq_swiglu_int8";
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad shape", fn);
+    if (scheme != SGQ_PER_TENSOR_SYMMETRIC && scheme != SGQ_PER_CHANNEL_SYMMETRIC)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad scheme", fn);
+    if (M == 0 || N == 0) return ok();
+    if (!h) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null output", fn);
+    const int64_t need = swiglu_ws_bytes(false, M, K, N);
+    if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+        return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes, 16-byte aligned", fn, (long long)need);
+    float* u = (float*)workspace;
+    if (K == 0) {  // both projections are their biases
+        SGQ_HIP(launch_fill_bias(h, M, N, bias_gate, s), "fill_bias");
+        SGQ_HIP(launch_fill_bias(u, M, N, bias_up, s), "fill_bias");
+        SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+        return ok();
+    }
+    if (!x || !packed_gate || !scales_gate || !packed_up || !scales_up)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
+    if (!aligned16(packed_gate) || !aligned16(packed_up) ||
+        (!per_tensor && (!aligned16(scales_gate) || !aligned16(scales_up))))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and per-channel scales must be 16-byte aligned", fn);
+    if (M <= kGemvMaxM) {
+        SGQ_HIP(launch_swiglu_gemv_i8(x, M, K, N, packed_gate, scales_gate, bias_gate, packed_up, scales_up, bias_up,
+                                      per_tensor, h, s),
+                "swiglu_gemv_i8");
+        return ok();
+    }
+    void* split = (char*)workspace + align_up(M * N * 4);
+    SGQ_HIP(launch_gemm_i8(x, M, K, N, packed_gate, scales_gate, per_tensor, bias_gate, h, split, s), "gemm_i8");
+    SGQ_HIP(launch_gemm_i8(x, M, K, N, packed_up, scales_up, per_tensor, bias_up, u, split, s), "gemm_i8");
+    SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+    return ok();
+}
+
+int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_gate,
+                    const float* scales_gate, const float* devscales_gate, const float* bias_gate,
+                    const void* packed_up, const float* scales_up, const float* devscales_up, const float* bias_up,
+                    int64_t group_size, float* h, void* workspace, int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    const char* fn = "sgq_swiglu_int4";
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad shape", fn);
+    if (M == 0 || N == 0) return ok();
+    if (!h) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null output", fn);
+    const I4Geom g(K, N, group_size);
+    const int64_t need = swiglu_ws_bytes(!g.tiled, M, K, N);
+    if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+        return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes, 16-byte aligned", fn, (long long)need);
+    float* u = (float*)workspace;
+    if (K == 0) {
+        SGQ_HIP(launch_fill_bias(h, M, N, bias_gate, s), "fill_bias");
+        SGQ_HIP(launch_fill_bias(u, M, N, bias_up, s), "fill_bias");
+        SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+        return ok();
+    }
+    if (!x || !packed_gate || !packed_up) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    if (!g.tiled) {
+        if (!scales_gate || !scales_up) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: flat layout needs scales", fn);
+        SGQ_HIP(launch_linear_i4_flat(x, M, K, N, packed_gate, scales_gate, g.G, bias_gate, h, s), "linear_i4_flat");
+        SGQ_HIP(launch_linear_i4_flat(x, M, K, N, packed_up, scales_up, g.G, bias_up, u, s), "linear_i4_flat");
+        SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+        return ok();
+    }
+    if (!devscales_gate || !devscales_up)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: tiled layout needs devscales", fn);
+    if (!aligned16(packed_gate) || !aligned16(packed_up) || !aligned16(devscales_gate) || !aligned16(devscales_up))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
+    if (M <= kGemvMaxM) {
+        SGQ_HIP(launch_swiglu_gemv_i4(x, M, K, N, packed_gate, devscales_gate, bias_gate, packed_up, devscales_up,
+                                      bias_up, g, h, s),
+                "swiglu_gemv_i4");
+        return ok();
+    }
+    void* split = (char*)workspace + align_up(M * N * 4);
+    SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_gate, devscales_gate, g, bias_gate, h, split, s), "gemm_i4");
+    SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_up, devscales_up, g, bias_up, u, split, s), "gemm_i4");
+    SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
     return ok();
 }
 

@@ -118,4 +118,17 @@ hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const
 hipError_t launch_linear_i4_flat(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                                  const float* scales, int64_t G, const float* bias, float* y, hipStream_t s);
 
+// Gated MLP: h = silu(x*Wg + bg) * (x*Wu + bu).  The GEMV form (M <= kGemvMaxM)
+// runs both weights in one launch; larger batches run two projections and
+// launch_silu_mul (h = silu(h) * u, elementwise over n floats).
+hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
+                                 const float* scales_g, const float* bias_g, const void* packed_u,
+                                 const float* scales_u, const float* bias_u, bool per_tensor, float* h,
+                                 hipStream_t s);
+hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
+                                 const float* devscales_g, const float* bias_g, const void* packed_u,
+                                 const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
+                                 hipStream_t s);
+hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s);
+
 }  // namespace sgq

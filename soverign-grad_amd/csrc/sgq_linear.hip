@@ -170,6 +170,11 @@ constexpr int red_dup_mask(int H) {
     return m;
 }
 
+// silu(v) = v / (1 + exp(-v)), as simd::vec_silu (simd.hpp:103-108); the
+// device expf differs from libm's by at most a few ulp, the division is
+// correctly rounded.
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
+
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
 // XCD b % 8), and each XCD has its own L2.  Strips that share a scale column
 // (and, for the MFMA GEMM, tiles that share operands) should run on the same
@@ -192,28 +197,39 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
 // scales and x of one row quad all sit at byte 16*rq of their buffers, so the
 // four loads share one lane offset and one SGPR iteration offset.
 // ---------------------------------------------------------------------------
-template <int BITS, int MT, int NW, int U, bool KALIGN4>
-__global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, int M, int K, int N,
-                                                  const uint4* __restrict__ W, const float* __restrict__ SC,
-                                                  int mode, int Kpad, int RQ, const float* __restrict__ bias,
-                                                  float* __restrict__ y) {
+//
+// NG == 2 is the gated MLP (SwiGLU::forward up to the down projection,
+// include/sovereigngrad/nn.hpp:151-154): the workgroup runs NW wavefronts on
+// strip j of the gate weight and NW on strip j of the up weight -- x is read
+// by both groups from the same CU's caches -- and the epilogue writes
+// silu(gate + bias) * (up + bias2).
+template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG>
+__global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__ x, int M, int K, int N,
+                                                       const uint4* __restrict__ W, const float* __restrict__ SC,
+                                                       const uint4* __restrict__ W2, const float* __restrict__ SC2,
+                                                       int mode, int Kpad, int RQ, const float* __restrict__ bias,
+                                                       const float* __restrict__ bias2, float* __restrict__ y) {
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
-    constexpr int RQ_IT = NW * 64;           // row quads per workgroup iteration
+    constexpr int RQ_IT = NW * 64;           // row quads per group iteration
     constexpr int V = MT * SW;               // accumulators per lane
-    __shared__ float red[NW][V];
+    __shared__ float red[NG * NW][V];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
+    const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
     const int j = xcd_swizzle(blockIdx.x, gridDim.x);  // strips of a scale column share an XCD's L2
-    const int voff = threadIdx.x * 16;
+    const int voff = gtid * 16;
+    const uint4* __restrict__ Wm = grp ? W2 : W;
+    const float* __restrict__ SCm = grp ? SC2 : SC;
 
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)j * RQ, (uint32_t)RQ * 16u);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wm + (int64_t)j * RQ, (uint32_t)RQ * 16u);
     __amdgpu_buffer_rsrc_t rS;
     float s_all = 0.0f;
     if constexpr (BITS == 4) {
-        rS = make_rsrc(SC + (int64_t)(j / mode) * Kpad, (uint32_t)Kpad * 4u);
+        rS = make_rsrc(SCm + (int64_t)(j / mode) * Kpad, (uint32_t)Kpad * 4u);
     } else {
-        rS = make_rsrc(SC, mode ? 4u : (uint32_t)K * 4u);
-        if (mode) s_all = SC[0];
+        rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
+        if (mode) s_all = SCm[0];
     }
     __amdgpu_buffer_rsrc_t rX[MT];
 #pragma unroll
@@ -242,7 +258,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, i
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int k0 = 4 * ((it0 + u) * RQ_IT) + 4 * threadIdx.x;
+            const int k0 = 4 * ((it0 + u) * RQ_IT) + 4 * gtid;
             if constexpr (BITS == 8) {
                 if (mode) {
                     // Rows past K must give exactly zero, also for a non-finite per-tensor scale.
@@ -293,7 +309,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, i
 
     // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
     const float post = (BITS == 4) ? 0.0625f : 1.0f;
-    for (int v = threadIdx.x; v < V; v += NW * 64) {
+    for (int v = threadIdx.x; v < V; v += NG * NW * 64) {
         const int m = v / SW, e = v - m * SW;
         const int n = j * SW + e;
         if (m < M && n < N) {
@@ -302,6 +318,14 @@ __global__ __launch_bounds__(NW * 64) void k_gemv(const float* __restrict__ x, i
             for (int w = 0; w < NW; ++w) r += red[w][v];
             r = r * post;
             if (bias) r = r + bias[n];
+            if constexpr (NG == 2) {
+                float r2 = 0.0f;
+#pragma unroll
+                for (int w = NW; w < 2 * NW; ++w) r2 += red[w][v];
+                r2 = r2 * post;
+                if (bias2) r2 = r2 + bias2[n];
+                r = silu_f32(r) * r2;
+            }
             y[(int64_t)m * N + n] = r;
         }
     }
@@ -528,6 +552,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 }
 
+// h[i] = silu(h[i]) * u[i]: the gated MLP's elementwise tail after two
+// separate projections (mul of equal shapes is one multiply, ops.cpp:239-253).
+__global__ __launch_bounds__(kThreads) void k_silu_mul(float* __restrict__ h, const float* __restrict__ u, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        h[i] = silu_f32(h[i]) * u[i];
+}
+
 // y[m][n] = sum over splits s = 0..KS-1, in that order, of part[s][m][n] (+ bias[n]).
 constexpr int kMaxSplits = 16;
 __global__ __launch_bounds__(kThreads) void k_splitk_reduce(const float* __restrict__ part, int KS, int64_t MN, int N,
@@ -570,35 +601,44 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
 
 bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
 
-template <int BITS, int MT, int NW, int U>
-hipError_t gemv_launch_nu(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
-                          int RQ, int NS, const float* bias, float* y, hipStream_t s) {
+// One weight operand of the GEMV: packed codes, scales in the kernel's mode, bias.
+struct GemvWeight {
+    const void* packed;
+    const float* sc;
+    const float* bias;
+};
+
+template <int BITS, int MT, int NW, int U, int NG>
+hipError_t gemv_launch_nu(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad,
+                          int RQ, int NS, float* y, hipStream_t s) {
     const dim3 grid((unsigned)NS);
     if (K % 4 == 0)
-        k_gemv<BITS, MT, NW, U, true><<<grid, NW * 64, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
-                                                               bias, y);
+        k_gemv<BITS, MT, NW, U, true, NG><<<grid, NG * NW * 64, 0, s>>>(
+            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, w.bias, w2.bias,
+            y);
     else
-        k_gemv<BITS, MT, NW, U, false><<<grid, NW * 64, 0, s>>>(x, M, K, N, (const uint4*)packed, sc, mode, Kpad, RQ,
-                                                                bias, y);
+        k_gemv<BITS, MT, NW, U, false, NG><<<grid, NG * NW * 64, 0, s>>>(
+            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, w.bias, w2.bias,
+            y);
     return hipGetLastError();
 }
 
-// Wavefronts per workgroup (each workgroup owns one strip).  Measured on
-// MI355X for K in 2048..11008 and M in 1..8, 4, 8 and 16 wavefronts per strip
-// are within a few percent of each other; 4 keeps the cross-wave LDS
-// reduction short.
+// Wavefronts per workgroup and weight (each workgroup owns one strip).
+// Measured on MI355X for K in 2048..11008 and M in 1..8, 4, 8 and 16
+// wavefronts per strip are within a few percent of each other; 4 keeps the
+// cross-wave LDS reduction short.
 constexpr int kGemvWaves = 4;
 
-template <int BITS, int MT>
-hipError_t gemv_launch(const float* x, int M, int K, int N, const void* packed, const float* sc, int mode, int Kpad,
-                       int RQ, int NS, const float* bias, float* y, hipStream_t s) {
+template <int BITS, int MT, int NG>
+hipError_t gemv_launch(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad, int RQ,
+                       int NS, float* y, hipStream_t s) {
     // Register budget: row quads in flight per lane shrink as the batch grows.
     constexpr int UMAX = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);
     const int per_lane = (RQ + kGemvWaves * 64 - 1) / (kGemvWaves * 64);
     const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
 #define SGQ_GEMV_NU(U_)                                                                                      \
     if ((u >= U_ || U_ == 1) && U_ <= UMAX)                                                                \
-        return gemv_launch_nu<BITS, MT, kGemvWaves, U_>(x, M, K, N, packed, sc, mode, Kpad, RQ, NS, bias, y, s);
+        return gemv_launch_nu<BITS, MT, kGemvWaves, U_, NG>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
     SGQ_GEMV_NU(4)
     SGQ_GEMV_NU(2)
     SGQ_GEMV_NU(1)
@@ -607,9 +647,9 @@ hipError_t gemv_launch(const float* x, int M, int K, int N, const void* packed, 
 }
 
 // Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
-template <int BITS>
-hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc,
-                         int mode, int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, hipStream_t s) {
+template <int BITS, int NG>
+hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, GemvWeight w, GemvWeight w2, int mode,
+                         int64_t Kpad, int64_t RQ, int64_t NS, float* y, hipStream_t s) {
     const int k = (int)K, n = (int)N, kp = (int)Kpad, rq = (int)RQ, ns = (int)NS;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int m = (int)((M - m0) < 8 ? (M - m0) : 8);
@@ -617,13 +657,13 @@ hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, const 
         float* ym = y + m0 * N;
         hipError_t e;
         if (m <= 1)
-            e = gemv_launch<BITS, 1>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 1, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
         else if (m <= 2)
-            e = gemv_launch<BITS, 2>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 2, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
         else if (m <= 4)
-            e = gemv_launch<BITS, 4>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 4, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
         else
-            e = gemv_launch<BITS, 8>(xm, m, k, n, packed, sc, mode, kp, rq, ns, bias, ym, s);
+            e = gemv_launch<BITS, 8, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -633,13 +673,40 @@ hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, const 
 
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
-    return gemv_dispatch<4>(x, M, K, N, packed, devscales, (int)g.spc, g.Kpad, g.RQ, g.NS, bias, y, s);
+    const GemvWeight w{packed, devscales, bias};
+    return gemv_dispatch<4, 1>(x, M, K, N, w, w, (int)g.spc, g.Kpad, g.RQ, g.NS, y, s);
 }
 
 hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, hipStream_t s) {
     I8Geom g(K, N);
-    return gemv_dispatch<8>(x, M, K, N, packed, scales, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, bias, y, s);
+    const GemvWeight w{packed, scales, bias};
+    return gemv_dispatch<8, 1>(x, M, K, N, w, w, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, y, s);
+}
+
+hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
+                                 const float* devscales_g, const float* bias_g, const void* packed_u,
+                                 const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
+                                 hipStream_t s) {
+    return gemv_dispatch<4, 2>(x, M, K, N, GemvWeight{packed_g, devscales_g, bias_g},
+                               GemvWeight{packed_u, devscales_u, bias_u}, (int)g.spc, g.Kpad, g.RQ, g.NS, h, s);
+}
+
+hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
+                                 const float* scales_g, const float* bias_g, const void* packed_u,
+                                 const float* scales_u, const float* bias_u, bool per_tensor, float* h,
+                                 hipStream_t s) {
+    I8Geom g(K, N);
+    return gemv_dispatch<8, 2>(x, M, K, N, GemvWeight{packed_g, scales_g, bias_g},
+                               GemvWeight{packed_u, scales_u, bias_u}, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, h, s);
+}
+
+hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int64_t blocks = ceil_div(n, kThreads);
+    if (blocks > 4096) blocks = 4096;
+    k_silu_mul<<<(unsigned)blocks, kThreads, 0, s>>>(h, u, n);
+    return hipGetLastError();
 }
 
 GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N) {

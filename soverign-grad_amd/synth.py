@@ -7,13 +7,15 @@ float32.  The reference's own Tensor::randn is unseeded
 (src/tensor.cpp:136-153) and is never used for parity data.
 
 Seeds follow the benchmark plan: 0x5EED0000 + config index, with sub-streams
-STREAM_W, STREAM_X and STREAM_BIAS for weights, activations and bias.
+STREAM_W, STREAM_X and STREAM_BIAS for weights, activations and bias, and
+STREAM_W2 / STREAM_BIAS2 for the second (up) projection of a gated MLP.
 """
 from __future__ import annotations
 
 import numpy as np
 
 STREAM_W, STREAM_X, STREAM_BIAS = 0, 1, 2
+STREAM_W2, STREAM_BIAS2 = 3, 4
 BASE_SEED = 0x5EED0000
 
 _M1 = np.uint64(0xBF58476D1CE4E5B9)

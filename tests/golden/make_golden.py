@@ -6,7 +6,8 @@ by `make -C oracle ref` from the reference's own sources):
     python tests/golden/make_golden.py
 
 Every expected output comes from the reference's own functions
-(quantization::quantize_int8/_int4, dequantize_*, quantized_matmul_*; see
+(quantization::quantize_int8/_int4, dequantize_*, quantized_matmul_*, and
+silu / mul composed as SwiGLU::forward composes them; see
 oracle/ref_shim.cpp).  Inputs are seeded (soverign-grad_amd/synth.py) or
 hand-built special values.  The fixtures are data only: inputs and the
 reference's outputs.
@@ -125,6 +126,37 @@ def main() -> None:
         if b is not None:
             t["bias"] = b
         add("linear_int4", {"M": M, "K": K, "N": N, "group_size": g}, **t)
+
+    # ---- silu and the gated MLP half of SwiGLU (nn.hpp:151-154) ------------
+    sx = np.array([0.0, -0.0, 1.0, -1.0, 0.5, -0.5, 3.0, -3.0, 10.0, -10.0, 20.0, -20.0, 88.0, -88.0, 89.0, -89.0,
+                   104.0, -104.0, 1e-30, -1e-30, 1e-40, -1e-40, np.inf, -np.inf, np.nan, 1e30, -1e30],
+                  dtype=np.float32)
+    sx = np.concatenate([sx, x_of((64,), 0, 4.0)])
+    add("silu", {"n": int(sx.size)}, x=sx, y=ref.silu(sx))
+    for (M, K, N, bits, gs, with_bias) in [(1, 64, 32, 4, 32, True), (5, 96, 40, 4, 8, False),
+                                           (8, 128, 64, 4, 128, True), (20, 64, 48, 4, 16, True),
+                                           (3, 64, 36, 8, 0, True), (17, 40, 24, 8, 1, False)]:
+        xx = x_of((M, K), 1)
+        Wg, Wu = x_of((K, N), 0, 0.05), x_of((K, N), 0, 0.05)
+        bg = x_of((1, N), 2, 0.5) if with_bias else None
+        bu = x_of((1, N), 2, 0.5) if with_bias else None
+        if bits == 4:
+            qg, sg = ref.quantize_int4(Wg, gs)
+            qu, su = ref.quantize_int4(Wu, gs)
+            g = ref.quantized_matmul_int4(xx, qg, sg, gs, bg)
+            u = ref.quantized_matmul_int4(xx, qu, su, gs, bu)
+            params = {"M": M, "K": K, "N": N, "group_size": gs}
+        else:
+            qg, sg = ref.quantize_int8(Wg, gs)
+            qu, su = ref.quantize_int8(Wu, gs)
+            g = ref.quantized_matmul_int8(xx, qg, sg, gs, bg)
+            u = ref.quantized_matmul_int8(xx, qu, su, gs, bu)
+            params = {"M": M, "K": K, "N": N, "scheme": gs}
+        h = ref.mul(ref.silu(g), u)
+        t = dict(x=xx, qg=qg, sg=sg, qu=qu, su=su, y=h)
+        if bg is not None:
+            t["bias_gate"], t["bias_up"] = bg, bu
+        add(f"swiglu_int{bits}", params, **t)
 
     np.savez_compressed(OUT_NPZ, **arrays)
     OUT_JSON.write_text(json.dumps({"generator": "tests/golden/make_golden.py", "cases": cases}, indent=1))

@@ -65,6 +65,40 @@ def test_workspace_sizes(lib):
             assert lib.sgq_linear_workspace_bytes(bits_, M, K, N) >= 0
 
 
+def test_swiglu_workspace_sizes(lib):
+    # One-launch GEMV (tiled, M <= 16): none.  Otherwise the up projection
+    # (M*N floats, 256-byte aligned) followed by the GEMM's split-K partials.
+    assert lib.sgq_swiglu_workspace_bytes(4, 1, 4096, 11008, 128) == 0
+    assert lib.sgq_swiglu_workspace_bytes(8, 16, 1024, 1024, 0) == 0
+    assert lib.sgq_swiglu_workspace_bytes(4, 2048, 4096, 4096, 128) == 2048 * 4096 * 4
+    u = 128 * 1024 * 4
+    assert lib.sgq_swiglu_workspace_bytes(8, 128, 1024, 1024, 0) == u + lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)
+    assert lib.sgq_swiglu_workspace_bytes(4, 3, 60, 50, 7) == 768  # flat INT4: always two projections
+    assert lib.sgq_swiglu_workspace_bytes(8, 3, 0, 5, 0) == 256  # K == 0: bias-only projections
+    assert lib.sgq_swiglu_workspace_bytes(8, 0, 64, 64, 0) == 0
+    assert lib.sgq_swiglu_workspace_bytes(5, 1, 4, 4, 0) == -1
+
+
+def test_swiglu_argument_errors_before_gpu(lib):
+    # int8: bad scheme, missing pointers, misalignment, missing workspace
+    assert lib.sgq_swiglu_int8(16, 1, 64, 64, 16, 16, None, 16, 16, None, 7, 16, None, 0, None) == 1
+    assert lib.sgq_swiglu_int8(16, 1, 64, 64, 16, 16, None, None, 16, None, 0, 16, None, 0, None) == 1
+    assert lib.sgq_swiglu_int8(16, 1, 64, 64, 16, 16, None, 24, 16, None, 0, 16, None, 0, None) == 1
+    assert b"aligned" in lib.sgq_last_error()
+    need = lib.sgq_swiglu_workspace_bytes(8, 32, 64, 64, 0)
+    assert lib.sgq_swiglu_int8(16, 32, 64, 64, 16, 16, None, 16, 16, None, 0, 16, None, 0, None) == 3
+    assert str(need).encode() in lib.sgq_last_error()
+    assert lib.sgq_swiglu_int8(16, 32, 64, 64, 16, 16, None, 16, 16, None, 0, 16, 16, need - 4, None) == 3
+    # int4: tiled layout needs devscales; flat layout needs scales and a workspace even for M = 1
+    assert lib.sgq_swiglu_int4(16, 1, 64, 64, 16, 16, None, None, 16, 16, 16, None, 32, 16, None, 0, None) == 1
+    assert b"devscales" in lib.sgq_last_error()
+    assert lib.sgq_swiglu_int4(16, 1, 60, 50, 16, 16, None, None, 16, 16, None, None, 7, 16, None, 0, None) == 3
+    assert lib.sgq_swiglu_int4(16, 1, 60, 50, 16, None, None, None, 16, 16, None, None, 7, 16, 16, 256, None) == 1
+    assert b"scales" in lib.sgq_last_error()
+    assert lib.sgq_swiglu_int4(None, -1, 64, 64, None, None, None, None, None, None, None, None, 32, None, None, 0,
+                               None) == 1
+
+
 def test_argument_errors_before_gpu(lib, sgq):
     # Each of these fails validation on the host; nothing reaches the GPU.
     assert lib.sgq_quantize_int8(None, -1, 4, 0, None, None, None, None, 0, None) == 1

@@ -198,3 +198,68 @@ def test_bias_broadcast(oracle, synth):
     y0 = oracle.quantized_matmul_int8(x, q, s, 1)
     y1 = oracle.quantized_matmul_int8(x, q, s, 1, b)
     assert same_bits(y1, (y0 + b).astype(np.float32))
+
+
+# ---- silu and the gated MLP (SwiGLU::forward, nn.hpp:151-154) -------------
+
+def test_golden_silu_and_swiglu(oracle, golden):
+    kinds = {"silu": 0, "swiglu_int4": 0, "swiglu_int8": 0}
+    for c in golden:
+        k = c["kind"]
+        if k == "silu":
+            y = oracle.silu(c["x"])
+        elif k == "swiglu_int4":
+            y = oracle.swiglu_int4(c["x"], c["qg"], c["sg"], c["qu"], c["su"], c["params"]["group_size"],
+                                   c.get("bias_gate"), c.get("bias_up"))
+        elif k == "swiglu_int8":
+            y = oracle.swiglu_int8(c["x"], c["qg"], c["sg"], c["qu"], c["su"], c["params"]["scheme"],
+                                   c.get("bias_gate"), c.get("bias_up"))
+        else:
+            continue
+        assert same_bits(y, c["y"]), (k, c["params"])  # same libm expf, same products
+        kinds[k] += 1
+    assert kinds["silu"] >= 1 and kinds["swiglu_int4"] >= 4 and kinds["swiglu_int8"] >= 2
+
+
+def test_reference_live_silu(oracle, ref, synth):
+    x = synth.normal((4096,), 91, 0, 0.0, 8.0)
+    assert same_bits(oracle.silu(x), ref.silu(x))
+    y = synth.normal((4096,), 92, 0)
+    assert same_bits(oracle.mul(x, y), ref.mul(x, y))
+
+
+def test_silu_closed_forms(oracle):
+    # silu(x) - silu(-x) = x (x*s(x) + x*s(-x) = x since s(x) + s(-x) = 1),
+    # saturation to x and to -0, the value at 0 and the known global minimum
+    # (about -0.27846 at x about -1.27846).
+    x = np.linspace(-30, 30, 6001, dtype=np.float32)
+    s, sm = oracle.silu(x).astype(np.float64), oracle.silu(-x).astype(np.float64)
+    assert np.all(np.abs((s - sm) - x) <= 4 * np.spacing(np.abs(x).astype(np.float32)) + 1e-7)
+    big = np.array([50.0, 100.0, 1e6], np.float32)
+    assert np.array_equal(oracle.silu(big), big)
+    # exp(-x) overflows fp32 past x = 88.7: x / inf = -0; before that the tail is x * e^x
+    tiny = oracle.silu(-big[1:])
+    assert np.all(tiny == 0.0) and np.all(np.signbit(tiny))
+    assert abs(float(oracle.silu(np.array([-50.0], np.float32))[0]) / (-50.0 * math.exp(-50.0)) - 1.0) < 1e-6
+    assert oracle.silu(np.zeros(1, np.float32))[0] == 0.0
+    grid = np.linspace(-2.0, -0.5, 150001, dtype=np.float32)
+    v = oracle.silu(grid)
+    i = int(np.argmin(v))
+    assert abs(float(grid[i]) + 1.27846) < 1e-3 and abs(float(v[i]) + 0.278465) < 1e-5
+    assert np.isnan(oracle.silu(np.array([np.nan], np.float32))[0])
+
+
+def test_swiglu_is_silu_of_gate_times_up(oracle, synth):
+    # The composition against the oracle's pinned pieces, with bias on both
+    # projections and an odd group size.
+    M, K, N, G = 6, 70, 24, 8
+    x = synth.normal((M, K), 93, 1)
+    Wg, Wu = synth.normal((K, N), 94, 0, 0.0, 0.05), synth.normal((K, N), 95, 0, 0.0, 0.05)
+    bg, bu = synth.normal((1, N), 96, 2, 0.0, 0.5), synth.normal((1, N), 97, 2, 0.0, 0.5)
+    qg, sg = oracle.quantize_int4(Wg, G)
+    qu, su = oracle.quantize_int4(Wu, G)
+    g = oracle.quantized_matmul_int4(x, qg, sg, G, bg)
+    u = oracle.quantized_matmul_int4(x, qu, su, G, bu)
+    ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
+    h = oracle.swiglu_int4(x, qg, sg, qu, su, G, bg, bu)
+    assert np.max(np.abs(h - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
