@@ -158,8 +158,10 @@ class Case:
         torch.cuda.synchronize()
         return s.elapsed_time(e) / steps  # ms per step
 
-    def time_graph(self, steps: int, warmup: int) -> float:
-        """K launches captured into one hipGraph, replayed once in the timed region."""
+    def time_graph(self, steps: int, warmup: int, extra_replays: int = 0) -> float:
+        """K launches captured into one hipGraph, replayed once in the timed region.
+        extra_replays > 0 replays it that many more times afterwards (untimed by
+        the contract) and keeps their per-call times in self.replay_ms."""
         import torch
 
         for i in range(warmup):
@@ -177,7 +179,15 @@ class Case:
         g.replay()
         e.record()
         torch.cuda.synchronize()
-        return s.elapsed_time(e) / steps
+        ms = s.elapsed_time(e) / steps
+        self.replay_ms = []
+        for _ in range(extra_replays):
+            s.record()
+            g.replay()
+            e.record()
+            torch.cuda.synchronize()
+            self.replay_ms.append(s.elapsed_time(e) / steps)
+        return ms
 
     def check(self, oracle, rows=None) -> float:
         """max rel error of the last output against the oracle (row subset for big M)."""
@@ -239,6 +249,19 @@ def cpu_baseline(c, budget_s: float):
         reps = int(max(3, min(200, budget_s / max(first[0], 1e-6))))
         secs, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, reps)
         kind, cores = "reference", ref.omp_max_threads()
+        # The three phases of the same forward, then the whole forward on one thread.
+        ph = ref.time_phases(c["bits"], x, q, s, c["scheme"], c["G"], b, max(3, min(50, reps // 4)))
+        phases = {k: round(statistics.median(p[i] for p in ph) * 1e3, 4)
+                  for i, k in enumerate(("dequantize_ms", "matmul_ms", "bias_ms"))}
+        prev = ref.set_threads(1)
+        try:
+            one, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, 1)
+            n1 = int(max(3, min(50, (budget_s / 4) / max(one[0], 1e-6))))
+            one, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, n1)
+        finally:
+            ref.set_threads(prev)
+        one_thread = {"value": round(alg_bytes(c) / statistics.median(one) / 1e9, 4), "unit": "GB/s", "cores": 1,
+                      "ms": round(statistics.median(one) * 1e3, 3), "calls": n1}
     else:
         secs = []
         t_end = time.time() + budget_s
@@ -252,6 +275,7 @@ def cpu_baseline(c, budget_s: float):
             if len(secs) >= 200:
                 break
         kind, cores = "port", 1
+        phases, one_thread = None, None
     med = statistics.median(secs)
     return {
         "value": round(alg_bytes(c) / med / 1e9, 3),
@@ -262,6 +286,8 @@ def cpu_baseline(c, budget_s: float):
                   f"(dequantize + blocked AVX2 matmul + bias), host {platform.processor() or platform.machine()}, "
                   f"nproc={os.cpu_count()}",
         "tflops": round(alg_flops(c) / med / 1e12, 4),
+        "phases_ms": phases,
+        "one_thread": one_thread,
     }
 
 
@@ -469,7 +495,12 @@ def main() -> int:
     calibration_copy(dev)
     case = Case(pkg, c, dev, copies)
     ms_eager = case.time_eager(min(args.steps, 500), args.warmup)
-    ms = ms_eager if args.eager else case.time_graph(args.steps, args.warmup)
+    ms = ms_eager if args.eager else case.time_graph(args.steps, args.warmup, extra_replays=9)
+    spread = None
+    if not args.eager:
+        q = np.percentile(np.array([ms] + case.replay_ms) * 1e3, [10, 50, 90])
+        spread = {"p10": round(float(q[0]), 3), "p50": round(float(q[1]), 3), "p90": round(float(q[2]), 3),
+                  "replays": 1 + len(case.replay_ms)}
     err = case.check(Oracle(), rows=None if c["M"] <= 256 else np.r_[0:8, c["M"] - 8:c["M"]])
     log(f"[bench] {args.config}: {ms * 1e3:.3f} us/step (eager {ms_eager * 1e3:.3f} us), rel_err {err:.2e}")
     if err > 1e-5:
@@ -501,6 +532,7 @@ def main() -> int:
                    "group_size": c["G"] or None, "bits": c["bits"], "weight_copies": copies,
                    "launch": "eager" if args.eager else "one hipGraph of K back-to-back forward calls",
                    "eager_us_per_step": round(ms_eager * 1e3, 3), "tflops": round(tfl, 4),
+                   "us_per_step_over_replays": spread,
                    "rel_err_vs_oracle": err},
         "roofline": roofline,
     }

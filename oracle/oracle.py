@@ -174,6 +174,10 @@ class Reference:
         L.ref_time_quantized_matmul.argtypes = [_int, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _int, _i64, _vp, _int,
                                                 ctypes.POINTER(_dbl), _vp]
         L.ref_omp_max_threads.restype = _int
+        L.ref_time_phases.argtypes = [_int, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _int, _i64, _vp, _int,
+                                      ctypes.POINTER(_dbl)]
+        L.ref_set_threads.argtypes = [_int]
+        L.ref_set_threads.restype = _int
         L.ref_silu.argtypes = [_vp, _i64, _vp]
         L.ref_mul.argtypes = [_vp, _vp, _i64, _vp]
 
@@ -275,6 +279,21 @@ class Reference:
 
     def omp_max_threads(self) -> int:
         return int(self.lib.ref_omp_max_threads())
+
+    def set_threads(self, n: int) -> int:
+        """OpenMP threads for later calls; returns the previous maximum."""
+        return int(self.lib.ref_set_threads(int(n)))
+
+    def time_phases(self, bits: int, x, q, s, scheme: int, group_size: int, bias, reps: int):
+        """Per-call seconds of (dequantize, matmul, bias add) of the reference forward."""
+        x, q, s = _f32(x), _f32(q), _f32(s)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        secs = (_dbl * (3 * reps))()
+        rc = self.lib.ref_time_phases(bits, _p(x), x.shape[0], x.shape[1], q.shape[1], _p(q), _p(s), s.size, scheme,
+                                      group_size, _p(b), reps, secs)
+        if rc != 0:
+            raise RuntimeError("reference forward raised")
+        return [tuple(secs[3 * r: 3 * r + 3]) for r in range(reps)]
 
 
 def reference_available() -> bool:

@@ -179,6 +179,47 @@ int ref_time_quantized_matmul(int bits, const float* x, int64_t M, int64_t K, in
     }
 }
 
+// The same forward split into its three phases as quantization.cpp:189-206
+// runs them (dequantize, x.matmul(w), out + bias): writes per-call seconds
+// of each phase into secs[3*r + 0..2].
+int ref_time_phases(int bits, const float* x, int64_t M, int64_t K, int64_t N, const float* q, const float* scales,
+                    int64_t nscales, int scheme, int64_t group_size, const float* bias, int reps, double* secs) {
+    try {
+        QuantizedTensor qt = make_qt(q, scales, nscales, K, N, bits == 8 ? scheme : 2,
+                                     bits == 8 ? K * N : group_size, bits);
+        Tensor tx = from_host(x, {M, K});
+        Tensor tb = bias ? from_host(bias, {1, N}) : Tensor();
+        for (int r = 0; r < reps; ++r) {
+            auto t0 = std::chrono::steady_clock::now();
+            Tensor w = bits == 8 ? quantization::dequantize_int8(qt) : quantization::dequantize_int4(qt);
+            auto t1 = std::chrono::steady_clock::now();
+            Tensor y = tx.matmul(w);
+            auto t2 = std::chrono::steady_clock::now();
+            if (tb.is_defined()) y = y + tb;
+            auto t3 = std::chrono::steady_clock::now();
+            secs[3 * r + 0] = std::chrono::duration<double>(t1 - t0).count();
+            secs[3 * r + 1] = std::chrono::duration<double>(t2 - t1).count();
+            secs[3 * r + 2] = std::chrono::duration<double>(t3 - t2).count();
+        }
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Sets the OpenMP thread count of later calls (the reference parallelises
+// with OpenMP only); returns the previous maximum.
+int ref_set_threads(int n) {
+#ifdef _OPENMP
+    const int prev = omp_get_max_threads();
+    omp_set_num_threads(n);
+    return prev;
+#else
+    (void)n;
+    return 1;
+#endif
+}
+
 int ref_silu(const float* x, int64_t n, float* out) {
     try {
         to_host(silu(from_host(x, {n})), out);

@@ -203,30 +203,41 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
 // strip j of the gate weight and NW on strip j of the up weight -- x is read
 // by both groups from the same CU's caches -- and the epilogue writes
 // silu(gate + bias) * (up + bias2).
-template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG>
+//
+// SPW > 1 strips per workgroup (adjacent strips j0 .. j0+SPW-1, which must
+// share their INT4 scale column: spc % SPW == 0) load each x and scale quad
+// once for all of them: fewer load instructions per code byte, which is what
+// bounds the single-row GEMV.
+template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW>
 __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__ x, int M, int K, int N,
                                                        const uint4* __restrict__ W, const float* __restrict__ SC,
                                                        const uint4* __restrict__ W2, const float* __restrict__ SC2,
-                                                       int mode, int Kpad, int RQ, const float* __restrict__ bias,
+                                                       int mode, int Kpad, int RQ, int NS,
+                                                       const float* __restrict__ bias,
                                                        const float* __restrict__ bias2, float* __restrict__ y) {
+    static_assert(NG == 1 || SPW == 1, "the gated form takes one strip of each weight");
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
     constexpr int RQ_IT = NW * 64;           // row quads per group iteration
-    constexpr int V = MT * SW;               // accumulators per lane
+    constexpr int CW = SPW * SW;             // columns per workgroup
+    constexpr int V = MT * CW;               // accumulators per lane
     __shared__ float red[NG * NW][V];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
     const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
-    const int j = xcd_swizzle(blockIdx.x, gridDim.x);  // strips of a scale column share an XCD's L2
+    const int j0 = SPW * xcd_swizzle(blockIdx.x, gridDim.x);  // strips of a scale column share an XCD's L2
     const int voff = gtid * 16;
     const uint4* __restrict__ Wm = grp ? W2 : W;
     const float* __restrict__ SCm = grp ? SC2 : SC;
 
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wm + (int64_t)j * RQ, (uint32_t)RQ * 16u);
+    __amdgpu_buffer_rsrc_t rW[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)  // a strip past the last reads zeros and is not stored
+        rW[s] = make_rsrc(Wm + (int64_t)(j0 + s < NS ? j0 + s : 0) * RQ, j0 + s < NS ? (uint32_t)RQ * 16u : 0u);
     __amdgpu_buffer_rsrc_t rS;
     float s_all = 0.0f;
     if constexpr (BITS == 4) {
-        rS = make_rsrc(SCm + (int64_t)(j / mode) * Kpad, (uint32_t)Kpad * 4u);
+        rS = make_rsrc(SCm + (int64_t)(j0 / mode) * Kpad, (uint32_t)Kpad * 4u);
     } else {
         rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
         if (mode) s_all = SCm[0];
@@ -241,13 +252,14 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
 
     const int nit = (RQ + RQ_IT - 1) / RQ_IT;
     for (int it0 = 0; it0 < nit; it0 += U) {
-        uint4 w[U];
+        uint4 w[U][SPW];
         float4 sv[U];
         float4 xv[U][MT];  // x is loaded with the codes (measured 4-7% faster for M >= 4 than at use)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int soff = (it0 + u) * RQ_IT * 16;
-            w[u] = buf_load16(rW, voff, soff);
+#pragma unroll
+            for (int s = 0; s < SPW; ++s) w[u][s] = buf_load16(rW[s], voff, soff);
             if constexpr (BITS == 4) {
                 sv[u] = buf_load4f<true>(rS, voff, soff);  // devscales rows are padded to 16
             } else if (!mode) {
@@ -268,29 +280,33 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
                     sv[u].w = (k0 + 3 < K) ? s_all : 0.0f;
                 }
             }
-            const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const float4 xm = xv[u][m];
                 float xs[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
-                if constexpr (BITS == 4) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t hi = dw[r] & 0xF0F0F0F0u;         // columns 2b+1, as 16*q
-                        const uint32_t lo = (dw[r] << 4) & 0xF0F0F0F0u;  // columns 2b, as 16*q
+                for (int s = 0; s < SPW; ++s) {
+                    const uint32_t dw[4] = {w[u][s].x, w[u][s].y, w[u][s].z, w[u][s].w};
+                    float* a = acc + m * CW + s * SW;
+                    if constexpr (BITS == 4) {
 #pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            acc[m * 8 + 2 * b] = fmaf(i8_byte(lo, b), xs[r], acc[m * 8 + 2 * b]);
-                            acc[m * 8 + 2 * b + 1] = fmaf(i8_byte(hi, b), xs[r], acc[m * 8 + 2 * b + 1]);
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t hi = dw[r] & 0xF0F0F0F0u;         // columns 2b+1, as 16*q
+                            const uint32_t lo = (dw[r] << 4) & 0xF0F0F0F0u;  // columns 2b, as 16*q
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) {
+                                a[2 * b] = fmaf(i8_byte(lo, b), xs[r], a[2 * b]);
+                                a[2 * b + 1] = fmaf(i8_byte(hi, b), xs[r], a[2 * b + 1]);
+                            }
                         }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+#pragma unroll
+                            for (int d = 0; d < 4; ++d) a[d] = fmaf(i8_byte(dw[d], r), xs[r], a[d]);
                     }
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-#pragma unroll
-                        for (int d = 0; d < 4; ++d) acc[m * 4 + d] = fmaf(i8_byte(dw[d], r), xs[r], acc[m * 4 + d]);
                 }
             }
         }
@@ -310,8 +326,8 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
     // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
     const float post = (BITS == 4) ? 0.0625f : 1.0f;
     for (int v = threadIdx.x; v < V; v += NG * NW * 64) {
-        const int m = v / SW, e = v - m * SW;
-        const int n = j * SW + e;
+        const int m = v / CW, e = v - m * CW;
+        const int n = j0 * SW + e;
         if (m < M && n < N) {
             float r = 0.0f;
 #pragma unroll
@@ -608,18 +624,18 @@ struct GemvWeight {
     const float* bias;
 };
 
-template <int BITS, int MT, int NW, int U, int NG>
+template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad,
                           int RQ, int NS, float* y, hipStream_t s) {
-    const dim3 grid((unsigned)NS);
+    const dim3 grid((unsigned)((NS + SPW - 1) / SPW));
     if (K % 4 == 0)
-        k_gemv<BITS, MT, NW, U, true, NG><<<grid, NG * NW * 64, 0, s>>>(
-            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, w.bias, w2.bias,
-            y);
+        k_gemv<BITS, MT, NW, U, true, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(
+            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, NS, w.bias,
+            w2.bias, y);
     else
-        k_gemv<BITS, MT, NW, U, false, NG><<<grid, NG * NW * 64, 0, s>>>(
-            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, w.bias, w2.bias,
-            y);
+        k_gemv<BITS, MT, NW, U, false, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(
+            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, NS, w.bias,
+            w2.bias, y);
     return hipGetLastError();
 }
 
@@ -629,21 +645,43 @@ hipError_t gemv_launch_nu(const float* x, int M, int K, int N, GemvWeight w, Gem
 // cross-wave LDS reduction short.
 constexpr int kGemvWaves = 4;
 
-template <int BITS, int MT, int NG>
-hipError_t gemv_launch(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad, int RQ,
-                       int NS, float* y, hipStream_t s) {
+#ifndef SGQ_GEMV_SPW
+#define SGQ_GEMV_SPW 1
+#endif
+#ifndef SGQ_GEMV_SPW_WAVES
+#define SGQ_GEMV_SPW_WAVES 4
+#endif
+#ifndef SGQ_GEMV_SPW_MAXMT
+#define SGQ_GEMV_SPW_MAXMT 2
+#endif
+
+template <int BITS, int MT, int NG, int SPW, int NW>
+hipError_t gemv_launch_spw(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad,
+                           int RQ, int NS, float* y, hipStream_t s) {
     // Register budget: row quads in flight per lane shrink as the batch grows.
-    constexpr int UMAX = (MT <= 2) ? 4 : (MT <= 4 ? 2 : 1);
-    const int per_lane = (RQ + kGemvWaves * 64 - 1) / (kGemvWaves * 64);
+    constexpr int UMAX = (MT * SPW <= 2) ? 4 : (MT * SPW <= 4 ? 2 : 1);
+    const int per_lane = (RQ + NW * 64 - 1) / (NW * 64);
     const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
 #define SGQ_GEMV_NU(U_)                                                                                      \
     if ((u >= U_ || U_ == 1) && U_ <= UMAX)                                                                \
-        return gemv_launch_nu<BITS, MT, kGemvWaves, U_, NG>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
+        return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
     SGQ_GEMV_NU(4)
     SGQ_GEMV_NU(2)
     SGQ_GEMV_NU(1)
 #undef SGQ_GEMV_NU
     return hipErrorInvalidValue;
+}
+
+template <int BITS, int MT, int NG>
+hipError_t gemv_launch(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad, int RQ,
+                       int NS, float* y, hipStream_t s) {
+    if constexpr (NG == 1 && SGQ_GEMV_SPW > 1 && MT <= SGQ_GEMV_SPW_MAXMT) {
+        // INT4 strips of one workgroup must share a scale column.
+        if (BITS == 8 || mode % SGQ_GEMV_SPW == 0)
+            return gemv_launch_spw<BITS, MT, NG, SGQ_GEMV_SPW, SGQ_GEMV_SPW_WAVES>(x, M, K, N, w, w2, mode, Kpad, RQ,
+                                                                                NS, y, s);
+    }
+    return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
 }
 
 // Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
