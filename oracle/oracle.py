@@ -33,6 +33,33 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+# Projections of a LLaMA block, in the order the block functions take them.
+BLOCK_PROJ = ("q", "k", "v", "out", "gate", "up", "down")
+
+
+def block_shapes(D: int, H: int):
+    """[K, N] of each projection of BLOCK_PROJ for model width D and MLP width H."""
+    return [(D, D), (D, D), (D, D), (D, D), (D, H), (D, H), (H, D)]
+
+
+def _ptrs(arrays):
+    """A C array of pointers to the given float32 arrays (None -> NULL), plus
+    the converted arrays, which the caller keeps alive across the call."""
+    conv = [None if a is None else _f32(a) for a in arrays]
+    arr = (_vp * len(conv))(*[None if a is None else a.ctypes.data for a in conv])
+    return arr, conv
+
+
+def _block_args(proj):
+    """proj: 7 (codes[K,N], scales, bias or None) in BLOCK_PROJ order."""
+    if len(proj) != 7:
+        raise ValueError("a block has 7 projections")
+    q, kq = _ptrs([p[0] for p in proj])
+    s, ks = _ptrs([p[1] for p in proj])
+    b, kb = _ptrs([p[2] if len(p) > 2 else None for p in proj])
+    return q, s, b, (kq, ks, kb)
+
+
 class Oracle:
     """The C restatement (sgq_oracle.c)."""
 
@@ -56,6 +83,12 @@ class Oracle:
         L.oracle_mul.argtypes = [_vp, _vp, _i64, _vp]
         L.oracle_swiglu_int8.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp]
         L.oracle_swiglu_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]
+        L.oracle_rms_norm.argtypes = [_vp, _i64, _i64, _vp, ctypes.c_float, _vp]
+        L.oracle_softmax_rows.argtypes = [_vp, _i64, _i64, _vp]
+        L.oracle_embedding.argtypes = [_vp, _i64, _vp, _i64, _i64, _vp]
+        L.oracle_causal_attention.argtypes = [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]
+        L.oracle_qllama_block_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                               ctypes.c_float, _i64, _vp]
 
     # quantize_int8: per-tensor for scheme 0 or rank < 2 (src/quantization.cpp:22)
     def quantize_int8(self, x: np.ndarray, scheme: int) -> Tuple[np.ndarray, np.ndarray]:
@@ -138,6 +171,44 @@ class Oracle:
                                     _p(su), _p(bu), per_tensor, _p(out))
         return out
 
+    def rms_norm(self, x, g, eps: float = 1e-5) -> np.ndarray:
+        x, g = _f32(x), _f32(g).reshape(-1)
+        out = np.empty_like(x)
+        D = x.shape[-1]
+        self.lib.oracle_rms_norm(_p(x), x.size // max(D, 1), D, _p(g), eps, _p(out))
+        return out
+
+    def softmax_rows(self, x) -> np.ndarray:
+        x = _f32(x)
+        out = np.empty_like(x)
+        self.lib.oracle_softmax_rows(_p(x), x.size // max(x.shape[-1], 1), x.shape[-1], _p(out))
+        return out
+
+    def embedding(self, idx, w) -> np.ndarray:
+        idx, w = _f32(idx).reshape(-1), _f32(w)
+        out = np.empty((idx.size, w.shape[1]), np.float32)
+        self.lib.oracle_embedding(_p(idx), idx.size, _p(w), w.shape[0], w.shape[1], _p(out))
+        return out
+
+    def causal_attention(self, q, k, v, scale: float) -> np.ndarray:
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        out = np.empty_like(q)
+        self.lib.oracle_causal_attention(_p(q), _p(k), _p(v), q.shape[0], q.shape[1], scale, _p(out))
+        return out
+
+    def qllama_block_int4(self, x, proj, g1, g2, eps: float, attn_scale: float, group_size: int) -> np.ndarray:
+        """LLaMABlock::forward on x[L, D] with quantized projections; proj as in _block_args."""
+        x = _f32(x)
+        L, D = x.shape
+        H = _f32(proj[4][0]).shape[1]
+        qa, sa, ba, keep = _block_args(proj)
+        g1, g2 = _f32(g1).reshape(-1), _f32(g2).reshape(-1)
+        out = np.empty_like(x)
+        self.lib.oracle_qllama_block_int4(_p(x), L, D, H, qa, sa, ba, _p(g1), _p(g2), eps, attn_scale, group_size,
+                                          _p(out))
+        del keep
+        return out
+
     def swiglu_int4(self, x, qg, sg, qu, su, group_size: int, bias_gate=None, bias_up=None) -> np.ndarray:
         x, qg, sg, qu, su = _f32(x), _f32(qg), _f32(sg), _f32(qu), _f32(su)
         out = np.empty((x.shape[0], qg.shape[1]), np.float32)
@@ -179,6 +250,11 @@ class Reference:
         L.ref_set_threads.argtypes = [_int]
         L.ref_set_threads.restype = _int
         L.ref_silu.argtypes = [_vp, _i64, _vp]
+        L.ref_rms_norm.argtypes = [_vp, _i64, _i64, _vp, ctypes.c_float, _vp]
+        L.ref_softmax.argtypes = [_vp, _i64, _i64, _vp]
+        L.ref_embedding.argtypes = [_vp, _i64, _vp, _i64, _i64, _vp]
+        L.ref_qllama_block_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                            ctypes.c_float, _i64, _vp]
         L.ref_mul.argtypes = [_vp, _vp, _i64, _vp]
 
     @staticmethod
@@ -275,6 +351,41 @@ class Reference:
         out = np.empty_like(a)
         if self.lib.ref_mul(_p(a), _p(b), a.size, _p(out)) != 0:
             raise RuntimeError("reference mul raised")
+        return out
+
+    def rms_norm(self, x, g, eps: float = 1e-5):
+        x, g = _f32(x), _f32(g).reshape(-1)
+        out = np.empty_like(x)
+        D = x.shape[-1]
+        if self.lib.ref_rms_norm(_p(x), x.size // max(D, 1), D, _p(g), eps, _p(out)) != 0:
+            raise RuntimeError("reference rms_norm raised")
+        return out
+
+    def softmax_rows(self, x):
+        x = _f32(x)
+        out = np.empty_like(x)
+        if self.lib.ref_softmax(_p(x), x.size // max(x.shape[-1], 1), x.shape[-1], _p(out)) != 0:
+            raise RuntimeError("reference softmax raised")
+        return out
+
+    def embedding(self, idx, w):
+        idx, w = _f32(idx).reshape(-1), _f32(w)
+        out = np.empty((idx.size, w.shape[1]), np.float32)
+        if self.lib.ref_embedding(_p(idx), idx.size, _p(w), w.shape[0], w.shape[1], _p(out)) != 0:
+            raise RuntimeError("reference embedding raised")
+        return out
+
+    def qllama_block_int4(self, x, proj, g1, g2, eps: float, attn_scale: float, group_size: int):
+        x = _f32(x)
+        L, D = x.shape
+        H = _f32(proj[4][0]).shape[1]
+        qa, sa, ba, keep = _block_args(proj)
+        g1, g2 = _f32(g1).reshape(-1), _f32(g2).reshape(-1)
+        out = np.empty_like(x)
+        if self.lib.ref_qllama_block_int4(_p(x), L, D, H, qa, sa, ba, _p(g1), _p(g2), eps, attn_scale, group_size,
+                                          _p(out)) != 0:
+            raise RuntimeError("reference block raised")
+        del keep
         return out
 
     def omp_max_threads(self) -> int:

@@ -16,6 +16,11 @@
 //   ref_matmul                matmul (src/ops.cpp:378-455)
 //   ref_silu                  silu   (src/ops.cpp:561-575)
 //   ref_mul                   mul    (src/ops.cpp:239-253)
+//   ref_rms_norm              rms_norm (src/ops.cpp:1532-1556)
+//   ref_softmax               softmax over the last dimension (src/ops.cpp:2101-2140)
+//   ref_embedding             embedding (src/ops.cpp:2624-2650)
+//   ref_qllama_block_int4     LLaMABlock::forward (include/sovereigngrad/models.hpp:217-222)
+//                             written out with QuantizedLinear4Bit projections
 #include "sovereigngrad/quantization.hpp"
 #include "sovereigngrad/ops.hpp"
 
@@ -232,6 +237,74 @@ int ref_silu(const float* x, int64_t n, float* out) {
 int ref_mul(const float* a, const float* b, int64_t n, float* out) {
     try {
         to_host(mul(from_host(a, {n}), from_host(b, {n})), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_rms_norm(const float* x, int64_t B, int64_t D, const float* g, float eps, float* out) {
+    try {
+        to_host(rms_norm(from_host(x, {B, D}), from_host(g, {D}), eps), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_softmax(const float* x, int64_t R, int64_t C, float* out) {
+    try {
+        to_host(softmax(from_host(x, {R, C}), -1), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_embedding(const float* idx, int64_t n, const float* w, int64_t V, int64_t E, float* out) {
+    try {
+        to_host(embedding(from_host(idx, {n}), from_host(w, {V, E})), out);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// LLaMABlock::forward (models.hpp:217-222) on x[L, D], its attention
+// (CausalSelfAttention::forward, nn.hpp:533-553, non-flash branch) and MLP
+// (SwiGLU::forward, nn.hpp:151-156) written out statement by statement, each
+// Linear replaced by QuantizedLinear4Bit::forward (nn.hpp:994-996), i.e.
+// quantized_matmul_int4 with the module's [1, N] bias.  Projection p = 0..6:
+// q, k, v, out, gate, up, down; bias[p] may be NULL (no bias add).
+int ref_qllama_block_int4(const float* x, int64_t L, int64_t D, int64_t H, const float* const* codes,
+                          const float* const* scales, const float* const* bias, const float* g1, const float* g2,
+                          float eps, float attn_scale, int64_t group_size, float* out) {
+    try {
+        const int64_t K[7] = {D, D, D, D, D, D, H}, N[7] = {D, D, D, D, H, H, D};
+        auto proj = [&](const Tensor& in, int p) {
+            const int64_t G = group_size <= 0 ? 32 : group_size;
+            QuantizedTensor qt = make_qt(codes[p], scales[p], (K[p] * N[p] + G - 1) / G, K[p], N[p], 2, G, 4);
+            Tensor b = bias[p] ? from_host(bias[p], {1, N[p]}) : Tensor();
+            return quantization::quantized_matmul_int4(in, qt, b);
+        };
+        Tensor tx = from_host(x, {L, D});
+        Tensor tg1 = from_host(g1, {D}), tg2 = from_host(g2, {D});
+        // attn->forward(norm1->forward(x))
+        Tensor n1 = rms_norm(tx, tg1, eps);
+        Tensor Q = proj(n1, 0), Kt = proj(n1, 1), V = proj(n1, 2);
+        Tensor K_t = Kt.transpose(0, 1).contiguous();
+        Tensor scores = Q.matmul(K_t) * attn_scale;
+        Tensor mask = Tensor::triu({L, L}, 1, Device::CPU);
+        scores = scores.masked_fill(mask, -1e9f);
+        Tensor attn_weights = softmax(scores, -1);
+        Tensor context = attn_weights.matmul(V);
+        Tensor h = tx + proj(context, 3);
+        // mlp->forward(norm2->forward(h))
+        Tensor n2 = rms_norm(h, tg2, eps);
+        Tensor gate = proj(n2, 4).silu();
+        Tensor up = proj(n2, 5);
+        Tensor hidden = gate * up;
+        to_host(h + proj(hidden, 6), out);
         return 0;
     } catch (const std::exception&) {
         return -1;

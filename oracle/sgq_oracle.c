@@ -25,6 +25,15 @@
  *   oracle_swiglu_int8 / _int4        include/sovereigngrad/nn.hpp:151-154 (the
  *                                     gate/up half of SwiGLU::forward) on
  *                                     quantized weights
+ *   oracle_rms_norm                   src/ops.cpp:1532-1556
+ *   oracle_softmax_rows               src/ops.cpp:2101-2140 (last dimension)
+ *   oracle_embedding                  src/ops.cpp:2624-2650
+ *   oracle_causal_attention           include/sovereigngrad/nn.hpp:533-553 (the
+ *                                     non-flash branch of CausalSelfAttention)
+ *   oracle_qllama_block_int4          include/sovereigngrad/models.hpp:217-222
+ *                                     (LLaMABlock::forward) with every
+ *                                     projection a QuantizedLinear4Bit
+ *                                     (nn.hpp:994-996)
  *
  * Floating-point contract.  The reference is built with GCC -O3 -mavx2 -mfma
  * in gnu++17 mode, where -ffp-contract=fast is the default, so every
@@ -265,6 +274,134 @@ void oracle_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const f
     oracle_quantized_matmul_int4(x, M, K, N, qg, sg, group_size, bg, gate);
     oracle_quantized_matmul_int4(x, M, K, N, qu, su, group_size, bu, up);
     swiglu_finish(gate, up, M * N, out);
+    free(gate);
+    free(up);
+}
+
+/* rms_norm, CPU branch (src/ops.cpp:1532-1556), rows of [B, D]:
+ * inv_rms = 1 / sqrt(sum_sq / D + eps) with IEEE divide and sqrt, and
+ * out = x * inv_rms * g as two multiplies, left to right.
+ *
+ * sum_sq is `sum_sq += v * v` over d in order.  With the reference's flags
+ * (-O3 -mavx2 -mfma, no fast-math) GCC vectorises this loop as an in-order
+ * reduction: whole blocks of 8, then one block of 4 if at least 4 remain, take
+ * the products as separate multiplies and add them one at a time in order;
+ * the last 0-3 elements run the scalar loop, which is contracted to FMA.  The
+ * golden fixtures pin this against the compiled reference. */
+static float rms_sum_squares(const float* x, int64_t D) {
+    float ss = 0.0f;
+    int64_t d = 0;
+    if (D >= 8)
+        for (; d + 8 <= D; d += 8)
+            for (int64_t l = 0; l < 8; ++l) ss = ss + x[d + l] * x[d + l];
+    if (D - d >= 4) {
+        for (int64_t l = 0; l < 4; ++l) ss = ss + x[d + l] * x[d + l];
+        d += 4;
+    }
+    for (; d < D; ++d) ss = fmaf(x[d], x[d], ss);
+    return ss;
+}
+
+void oracle_rms_norm(const float* x, int64_t B, int64_t D, const float* g, float eps, float* out) {
+    for (int64_t i = 0; i < B; ++i) {
+        const float* xi = x + i * D;
+        const float inv = 1.0f / sqrtf(rms_sum_squares(xi, D) / (float)D + eps);
+        for (int64_t d = 0; d < D; ++d) out[i * D + d] = (xi[d] * inv) * g[d];
+    }
+}
+
+/* softmax over the last dimension (src/ops.cpp:2101-2140 with inner_size 1):
+ * the maximum starts at element 0 and is replaced on `>`; the sum of
+ * exp(x - max) runs in order; out = exp(x - max) / sum, exp being libm's expf. */
+void oracle_softmax_rows(const float* x, int64_t R, int64_t C, float* out) {
+    for (int64_t r = 0; r < R; ++r) {
+        const float* xr = x + r * C;
+        float mx = xr[0];
+        for (int64_t d = 1; d < C; ++d)
+            if (xr[d] > mx) mx = xr[d];
+        float sum = 0.0f;
+        for (int64_t d = 0; d < C; ++d) sum += expf(xr[d] - mx);
+        for (int64_t d = 0; d < C; ++d) out[r * C + d] = expf(xr[d] - mx) / sum;
+    }
+}
+
+/* embedding (src/ops.cpp:2624-2650): token id = (int)index (truncation); ids
+ * outside [0, V) give a zero row. */
+void oracle_embedding(const float* idx, int64_t n, const float* w, int64_t V, int64_t E, float* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const int id = (int)idx[i];
+        if (id >= 0 && id < V)
+            memcpy(out + i * E, w + (int64_t)id * E, (size_t)E * sizeof(float));
+        else
+            memset(out + i * E, 0, (size_t)E * sizeof(float));
+    }
+}
+
+/* CausalSelfAttention::forward after the projections (nn.hpp:545-552):
+ * scores = Q . K^T (the reference matmul on the contiguous transpose), times
+ * scale (one multiply each), masked_fill of the strict upper triangle
+ * (Tensor::triu(..., 1), tensor.cpp:205-222) with -1e9, softmax over the last
+ * dimension, then weights . V.  One attention over the full width D. */
+void oracle_causal_attention(const float* Q, const float* K, const float* V, int64_t L, int64_t D, float scale,
+                             float* ctx) {
+    const size_t ll = (size_t)(L * L > 0 ? L * L : 1);
+    float* kt = (float*)calloc((size_t)(L * D > 0 ? L * D : 1), sizeof(float));
+    float* sc = (float*)malloc(ll * sizeof(float));
+    float* w = (float*)malloc(ll * sizeof(float));
+    for (int64_t j = 0; j < L; ++j)
+        for (int64_t d = 0; d < D; ++d) kt[d * L + j] = K[j * D + d];
+    oracle_matmul(Q, kt, sc, L, D, L);
+    for (int64_t r = 0; r < L; ++r)
+        for (int64_t c = 0; c < L; ++c) {
+            const float v = sc[r * L + c] * scale;
+            sc[r * L + c] = (c >= r + 1) ? -1e9f : v;
+        }
+    oracle_softmax_rows(sc, L, L, w);
+    oracle_matmul(w, V, ctx, L, L, D);
+    free(kt);
+    free(sc);
+    free(w);
+}
+
+/* LLaMABlock::forward (models.hpp:217-222) on x[L, D] with every projection a
+ * QuantizedLinear4Bit (quantized_matmul_int4 with its [1, N] bias):
+ *   h   = x + out_proj(attention(q_proj(n1), k_proj(n1), v_proj(n1))),  n1 = rms_norm(x, g1)
+ *   out = h + w_down(silu(w_gate(n2)) * w_up(n2)),                      n2 = rms_norm(h, g2)
+ * Projections p = 0..6 are q, k, v, out ([D, D]), gate, up ([D, H]) and down
+ * ([H, D]); codes[p] are fp32 INT4 codes in the weight's [K, N] shape,
+ * scales[p] their group scales, bias[p] a row of N floats or NULL.  The two
+ * residual adds are equal-shape vec_add (one addition per element). */
+void oracle_qllama_block_int4(const float* x, int64_t L, int64_t D, int64_t H, const float* const* codes,
+                              const float* const* scales, const float* const* bias, const float* g1,
+                              const float* g2, float eps, float attn_scale, int64_t group_size, float* out) {
+    const size_t ld = (size_t)(L * D > 0 ? L * D : 1), lh = (size_t)(L * H > 0 ? L * H : 1);
+    float* n1 = (float*)malloc(ld * sizeof(float));
+    float* q = (float*)malloc(ld * sizeof(float));
+    float* k = (float*)malloc(ld * sizeof(float));
+    float* v = (float*)malloc(ld * sizeof(float));
+    float* ctx = (float*)malloc(ld * sizeof(float));
+    float* h = (float*)malloc(ld * sizeof(float));
+    float* gate = (float*)malloc(lh * sizeof(float));
+    float* up = (float*)malloc(lh * sizeof(float));
+    oracle_rms_norm(x, L, D, g1, eps, n1);
+    oracle_quantized_matmul_int4(n1, L, D, D, codes[0], scales[0], group_size, bias[0], q);
+    oracle_quantized_matmul_int4(n1, L, D, D, codes[1], scales[1], group_size, bias[1], k);
+    oracle_quantized_matmul_int4(n1, L, D, D, codes[2], scales[2], group_size, bias[2], v);
+    oracle_causal_attention(q, k, v, L, D, attn_scale, ctx);
+    oracle_quantized_matmul_int4(ctx, L, D, D, codes[3], scales[3], group_size, bias[3], h);
+    for (int64_t i = 0; i < L * D; ++i) h[i] = x[i] + h[i];
+    oracle_rms_norm(h, L, D, g2, eps, n1);
+    oracle_quantized_matmul_int4(n1, L, D, H, codes[4], scales[4], group_size, bias[4], gate);
+    oracle_quantized_matmul_int4(n1, L, D, H, codes[5], scales[5], group_size, bias[5], up);
+    swiglu_finish(gate, up, L * H, gate);
+    oracle_quantized_matmul_int4(gate, L, H, D, codes[6], scales[6], group_size, bias[6], out);
+    for (int64_t i = 0; i < L * D; ++i) out[i] = h[i] + out[i];
+    free(n1);
+    free(q);
+    free(k);
+    free(v);
+    free(ctx);
+    free(h);
     free(gate);
     free(up);
 }

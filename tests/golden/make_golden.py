@@ -6,8 +6,9 @@ by `make -C oracle ref` from the reference's own sources):
     python tests/golden/make_golden.py
 
 Every expected output comes from the reference's own functions
-(quantization::quantize_int8/_int4, dequantize_*, quantized_matmul_*, and
-silu / mul composed as SwiGLU::forward composes them; see
+(quantization::quantize_int8/_int4, dequantize_*, quantized_matmul_*, silu /
+mul composed as SwiGLU::forward composes them, rms_norm, softmax, embedding,
+and LLaMABlock::forward written out with QuantizedLinear4Bit projections; see
 oracle/ref_shim.cpp).  Inputs are seeded (soverign-grad_amd/synth.py) or
 hand-built special values.  The fixtures are data only: inputs and the
 reference's outputs.
@@ -23,7 +24,7 @@ import numpy as np
 
 ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
-from oracle.oracle import Reference  # noqa: E402
+from oracle.oracle import BLOCK_PROJ, Reference, block_shapes  # noqa: E402
 
 spec = importlib.util.spec_from_file_location("sgq_synth", ROOT / "soverign-grad_amd" / "synth.py")
 synth = importlib.util.module_from_spec(spec)
@@ -157,6 +158,49 @@ def main() -> None:
         if bg is not None:
             t["bias_gate"], t["bias_up"] = bg, bu
         add(f"swiglu_int{bits}", params, **t)
+
+    # ---- rms_norm, softmax, embedding and the quantized LLaMA block ---------
+    for (B, D, std) in [(2, 1, 1.0), (3, 3, 1.0), (2, 4, 2.0), (2, 7, 1.0), (3, 8, 1.0), (2, 9, 3.0), (2, 12, 1.0),
+                        (2, 15, 1.0), (2, 16, 0.1), (3, 31, 1.0), (2, 97, 3.0), (2, 2048, 1.0)]:
+        xx = x_of((B, D), 1, std)
+        g = (1.0 + x_of((D,), 2, 0.1)).astype(np.float32)
+        add("rms_norm", {"B": B, "D": D, "eps": 1e-5}, x=xx, g=g, y=ref.rms_norm(xx, g, 1e-5))
+    xs = np.array([[0.0] * 6, [1e18, -1e18, 3.0, 0.0, 1.0, 2.0], [np.inf, 1.0, 2.0, 3.0, 4.0, 5.0],
+                   [1e-30, -1e-30, 1e-38, 0.0, -0.0, 5e-39]], np.float32)
+    gs6 = np.array([1.0, -1.0, 0.5, 2.0, 1.0, 3.0], np.float32)
+    add("rms_norm", {"B": 4, "D": 6, "eps": 1e-5, "special": True}, x=xs, g=gs6, y=ref.rms_norm(xs, gs6, 1e-5))
+    for (R, C) in [(1, 1), (3, 7), (4, 37), (2, 300)]:
+        sc = x_of((R, C), 1, 3.0)
+        add("softmax", {"R": R, "C": C}, x=sc, y=ref.softmax_rows(sc))
+    sc = x_of((4, 9), 1, 3.0)
+    sc[0, 3:] = -1e9
+    sc[1, :] = 2.5
+    sc[2, 1:] = -1e9
+    sc[3, 0] = 80.0
+    add("softmax", {"R": 4, "C": 9, "special": True}, x=sc, y=ref.softmax_rows(sc))
+    ew = x_of((11, 24), 0)
+    idx = np.array([0, 10, 3, -1, 11, 2.9, -0.5, 7, 7, 5.5], np.float32)
+    add("embedding", {"V": 11, "E": 24}, idx=idx, w=ew, y=ref.embedding(idx, ew))
+    for (L, D, H, G, heads, with_bias) in [(1, 32, 64, 32, 4, True), (5, 64, 160, 32, 4, True),
+                                           (9, 128, 256, 128, 8, True), (12, 64, 96, 16, 2, False),
+                                           (17, 32, 64, 32, 1, True)]:
+        xx = x_of((L, D), 1)
+        t = {"x": xx}
+        proj = []
+        for name, (K, N) in zip(BLOCK_PROJ, block_shapes(D, H)):
+            W = x_of((K, N), 0, 0.05)
+            q, s_ = ref.quantize_int4(W, G)
+            b = x_of((N,), 2, 0.02) if with_bias else None
+            proj.append((q, s_, b))
+            t[f"q_{name}"], t[f"s_{name}"] = q, s_
+            if b is not None:
+                t[f"b_{name}"] = b
+        g1 = (1.0 + x_of((D,), 2, 0.1)).astype(np.float32)
+        g2 = (1.0 + x_of((D,), 2, 0.1)).astype(np.float32)
+        scale = np.float32(1.0) / np.sqrt(np.float32(D // heads))  # CausalSelfAttention, nn.hpp:518
+        t.update(g1=g1, g2=g2, attn_scale=np.array([scale], np.float32))
+        t["y"] = ref.qllama_block_int4(xx, proj, g1, g2, 1e-5, float(scale), G)
+        add("qllama_block_int4", {"L": L, "D": D, "H": H, "group_size": G, "heads": heads, "eps": 1e-5}, **t)
 
     np.savez_compressed(OUT_NPZ, **arrays)
     OUT_JSON.write_text(json.dumps({"generator": "tests/golden/make_golden.py", "cases": cases}, indent=1))

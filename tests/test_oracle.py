@@ -263,3 +263,138 @@ def test_swiglu_is_silu_of_gate_times_up(oracle, synth):
     ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
     h = oracle.swiglu_int4(x, qg, sg, qu, su, G, bg, bu)
     assert np.max(np.abs(h - ref)) <= 1e-6 * max(1.0, np.max(np.abs(ref)))
+
+
+# ---- rms_norm, softmax, embedding, attention, quantized LLaMA block ----------
+
+def _block_proj(c):
+    from oracle.oracle import BLOCK_PROJ
+
+    return [(c[f"q_{n}"], c[f"s_{n}"], c.get(f"b_{n}")) for n in BLOCK_PROJ]
+
+
+def test_golden_norm_softmax_embedding_block(oracle, golden):
+    kinds = {"rms_norm": 0, "softmax": 0, "embedding": 0, "qllama_block_int4": 0}
+    for c in golden:
+        k, p = c["kind"], c["params"]
+        if k == "rms_norm":
+            y = oracle.rms_norm(c["x"], c["g"], p["eps"])
+        elif k == "softmax":
+            y = oracle.softmax_rows(c["x"])
+        elif k == "embedding":
+            y = oracle.embedding(c["idx"], c["w"])
+        elif k == "qllama_block_int4":
+            y = oracle.qllama_block_int4(c["x"], _block_proj(c), c["g1"], c["g2"], p["eps"], float(c["attn_scale"][0]),
+                                         p["group_size"])
+        else:
+            continue
+        assert same_bits(y, c["y"]), (k, p)
+        kinds[k] += 1
+    assert kinds["rms_norm"] >= 12 and kinds["softmax"] >= 5 and kinds["embedding"] >= 1
+    assert kinds["qllama_block_int4"] >= 5
+
+
+def _random_block(oracle, synth, L, D, H, G, seed, bias=True, zero_codes=False):
+    from oracle.oracle import block_shapes
+
+    proj = []
+    for i, (K, N) in enumerate(block_shapes(D, H)):
+        W = synth.normal((K, N), seed + i, 0, 0.0, 0.05)
+        q, s = oracle.quantize_int4(W, G)
+        if zero_codes:
+            q = np.zeros_like(q)
+        b = synth.normal((N,), seed + i, 2, 0.0, 0.3) if bias else None
+        proj.append((q, s, b))
+    x = synth.normal((L, D), seed, 1)
+    g1 = 1.0 + synth.normal((D,), seed + 20, 2, 0.0, 0.1)
+    g2 = 1.0 + synth.normal((D,), seed + 21, 2, 0.0, 0.1)
+    return x, proj, g1.astype(np.float32), g2.astype(np.float32)
+
+
+@pytest.mark.parametrize("L,D,H,G", [(7, 64, 96, 32), (10, 96, 128, 32), (3, 256, 512, 128)])
+def test_reference_live_block(oracle, ref, synth, L, D, H, G):
+    x, proj, g1, g2 = _random_block(oracle, synth, L, D, H, G, 300 + L)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D // 4)))
+    assert same_bits(oracle.qllama_block_int4(x, proj, g1, g2, 1e-5, scale, G),
+                     ref.qllama_block_int4(x, proj, g1, g2, 1e-5, scale, G))
+    for Dn in (1, 5, 8, 13, 64, 67, 1001):
+        xn = synth.normal((3, Dn), 400 + Dn, 1, 0.0, 2.0)
+        gn = synth.normal((Dn,), 401 + Dn, 2)
+        assert same_bits(oracle.rms_norm(xn, gn), ref.rms_norm(xn, gn)), Dn
+
+
+def test_rms_norm_closed_forms(oracle, synth):
+    # A constant row c gives c / sqrt(c^2 + eps) * g; the mean square of the
+    # output with g = 1 is D*ss/(ss + D*eps)/D, i.e. 1 up to eps; scaling x by
+    # a power of two leaves the output unchanged when eps is negligible.
+    D = 64
+    g = synth.normal((D,), 501, 2)
+    row = np.full((1, D), 3.0, np.float32)
+    out = oracle.rms_norm(row, g)
+    inv = np.float32(1.0) / np.sqrt(np.float32(9.0 + 1e-5))
+    assert np.array_equal(out[0], (np.float32(3.0) * inv) * g)
+    x = synth.normal((4, D), 502, 1)
+    y = oracle.rms_norm(x, np.ones(D, np.float32), 0.0)
+    assert np.allclose((y.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-6)
+    assert np.allclose(oracle.rms_norm(x * 64.0, np.ones(D, np.float32), 0.0), y, rtol=0, atol=2e-7)
+    z = oracle.rms_norm(np.zeros((1, D), np.float32), g)
+    assert np.all(z == 0)
+
+
+def test_softmax_closed_forms(oracle, synth):
+    # Rows sum to 1; a shift by an exactly representable constant leaves the
+    # bits unchanged (x - max is the same); -1e9 entries get weight exactly 0;
+    # equal entries get exactly 1/C when C is a power of two.
+    x = np.round(synth.normal((5, 33), 503, 1, 0.0, 4.0)).astype(np.float32)
+    p = oracle.softmax_rows(x)
+    assert np.allclose(p.astype(np.float64).sum(axis=1), 1.0, atol=1e-6)
+    assert same_bits(p, oracle.softmax_rows(x + np.float32(1000.0)))
+    m = x.copy()
+    m[:, 10:] = -1e9
+    pm = oracle.softmax_rows(m)
+    assert np.all(pm[:, 10:] == 0.0)
+    assert np.array_equal(oracle.softmax_rows(np.full((1, 16), 2.5, np.float32)), np.full((1, 16), 1 / 16, np.float32))
+
+
+def test_causal_attention_closed_forms(oracle, synth):
+    # Row 0 attends to itself only, so it is V[0] exactly; with equal keys
+    # every row r averages V[0..r]; changing later rows of Q, K, V never
+    # changes earlier output rows.
+    L, D = 9, 32
+    q, k, v = (synth.normal((L, D), 504 + i, 1) for i in range(3))
+    ctx = oracle.causal_attention(q, k, v, 0.25)
+    assert same_bits(ctx[0], v[0])
+    keq = np.tile(k[:1], (L, 1))
+    ce = oracle.causal_attention(q, keq, v, 0.25)
+    for r in range(L):
+        assert np.allclose(ce[r], v[: r + 1].astype(np.float64).mean(axis=0), rtol=1e-5, atol=1e-6)
+    q2, k2, v2 = q.copy(), k.copy(), v.copy()
+    q2[5:], k2[5:], v2[5:] = 7.0, -3.0, 11.0
+    assert same_bits(oracle.causal_attention(q2, k2, v2, 0.25)[:5], ctx[:5])
+
+
+def test_block_closed_forms(oracle, synth):
+    # All-zero codes leave only the biases: attention returns b_out, the MLP
+    # returns b_down, so out = (x + b_out) + b_down exactly.  Causality: later
+    # rows of x never change earlier output rows.  A prefix of the sequence
+    # reproduces the same rows up to summation order (decode equivalence).
+    L, D, H, G = 11, 64, 96, 32
+    x, proj, g1, g2 = _random_block(oracle, synth, L, D, H, G, 600, zero_codes=True)
+    out = oracle.qllama_block_int4(x, proj, g1, g2, 1e-5, 0.25, G)
+    assert same_bits(out, (x + proj[3][2]) + proj[6][2])
+    x, proj, g1, g2 = _random_block(oracle, synth, L, D, H, G, 700)
+    full = oracle.qllama_block_int4(x, proj, g1, g2, 1e-5, 0.25, G)
+    x2 = x.copy()
+    x2[6:] = 5.0
+    assert same_bits(oracle.qllama_block_int4(x2, proj, g1, g2, 1e-5, 0.25, G)[:6], full[:6])
+    for t in (0, 3, 8):
+        pre = oracle.qllama_block_int4(x[: t + 1], proj, g1, g2, 1e-5, 0.25, G)
+        assert np.allclose(pre[t], full[t], rtol=0, atol=2e-6 * np.abs(full[t]).max()), t
+
+
+def test_embedding_closed_forms(oracle, synth):
+    w = synth.normal((6, 8), 505, 0)
+    idx = np.array([5, 0, 2.99, -0.99, -1, 6], np.float32)
+    e = oracle.embedding(idx, w)
+    assert same_bits(e[0], w[5]) and same_bits(e[1], w[0]) and same_bits(e[2], w[2]) and same_bits(e[3], w[0])
+    assert np.all(e[4] == 0) and np.all(e[5] == 0)
