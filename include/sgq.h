@@ -210,6 +210,70 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
                     const void* packed_up, const float* scales_up, const float* devscales_up, const float* bias_up,
                     int64_t group_size, float* h, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- quantized LLaMA block, one decode step ---------------------------- */
+
+/* One INT4 projection in the tiled layout (written by sgq_quantize_int4 /
+ * sgq_pack_int4), with its bias row (NULL: no bias add). */
+typedef struct sgq_int4_linear {
+    const void* packed;
+    const float* devscales;
+    const float* bias;
+} sgq_int4_linear;
+
+/* LLaMABlock (include/sovereigngrad/models.hpp:197-224) with every nn::Linear
+ * a QuantizedLinear4Bit (nn.hpp:965-1001) of one group size:
+ *   q, k, v, o: [D, D] (CausalSelfAttention, nn.hpp:503-553)
+ *   gate, up: [D, H]; down: [H, D] (SwiGLU, nn.hpp:135-156)
+ *   norm1, norm2: the RMSNorm weights [D] (nn.hpp:67-85), eps their epsilon
+ *   attn_scale: CausalSelfAttention::scale, 1 / sqrt((float)(D / num_heads))
+ *     (nn.hpp:518); the reference attends over the full width D.
+ * D and H must be multiples of 8 and group_size a multiple of 8 (the tiled
+ * layout), D <= 8192. */
+typedef struct sgq_llama_block_int4 {
+    int64_t D, H, group_size;
+    float eps, attn_scale;
+    const float* norm1;
+    const float* norm2;
+    sgq_int4_linear q, k, v, o, gate, up, down;
+} sgq_llama_block_int4;
+
+/* Workspace bytes of sgq_llama_block_decode_int4 for B sequences, widths D
+ * and H, and at most max_len keys per sequence in the step. */
+int64_t sgq_llama_decode_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t max_len);
+
+/* One decode step of the block for B sequences, one new token each.
+ * Replaces LLaMABlock::forward (models.hpp:217-222) on the last row of each
+ * sequence: the reference reruns the whole sequence (NanoLLaMA::generate,
+ * models.hpp:270-302); here the keys and values of earlier positions are kept
+ * in a cache, so the step computes
+ *   h   = x + o(attention(q(n1), K, V)),          n1 = rms_norm(x, norm1)
+ *   out = h + down(silu(gate(n2)) * up(n2)),       n2 = rms_norm(h, norm2)
+ * where attention is CausalSelfAttention's last row (nn.hpp:545-552): softmax
+ * over positions 0..pos[b] of (q . k_j) * attn_scale, applied to v_j.
+ *   x, out:    [B, D]; out may be x (in-place update of the hidden state).
+ *   k_cache, v_cache: [B][max_tokens][D] fp32, 16-byte aligned; rows 0..pos[b]-1
+ *              hold the keys/values of earlier positions.  The step writes
+ *              row pos[b] (this token's key and value).
+ *   pos:       [B] int32 on the device: tokens already cached per sequence.
+ *              The caller advances it after the step (every layer of one step
+ *              uses the same positions).
+ *   max_len:   host bound on pos[b] + 1 for this step (sizes the launch),
+ *              1 <= max_len <= max_tokens.  A sequence whose pos[b] is
+ *              negative or >= min(max_len, max_tokens) gets a NaN output row
+ *              and no cache write.
+ *   workspace: sgq_llama_decode_workspace_bytes(B, D, H, max_len) bytes,
+ *              16-byte aligned.
+ * B <= 16 runs every projection on the GEMV (q, k, v in one launch; the
+ * residual adds in the epilogues); larger B on the MFMA GEMM.  fp32 throughout;
+ * outputs match the reference's full-sequence forward within 1e-5 relative. */
+int sgq_llama_block_decode_int4(const sgq_llama_block_int4* block, const float* x, float* out, int64_t B,
+                                float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,
+                                int64_t max_len, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Replaces rms_norm (src/ops.cpp:1532-1556) for rows of [rows, D]:
+ * out = x * (1 / sqrt(sum(x^2) / D + eps)) * g.  out may be x. */
+int sgq_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float eps, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

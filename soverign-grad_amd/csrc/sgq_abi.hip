@@ -84,6 +84,40 @@ int64_t swiglu_ws_bytes(bool flat, int64_t M, int64_t K, int64_t N) {
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
+// LLaMA block decode workspace, each region 256-byte aligned:
+//   n [B*D] | qkv [3*B*D] | ctx [B*D] | h [B*D] | hid [B*H] | tmp [B*max(D,H)]
+//   | attention partials | GEMM split-K partials (B > 16 only)
+struct DecodeWs {
+    int64_t n, qkv, ctx, h, hid, tmp, part, split, total;
+};
+DecodeWs decode_ws(int64_t B, int64_t D, int64_t H, int64_t max_len) {
+    DecodeWs w;
+    int64_t o = 0;
+    auto take = [&](int64_t floats) {
+        const int64_t at = o;
+        o += align_up((floats > 0 ? floats : 1) * 4);
+        return at;
+    };
+    w.n = take(B * D);
+    w.qkv = take(3 * B * D);
+    w.ctx = take(B * D);
+    w.h = take(B * D);
+    w.hid = take(B * H);
+    w.tmp = take(B * (D > H ? D : H));
+    w.part = take(attn_workspace_floats(B, D, max_len));
+    int64_t split = 0;
+    if (B > kGemvMaxM) {
+        const int64_t a = gemm_workspace_bytes(B, D, D), b = gemm_workspace_bytes(B, D, H),
+                      c = gemm_workspace_bytes(B, H, D);
+        split = a > b ? a : b;
+        split = split > c ? split : c;
+    }
+    w.split = o;
+    o += align_up(split > 0 ? split : 1);
+    w.total = o;
+    return w;
+}
+
 bool bad_dims(int64_t a, int64_t b) { return a < 0 || b < 0 || a > kMaxDim || b > kMaxDim || a * b > ((int64_t)1 << 40); }
 
 int check_codes_flag(const int* dflag, hipStream_t s) {
@@ -468,6 +502,109 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
     SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_gate, devscales_gate, g, bias_gate, h, split, s), "gemm_i4");
     SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_up, devscales_up, g, bias_up, u, split, s), "gemm_i4");
     SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+    return ok();
+}
+
+int64_t sgq_llama_decode_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_t max_len) {
+    if (B < 0 || D <= 0 || H <= 0 || max_len < 1 || bad_dims(B, D) || bad_dims(B, H) || bad_dims(max_len, D))
+        return -1;
+    return decode_ws(B, D, H, max_len).total;
+}
+
+int sgq_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float eps, float* out, void* stream) {
+    if (bad_dims(rows, D)) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_rms_norm: bad shape");
+    if (rows == 0 || D == 0) return ok();
+    if (!x || !g || !out) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_rms_norm: null pointer");
+    SGQ_HIP(launch_rms_norm(x, rows, D, g, eps, out, (hipStream_t)stream), "rms_norm");
+    return ok();
+}
+
+int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x, float* out, int64_t B,
+                                float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,
+                                int64_t max_len, void* workspace, int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    const char* fn = "sgq_llama_block_decode_int4";
+    if (!blk) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null block", fn);
+    const int64_t D = blk->D, H = blk->H, G = blk->group_size;
+    if (B < 0 || D <= 0 || H <= 0 || bad_dims(B, D) || bad_dims(B, H) || bad_dims(D, H))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad shape", fn);
+    if (max_tokens < 1 || max_len < 1 || max_len > max_tokens || bad_dims(max_tokens, D))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: need 1 <= max_len <= max_tokens", fn);
+    if (D > 8192) return fail(SGQ_ERR_UNSUPPORTED, "%s: D > 8192", fn);
+    const I4Geom gdd(D, D, G), gdh(D, H, G), ghd(H, D, G);
+    if (!gdd.tiled || !gdh.tiled || !ghd.tiled)
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: D, H and group_size must be multiples of 8 (tiled INT4 layout)", fn);
+    const sgq_int4_linear* lin[7] = {&blk->q, &blk->k, &blk->v, &blk->o, &blk->gate, &blk->up, &blk->down};
+    for (int i = 0; i < 7; ++i) {
+        if (!lin[i]->packed || !lin[i]->devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null weight", fn);
+        if (!aligned16(lin[i]->packed) || !aligned16(lin[i]->devscales))
+            return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
+    }
+    if (!blk->norm1 || !blk->norm2) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null norm weight", fn);
+    if (B == 0) return ok();
+    if (!x || !out || !k_cache || !v_cache || !pos) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    if (!aligned16(k_cache) || !aligned16(v_cache))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", fn);
+    const DecodeWs w = decode_ws(B, D, H, max_len);
+    if (!workspace || workspace_bytes < w.total || !aligned16(workspace))
+        return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes, 16-byte aligned", fn, (long long)w.total);
+    char* base = (char*)workspace;
+    float* n = (float*)(base + w.n);
+    float* qkv = (float*)(base + w.qkv);
+    float* ctx = (float*)(base + w.ctx);
+    float* h = (float*)(base + w.h);
+    float* hid = (float*)(base + w.hid);
+    float* tmp = (float*)(base + w.tmp);
+    float* part = (float*)(base + w.part);
+    void* split = base + w.split;
+
+    // attn->forward(norm1->forward(x)), then the residual: h = x + o(ctx)
+    SGQ_HIP(launch_rms_norm(x, B, D, blk->norm1, blk->eps, n, s), "rms_norm");
+    if (B <= kGemvMaxM) {
+        const void* pk[3] = {blk->q.packed, blk->k.packed, blk->v.packed};
+        const float* ds[3] = {blk->q.devscales, blk->k.devscales, blk->v.devscales};
+        const float* bs[3] = {blk->q.bias, blk->k.bias, blk->v.bias};
+        SGQ_HIP(launch_gemv_i4_multi(n, B, D, D, 3, pk, ds, bs, gdd, qkv, 3 * D, nullptr, s), "gemv_qkv");
+        SGQ_HIP(launch_attention_decode(qkv, qkv + D, qkv + 2 * D, 3 * D, B, D, k_cache, v_cache, max_tokens, pos,
+                                        max_len, blk->attn_scale, part, ctx, s),
+                "attention");
+        SGQ_HIP(launch_gemv_i4_multi(ctx, B, D, D, 1, &blk->o.packed, &blk->o.devscales, &blk->o.bias, gdd, h, D, x,
+                                     s),
+                "gemv_o");
+    } else {
+        float* qb = qkv;
+        float* kb = qkv + B * D;
+        float* vb = qkv + 2 * B * D;
+        SGQ_HIP(launch_gemm_i4(n, B, D, D, blk->q.packed, blk->q.devscales, gdd, blk->q.bias, qb, split, s), "gemm_q");
+        SGQ_HIP(launch_gemm_i4(n, B, D, D, blk->k.packed, blk->k.devscales, gdd, blk->k.bias, kb, split, s), "gemm_k");
+        SGQ_HIP(launch_gemm_i4(n, B, D, D, blk->v.packed, blk->v.devscales, gdd, blk->v.bias, vb, split, s), "gemm_v");
+        SGQ_HIP(launch_attention_decode(qb, kb, vb, D, B, D, k_cache, v_cache, max_tokens, pos, max_len,
+                                        blk->attn_scale, part, ctx, s),
+                "attention");
+        SGQ_HIP(launch_gemm_i4(ctx, B, D, D, blk->o.packed, blk->o.devscales, gdd, blk->o.bias, tmp, split, s),
+                "gemm_o");
+        SGQ_HIP(launch_add(x, tmp, h, B * D, s), "add");
+    }
+    // h + mlp->forward(norm2->forward(h))
+    SGQ_HIP(launch_rms_norm(h, B, D, blk->norm2, blk->eps, n, s), "rms_norm");
+    if (B <= kGemvMaxM) {
+        SGQ_HIP(launch_swiglu_gemv_i4(n, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
+                                      blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s),
+                "swiglu_gemv");
+        SGQ_HIP(launch_gemv_i4_multi(hid, B, H, D, 1, &blk->down.packed, &blk->down.devscales, &blk->down.bias, ghd,
+                                     out, D, h, s),
+                "gemv_down");
+    } else {
+        SGQ_HIP(launch_gemm_i4(n, B, D, H, blk->gate.packed, blk->gate.devscales, gdh, blk->gate.bias, hid, split, s),
+                "gemm_gate");
+        SGQ_HIP(launch_gemm_i4(n, B, D, H, blk->up.packed, blk->up.devscales, gdh, blk->up.bias, tmp, split, s),
+                "gemm_up");
+        SGQ_HIP(launch_silu_mul(hid, tmp, B * H, s), "silu_mul");
+        SGQ_HIP(launch_gemm_i4(hid, B, H, D, blk->down.packed, blk->down.devscales, ghd, blk->down.bias, tmp, split,
+                               s),
+                "gemm_down");
+        SGQ_HIP(launch_add(h, tmp, out, B * D, s), "add");
+    }
     return ok();
 }
 

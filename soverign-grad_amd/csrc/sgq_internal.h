@@ -101,6 +101,12 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
                           bool per_tensor, const float* bias, float* y, hipStream_t s);
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
+// nw (1..3) tiled INT4 weights of one shape [K, N] side by side on one input:
+// weight w writes y[m * ldy + w * N + n] (+ res at the same index when res is
+// set).  Strip layout only; M <= kGemvMaxM.
+hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N, int nw, const void* const* packed,
+                                const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
+                                int64_t ldy, const float* res, hipStream_t s);
 // MFMA GEMM (M > kGemvMaxM).  Grids with fewer 128x128 tiles than CUs split K
 // over workgroups; their partial tiles go to ws (gemm_workspace_bytes(M, K, N)
 // bytes, 0 when K is not split) and a second kernel adds them in fixed order.
@@ -130,5 +136,24 @@ hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
                                  hipStream_t s);
 hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s);
+
+// ---- LLaMA block decode step (sgq_decode.hip) ---------------------------
+hipError_t launch_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float eps, float* out,
+                           hipStream_t s);
+hipError_t launch_add(const float* a, const float* b, float* y, int64_t n, hipStream_t s);
+// Attention of one new token per sequence over its cache: keys split into
+// NC chunks of CS, combined by a second kernel when NC > 1.
+constexpr int kAttnMaxChunk = 64;
+struct AttnPlan {
+    int CS, NC;
+};
+AttnPlan attn_plan(int64_t B, int64_t max_len);
+int64_t attn_workspace_floats(int64_t B, int64_t D, int64_t max_len);
+// q, knew, vnew: rows of B sequences with row stride ldq; kc, vc: [B][max_tokens][D];
+// pos[b]: cached positions of sequence b before this step (the new row goes
+// to pos[b]); part: attn_workspace_floats floats; ctx: [B, D].
+hipError_t launch_attention_decode(const float* q, const float* knew, const float* vnew, int64_t ldq, int64_t B,
+                                   int64_t D, float* kc, float* vc, int64_t max_tokens, const int32_t* pos,
+                                   int64_t max_len, float scale, float* part, float* ctx, hipStream_t s);
 
 }  // namespace sgq

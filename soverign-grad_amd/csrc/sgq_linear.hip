@@ -188,6 +188,19 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
     return (b % kXcds) * per + b / kXcds;
 }
 
+// Arguments of one GEMV launch (passed by value in the kernel arguments).
+struct GemvArgs {
+    const float* x;  // [M, K] rows of this pass
+    int M, K, N;     // N: columns of one weight
+    const uint4* W[3];
+    const float* SC[3];
+    const float* bias[3];
+    int mode, Kpad, RQ, NS;  // NS: strips of one weight
+    const float* res;        // added to the output (same indexing), or null
+    float* y;
+    int ldy;                 // row stride of y and res
+};
+
 // ---------------------------------------------------------------------------
 // GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup of NW
 // wavefronts per strip (all K rows of SW columns): BITS 4 -> 8 columns,
@@ -208,14 +221,16 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
 // share their INT4 scale column: spc % SPW == 0) load each x and scale quad
 // once for all of them: fewer load instructions per code byte, which is what
 // bounds the single-row GEMV.
+//
+// With NG == 1, a.nw weights of equal shape may sit side by side along the
+// output (a LLaMA block's q, k and v projections of one input): workgroup
+// strips run over all of them and weight w writes columns w*N .. w*N+N-1 of
+// y.  a.res, when set, is added to every output (a residual connection).
 template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW>
-__global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__ x, int M, int K, int N,
-                                                       const uint4* __restrict__ W, const float* __restrict__ SC,
-                                                       const uint4* __restrict__ W2, const float* __restrict__ SC2,
-                                                       int mode, int Kpad, int RQ, int NS,
-                                                       const float* __restrict__ bias,
-                                                       const float* __restrict__ bias2, float* __restrict__ y) {
+__global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     static_assert(NG == 1 || SPW == 1, "the gated form takes one strip of each weight");
+    const float* __restrict__ x = a.x;
+    const int M = a.M, K = a.K, N = a.N, mode = a.mode, Kpad = a.Kpad, RQ = a.RQ, NS = a.NS;
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
     constexpr int RQ_IT = NW * 64;           // row quads per group iteration
     constexpr int CW = SPW * SW;             // columns per workgroup
@@ -225,10 +240,19 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
     const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
-    const int j0 = SPW * xcd_swizzle(blockIdx.x, gridDim.x);  // strips of a scale column share an XCD's L2
+    // Strips of a scale column share an XCD's L2.  Workgroups of one weight
+    // cover (NS + SPW - 1) / SPW strip groups; with several weights side by
+    // side (NG == 1), wt selects the weight.
+    const int jg = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int per_w = (NS + SPW - 1) / SPW;
+    const int wt = NG == 1 ? jg / per_w : 0;
+    const int j0 = SPW * (jg - wt * per_w);
+    const int widx = NG == 1 ? wt : grp;
+    const uint4* __restrict__ Wm = widx == 0 ? a.W[0] : (widx == 1 ? a.W[1] : a.W[2]);
+    const float* __restrict__ SCm = widx == 0 ? a.SC[0] : (widx == 1 ? a.SC[1] : a.SC[2]);
+    const float* __restrict__ bias = NG == 1 ? (wt == 0 ? a.bias[0] : (wt == 1 ? a.bias[1] : a.bias[2])) : a.bias[0];
+    const float* __restrict__ bias2 = a.bias[1];
     const int voff = gtid * 16;
-    const uint4* __restrict__ Wm = grp ? W2 : W;
-    const float* __restrict__ SCm = grp ? SC2 : SC;
 
     __amdgpu_buffer_rsrc_t rW[SPW];
 #pragma unroll
@@ -329,6 +353,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
         const int m = v / CW, e = v - m * CW;
         const int n = j0 * SW + e;
         if (m < M && n < N) {
+            const int64_t o = (int64_t)m * a.ldy + (int64_t)wt * N + n;
             float r = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) r += red[w][v];
@@ -342,7 +367,8 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const float* __restrict__
                 if (bias2) r2 = r2 + bias2[n];
                 r = silu_f32(r) * r2;
             }
-            y[(int64_t)m * N + n] = r;
+            if (a.res) r = r + a.res[o];
+            a.y[o] = r;
         }
     }
 }
@@ -617,25 +643,13 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
 
 bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
 
-// One weight operand of the GEMV: packed codes, scales in the kernel's mode, bias.
-struct GemvWeight {
-    const void* packed;
-    const float* sc;
-    const float* bias;
-};
-
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
-hipError_t gemv_launch_nu(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad,
-                          int RQ, int NS, float* y, hipStream_t s) {
-    const dim3 grid((unsigned)((NS + SPW - 1) / SPW));
-    if (K % 4 == 0)
-        k_gemv<BITS, MT, NW, U, true, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(
-            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, NS, w.bias,
-            w2.bias, y);
+hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
+    const dim3 grid((unsigned)(nw * ((a.NS + SPW - 1) / SPW)));
+    if (a.K % 4 == 0)
+        k_gemv<BITS, MT, NW, U, true, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(a);
     else
-        k_gemv<BITS, MT, NW, U, false, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(
-            x, M, K, N, (const uint4*)w.packed, w.sc, (const uint4*)w2.packed, w2.sc, mode, Kpad, RQ, NS, w.bias,
-            w2.bias, y);
+        k_gemv<BITS, MT, NW, U, false, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -645,6 +659,9 @@ hipError_t gemv_launch_nu(const float* x, int M, int K, int N, GemvWeight w, Gem
 // cross-wave LDS reduction short.
 constexpr int kGemvWaves = 4;
 
+// Strips per workgroup for MT <= SGQ_GEMV_SPW_MAXMT.  Measured on MI355X at
+// M=1: 2 strips x 8 wavefronts is 7% faster on 4096->11008 but 13-18% slower
+// on 11008->4096 and 2048->2048 (half the workgroups), so the default is 1.
 #ifndef SGQ_GEMV_SPW
 #define SGQ_GEMV_SPW 1
 #endif
@@ -656,15 +673,14 @@ constexpr int kGemvWaves = 4;
 #endif
 
 template <int BITS, int MT, int NG, int SPW, int NW>
-hipError_t gemv_launch_spw(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad,
-                           int RQ, int NS, float* y, hipStream_t s) {
+hipError_t gemv_launch_spw(const GemvArgs& a, int nw, hipStream_t s) {
     // Register budget: row quads in flight per lane shrink as the batch grows.
     constexpr int UMAX = (MT * SPW <= 2) ? 4 : (MT * SPW <= 4 ? 2 : 1);
-    const int per_lane = (RQ + NW * 64 - 1) / (NW * 64);
+    const int per_lane = (a.RQ + NW * 64 - 1) / (NW * 64);
     const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
-#define SGQ_GEMV_NU(U_)                                                                                      \
-    if ((u >= U_ || U_ == 1) && U_ <= UMAX)                                                                \
-        return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
+#define SGQ_GEMV_NU(U_)                                        \
+    if ((u >= U_ || U_ == 1) && U_ <= UMAX)                  \
+        return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s);
     SGQ_GEMV_NU(4)
     SGQ_GEMV_NU(2)
     SGQ_GEMV_NU(1)
@@ -673,61 +689,98 @@ hipError_t gemv_launch_spw(const float* x, int M, int K, int N, GemvWeight w, Ge
 }
 
 template <int BITS, int MT, int NG>
-hipError_t gemv_launch(const float* x, int M, int K, int N, GemvWeight w, GemvWeight w2, int mode, int Kpad, int RQ,
-                       int NS, float* y, hipStream_t s) {
+hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
     if constexpr (NG == 1 && SGQ_GEMV_SPW > 1 && MT <= SGQ_GEMV_SPW_MAXMT) {
         // INT4 strips of one workgroup must share a scale column.
-        if (BITS == 8 || mode % SGQ_GEMV_SPW == 0)
-            return gemv_launch_spw<BITS, MT, NG, SGQ_GEMV_SPW, SGQ_GEMV_SPW_WAVES>(x, M, K, N, w, w2, mode, Kpad, RQ,
-                                                                                NS, y, s);
+        if (nw == 1 && (BITS == 8 || a.mode % SGQ_GEMV_SPW == 0))
+            return gemv_launch_spw<BITS, MT, NG, SGQ_GEMV_SPW, SGQ_GEMV_SPW_WAVES>(a, nw, s);
     }
-    return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(x, M, K, N, w, w2, mode, Kpad, RQ, NS, y, s);
+    return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(a, nw, s);
 }
 
 // Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
 template <int BITS, int NG>
-hipError_t gemv_dispatch(const float* x, int64_t M, int64_t K, int64_t N, GemvWeight w, GemvWeight w2, int mode,
-                         int64_t Kpad, int64_t RQ, int64_t NS, float* y, hipStream_t s) {
-    const int k = (int)K, n = (int)N, kp = (int)Kpad, rq = (int)RQ, ns = (int)NS;
+hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
+    const float* x = a.x;
+    float* y = a.y;
+    const float* res = a.res;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
-        const int m = (int)((M - m0) < 8 ? (M - m0) : 8);
-        const float* xm = x + m0 * K;
-        float* ym = y + m0 * N;
+        a.M = (int)((M - m0) < 8 ? (M - m0) : 8);
+        a.x = x + m0 * a.K;
+        a.y = y + m0 * a.ldy;
+        a.res = res ? res + m0 * a.ldy : nullptr;
         hipError_t e;
-        if (m <= 1)
-            e = gemv_launch<BITS, 1, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
-        else if (m <= 2)
-            e = gemv_launch<BITS, 2, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
-        else if (m <= 4)
-            e = gemv_launch<BITS, 4, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
+        if (a.M <= 1)
+            e = gemv_launch<BITS, 1, NG>(a, nw, s);
+        else if (a.M <= 2)
+            e = gemv_launch<BITS, 2, NG>(a, nw, s);
+        else if (a.M <= 4)
+            e = gemv_launch<BITS, 4, NG>(a, nw, s);
         else
-            e = gemv_launch<BITS, 8, NG>(xm, m, k, n, w, w2, mode, kp, rq, ns, ym, s);
+            e = gemv_launch<BITS, 8, NG>(a, nw, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad, int64_t RQ, int64_t NS, float* y,
+                   int64_t ldy, const float* res) {
+    GemvArgs a{};
+    a.x = x;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.mode = mode;
+    a.Kpad = (int)Kpad;
+    a.RQ = (int)RQ;
+    a.NS = (int)NS;
+    a.y = y;
+    a.ldy = (int)ldy;
+    a.res = res;
+    return a;
 }
 
 }  // namespace
 
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
-    const GemvWeight w{packed, devscales, bias};
-    return gemv_dispatch<4, 1>(x, M, K, N, w, w, (int)g.spc, g.Kpad, g.RQ, g.NS, y, s);
+    return launch_gemv_i4_multi(x, M, K, N, 1, &packed, &devscales, &bias, g, y, N, nullptr, s);
+}
+
+hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N, int nw, const void* const* packed,
+                                const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
+                                int64_t ldy, const float* res, hipStream_t s) {
+    if (nw < 1 || nw > 3) return hipErrorInvalidValue;
+    GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, y, ldy, res);
+    for (int w = 0; w < nw; ++w) {
+        a.W[w] = (const uint4*)packed[w];
+        a.SC[w] = devscales[w];
+        a.bias[w] = bias[w];
+    }
+    return gemv_dispatch<4, 1>(a, M, nw, s);
 }
 
 hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, hipStream_t s) {
     I8Geom g(K, N);
-    const GemvWeight w{packed, scales, bias};
-    return gemv_dispatch<8, 1>(x, M, K, N, w, w, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, y, s);
+    GemvArgs a = gemv_args(x, K, N, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, y, N, nullptr);
+    a.W[0] = (const uint4*)packed;
+    a.SC[0] = scales;
+    a.bias[0] = bias;
+    return gemv_dispatch<8, 1>(a, M, 1, s);
 }
 
 hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
                                  hipStream_t s) {
-    return gemv_dispatch<4, 2>(x, M, K, N, GemvWeight{packed_g, devscales_g, bias_g},
-                               GemvWeight{packed_u, devscales_u, bias_u}, (int)g.spc, g.Kpad, g.RQ, g.NS, h, s);
+    GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, h, N, nullptr);
+    a.W[0] = (const uint4*)packed_g;
+    a.W[1] = (const uint4*)packed_u;
+    a.SC[0] = devscales_g;
+    a.SC[1] = devscales_u;
+    a.bias[0] = bias_g;
+    a.bias[1] = bias_u;
+    return gemv_dispatch<4, 2>(a, M, 1, s);
 }
 
 hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
@@ -735,8 +788,14 @@ hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N
                                  const float* scales_u, const float* bias_u, bool per_tensor, float* h,
                                  hipStream_t s) {
     I8Geom g(K, N);
-    return gemv_dispatch<8, 2>(x, M, K, N, GemvWeight{packed_g, scales_g, bias_g},
-                               GemvWeight{packed_u, scales_u, bias_u}, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, h, s);
+    GemvArgs a = gemv_args(x, K, N, per_tensor ? 1 : 0, g.Kpad, g.RQ, g.NS, h, N, nullptr);
+    a.W[0] = (const uint4*)packed_g;
+    a.W[1] = (const uint4*)packed_u;
+    a.SC[0] = scales_g;
+    a.SC[1] = scales_u;
+    a.bias[0] = bias_g;
+    a.bias[1] = bias_u;
+    return gemv_dispatch<8, 2>(a, M, 1, s);
 }
 
 hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {

@@ -99,6 +99,54 @@ def test_swiglu_argument_errors_before_gpu(lib):
                                None) == 1
 
 
+def _block_struct(D, H, G, ptr=16):
+    import soverign_grad_amd.decode as dm
+
+    st = dm.LlamaBlockInt4()
+    st.D, st.H, st.group_size, st.eps, st.attn_scale = D, H, G, 1e-5, 0.125
+    st.norm1 = st.norm2 = ptr
+    for f in ("q", "k", "v", "o", "gate", "up", "down"):
+        setattr(st, f, dm.Int4Linear(ptr, ptr, None))
+    return st
+
+
+def test_llama_decode_sizes_and_errors(lib, sgq):
+    import ctypes
+
+    # Workspace: normed input, q|k|v, context, h, MLP hidden, a projection
+    # output, attention partials (several key chunks), split-K partials (B > 16).
+    w1 = lib.sgq_llama_decode_workspace_bytes(8, 2048, 5632, 64)
+    assert w1 >= 4 * (8 * 2048 * 7 + 8 * 5632 * 2)
+    assert lib.sgq_llama_decode_workspace_bytes(8, 2048, 5632, 4096) > w1  # more key chunks
+    assert lib.sgq_llama_decode_workspace_bytes(32, 2048, 5632, 64) > lib.sgq_llama_decode_workspace_bytes(16, 2048,
+                                                                                                             5632, 64)
+    assert lib.sgq_llama_decode_workspace_bytes(1, 0, 8, 1) == -1
+    assert lib.sgq_llama_decode_workspace_bytes(1, 8, 8, 0) == -1
+    st = _block_struct(64, 128, 32)
+    need = lib.sgq_llama_decode_workspace_bytes(2, 64, 128, 4)
+    call = lambda blk, B=2, mt=8, ml=4, ws=16, nws=need, kc=256: lib.sgq_llama_block_decode_int4(
+        None if blk is None else ctypes.byref(blk), 16, 16, B, kc, kc, mt, 16, ml, ws, nws, None)
+    assert call(None) == 1
+    assert call(st, ml=9) == 1 and b"max_len" in lib.sgq_last_error()  # max_len > max_tokens
+    assert call(st, ml=0) == 1
+    assert call(st, ws=None) == 3 and str(need).encode() in lib.sgq_last_error()
+    assert call(st, nws=need - 4) == 3
+    assert call(st, kc=260) == 1 and b"aligned" in lib.sgq_last_error()
+    assert call(st, B=0) == 0  # nothing to do
+    assert call(_block_struct(60, 128, 32)) == 2  # D not a multiple of 8: no tiled layout
+    assert call(_block_struct(64, 128, 12)) == 2  # group size not a multiple of 8
+    assert call(_block_struct(16384, 128, 32)) == 2
+    bad = _block_struct(64, 128, 32)
+    bad.up = type(bad.up)(16, None, None)
+    assert call(bad) == 1 and b"null weight" in lib.sgq_last_error()
+    mis = _block_struct(64, 128, 32)
+    mis.down = type(mis.down)(24, 16, None)
+    assert call(mis) == 1 and b"aligned" in lib.sgq_last_error()
+    assert lib.sgq_rms_norm(None, -1, 4, None, ctypes.c_float(1e-5), None, None) == 1
+    assert lib.sgq_rms_norm(None, 0, 4, None, ctypes.c_float(1e-5), None, None) == 0
+    assert lib.sgq_rms_norm(None, 2, 4, 16, ctypes.c_float(1e-5), 16, None) == 1
+
+
 def test_argument_errors_before_gpu(lib, sgq):
     # Each of these fails validation on the host; nothing reaches the GPU.
     assert lib.sgq_quantize_int8(None, -1, 4, 0, None, None, None, None, 0, None) == 1
