@@ -17,6 +17,7 @@ absent) timed on this host under "cpu_baseline".
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -460,6 +461,84 @@ def decode_step(pkg, dev, oracle, steps, fused=False):
             "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "rel_err_vs_oracle": err}
 
 
+def block_decode_step(pkg, dev, oracle, steps, ctx_len):
+    """A real decode step of the 22-layer NanoLLaMA-shaped model with INT4 g128
+    projections: per layer RMSNorm, q/k/v, attention of the new token over
+    ctx_len cached positions (fp32 KV cache), out projection + residual,
+    RMSNorm, gated MLP, down projection + residual (sgq_llama_block_decode_int4),
+    batch 8.  Each layer has its own weight copy and its own cache.  Parity:
+    layer 0 decodes 3 tokens of 8 sequences from an empty cache against the
+    oracle's full-sequence block."""
+    import torch
+    import soverign_grad_amd.decode as dm
+    from soverign_grad_amd import synth
+    from oracle.oracle import BLOCK_PROJ
+
+    D, H, heads, G, B, L = 2048, 5632, 16, C5_G, C5_M, C5_LAYERS
+    seed = synth.config_seed(5)
+    shapes = dm.projection_shapes(D, H)
+    W = {k: synth_normal(shapes[k], seed + i, synth.STREAM_W, 0.0, 0.02) for i, k in enumerate(BLOCK_PROJ)}
+    bias = {k: synth_normal((shapes[k][1],), seed + i, synth.STREAM_BIAS, 0.0, 0.02) for i, k in enumerate(BLOCK_PROJ)}
+    g1 = (1.0 + synth_normal((D,), seed + 10, synth.STREAM_BIAS, 0.0, 0.1)).astype(np.float32)
+    g2 = (1.0 + synth_normal((D,), seed + 11, synth.STREAM_BIAS, 0.0, 0.1)).astype(np.float32)
+    t0 = time.time()
+    blk0 = dm.QuantizedLLaMABlock.from_float({k: torch.from_numpy(v).to(dev) for k, v in W.items()},
+                                             {k: torch.from_numpy(v).to(dev) for k, v in bias.items()},
+                                             torch.from_numpy(g1).to(dev), torch.from_numpy(g2).to(dev), heads, G)
+
+    # Parity on layer 0 from an empty cache.
+    xs = synth.normal((B, 3, D), seed + 20, synth.STREAM_X)
+    cache = dm.KVCache(B, 8, D, dev)
+    got = np.zeros((B, 3, D), np.float32)
+    for t in range(3):
+        cache.pos.fill_(t)
+        got[:, t] = blk0.decode(torch.from_numpy(np.ascontiguousarray(xs[:, t])).to(dev), cache.k[0], cache.v[0],
+                                cache.pos, t + 1).cpu().numpy()
+    codes = {k: pkg.unpack_codes(blk0.weights[k]).cpu().numpy() for k in BLOCK_PROJ}
+    scs = {k: blk0.weights[k].scales.cpu().numpy() for k in BLOCK_PROJ}
+    err = 0.0
+    for b in (0, B - 1):
+        ref = oracle.qllama_block_int4(xs[b], [(codes[k], scs[k], bias[k]) for k in BLOCK_PROJ], g1, g2, 1e-5,
+                                       blk0.attn_scale, G)
+        err = max(err, float(np.max(np.abs(got[b] - ref)) / np.max(np.abs(ref))))
+    del cache
+
+    # 22 layers, each with its own packed weights (copies of layer 0) and cache.
+    blocks = [blk0]
+    for _ in range(L - 1):
+        w = {k: dataclasses.replace(q, packed=q.packed.clone(), devscales=q.devscales.clone())
+             for k, q in blk0.weights.items()}
+        blocks.append(dm.QuantizedLLaMABlock(D, H, heads, G, w, blk0.biases, blk0.norm1, blk0.norm2))
+    Tmax = ctx_len + 1
+    cache = dm.KVCache(B, Tmax, D, dev, layers=L)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    for i in range(L):
+        cache.k[i].normal_(0.0, 1.0, generator=gen)
+        cache.v[i].normal_(0.0, 1.0, generator=gen)
+    cache.pos.fill_(ctx_len)  # ctx_len cached positions; the new token is position ctx_len
+    x = torch.from_numpy(synth.normal((B, D), seed + 21, synth.STREAM_X)).to(dev)
+    h = torch.empty_like(x)
+    torch.cuda.synchronize()
+    log(f"[bench] block decode: set up {L} layers, cache {ctx_len} positions in {time.time() - t0:.1f}s")
+
+    def body(_i):
+        dm.decode_layers(blocks, x, cache, ctx_len + 1, out=h)
+
+    ms = _graph_ms(dev, body, steps)
+    assert bool(torch.isfinite(h).all())
+    wbytes = L * sum(K * N // 2 + 4 * (K * N // G) + 4 * N for K, N in shapes.values())
+    kvbytes = L * B * (ctx_len + 1) * D * 4 * 2
+    flops = L * B * 2 * sum(K * N for K, N in shapes.values())
+    del blocks, cache
+    return {"workload": f"NanoLLaMA-shaped decode step: 22 quantized LLaMA blocks (d_model {D}, hidden {H}, INT4 "
+                        f"g{G}), batch {B}, attention over {ctx_len} cached positions (fp32 KV cache)",
+            "us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(B / ms * 1e3, 1),
+            "weight_GB_s": round(wbytes / ms / 1e6, 1), "kv_GB_s": round(kvbytes / ms / 1e6, 1),
+            "hbm_frac": round((wbytes + kvbytes) / ms / 1e6 / HBM_PEAK_GBS, 4), "TFLOP_s": round(flops / ms / 1e9, 3),
+            "launches_per_layer": 8, "rel_err_vs_oracle": err}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -572,6 +651,14 @@ def main() -> int:
             key = f"c3_swiglu_m{M}"
             others[key] = swiglu_pair(pkg, dev, oracle, max(20, min(400, args.steps // 5)), M)
             log(f"[bench] {key}: {others[key]['us_per_call']} us/call, {others[key]['GB_s']} GB/s, "
+                f"rel_err {others[key]['rel_err_vs_oracle']:.2e}")
+            if others[key]["rel_err_vs_oracle"] > 1e-5:
+                raise SystemExit(f"parity failure in bench ({key})")
+            torch.cuda.empty_cache()
+        for ctx_len in (128, 1024):
+            key = f"c5_block_decode_ctx{ctx_len}"
+            others[key] = block_decode_step(pkg, dev, oracle, max(2, min(10, args.steps // 200)), ctx_len)
+            log(f"[bench] {key}: {others[key]['us_per_step']} us/step, {others[key]['tokens_per_s']} tok/s, "
                 f"rel_err {others[key]['rel_err_vs_oracle']:.2e}")
             if others[key]["rel_err_vs_oracle"] > 1e-5:
                 raise SystemExit(f"parity failure in bench ({key})")

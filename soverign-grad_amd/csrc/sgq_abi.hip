@@ -531,6 +531,8 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
     if (max_tokens < 1 || max_len < 1 || max_len > max_tokens || bad_dims(max_tokens, D))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: need 1 <= max_len <= max_tokens", fn);
     if (D > 8192) return fail(SGQ_ERR_UNSUPPORTED, "%s: D > 8192", fn);
+    if (max_len > attn_max_len())
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: max_len > %lld", fn, (long long)attn_max_len());
     const I4Geom gdd(D, D, G), gdh(D, H, G), ghd(H, D, G);
     if (!gdd.tiled || !gdh.tiled || !ghd.tiled)
         return fail(SGQ_ERR_UNSUPPORTED, "%s: D, H and group_size must be multiples of 8 (tiled INT4 layout)", fn);
@@ -558,20 +560,22 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
     float* part = (float*)(base + w.part);
     void* split = base + w.split;
 
-    // attn->forward(norm1->forward(x)), then the residual: h = x + o(ctx)
-    SGQ_HIP(launch_rms_norm(x, B, D, blk->norm1, blk->eps, n, s), "rms_norm");
+    // attn->forward(norm1->forward(x)), then the residual: h = x + o(ctx).
+    // The GEMV path applies each RMSNorm inside the projection that reads it.
     if (B <= kGemvMaxM) {
         const void* pk[3] = {blk->q.packed, blk->k.packed, blk->v.packed};
         const float* ds[3] = {blk->q.devscales, blk->k.devscales, blk->v.devscales};
         const float* bs[3] = {blk->q.bias, blk->k.bias, blk->v.bias};
-        SGQ_HIP(launch_gemv_i4_multi(n, B, D, D, 3, pk, ds, bs, gdd, qkv, 3 * D, nullptr, s), "gemv_qkv");
+        SGQ_HIP(launch_gemv_i4_multi(x, B, D, D, 3, pk, ds, bs, gdd, qkv, 3 * D, nullptr, blk->norm1, blk->eps, s),
+                "gemv_qkv");
         SGQ_HIP(launch_attention_decode(qkv, qkv + D, qkv + 2 * D, 3 * D, B, D, k_cache, v_cache, max_tokens, pos,
                                         max_len, blk->attn_scale, part, ctx, s),
                 "attention");
         SGQ_HIP(launch_gemv_i4_multi(ctx, B, D, D, 1, &blk->o.packed, &blk->o.devscales, &blk->o.bias, gdd, h, D, x,
-                                     s),
+                                     nullptr, 0.0f, s),
                 "gemv_o");
     } else {
+        SGQ_HIP(launch_rms_norm(x, B, D, blk->norm1, blk->eps, n, s), "rms_norm");
         float* qb = qkv;
         float* kb = qkv + B * D;
         float* vb = qkv + 2 * B * D;
@@ -586,15 +590,16 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
         SGQ_HIP(launch_add(x, tmp, h, B * D, s), "add");
     }
     // h + mlp->forward(norm2->forward(h))
-    SGQ_HIP(launch_rms_norm(h, B, D, blk->norm2, blk->eps, n, s), "rms_norm");
     if (B <= kGemvMaxM) {
-        SGQ_HIP(launch_swiglu_gemv_i4(n, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
-                                      blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s),
+        SGQ_HIP(launch_swiglu_gemv_i4(h, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
+                                      blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s, blk->norm2,
+                                      blk->eps),
                 "swiglu_gemv");
         SGQ_HIP(launch_gemv_i4_multi(hid, B, H, D, 1, &blk->down.packed, &blk->down.devscales, &blk->down.bias, ghd,
-                                     out, D, h, s),
+                                     out, D, h, nullptr, 0.0f, s),
                 "gemv_down");
     } else {
+        SGQ_HIP(launch_rms_norm(h, B, D, blk->norm2, blk->eps, n, s), "rms_norm");
         SGQ_HIP(launch_gemm_i4(n, B, D, H, blk->gate.packed, blk->gate.devscales, gdh, blk->gate.bias, hid, split, s),
                 "gemm_gate");
         SGQ_HIP(launch_gemm_i4(n, B, D, H, blk->up.packed, blk->up.devscales, gdh, blk->up.bias, tmp, split, s),

@@ -10,6 +10,7 @@
 // stay in a cache, so a step reads them once and computes only the new row,
 // which is the last row of the reference's causal attention.
 #include "sgq_internal.h"
+#include "sgq_lanes.h"
 
 namespace sgq {
 namespace {
@@ -80,78 +81,136 @@ __device__ __forceinline__ int seq_keys(const int32_t* pos, int b, int64_t max_t
 // into the cache.  With a single chunk (direct) the workgroup writes
 // ctx = o_c / l_c; otherwise (o_c, m_c, l_c) go to part[b][c] for
 // k_attn_combine.  D % 4 == 0; rows 16-byte aligned.
+//
+// Latency, not bandwidth, bounds a decode step's attention (a few keys per
+// workgroup), so every phase issues all of its loads before using any: the
+// scores split D over the four wavefronts (each lane holds its slice of q and
+// loads its slice of all CS keys at once), and the value sum loads KB keys'
+// rows per batch.
+template <int CS>
 __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ knew,
                                                          const float* __restrict__ vnew, int64_t ldq, int64_t D,
                                                          float* __restrict__ kc, float* __restrict__ vc,
                                                          int64_t max_tokens, const int32_t* __restrict__ pos,
-                                                         int64_t max_len, int CS, float scale,
+                                                         int64_t max_len, float scale,
                                                          float* __restrict__ part, float* __restrict__ ctx) {
-    extern __shared__ float smem[];  // q row (D floats), then CS scores
-    float* qs = smem;
-    float* sc = smem + D;
+    constexpr int NWV = kBlock / 64;
+    __shared__ float red[NWV][CS];
+    __shared__ float ex[CS];
     const int b = blockIdx.y, c = blockIdx.x, nc = gridDim.x;
     const int T = seq_keys(pos, b, max_tokens, max_len);
     const int j0 = c * CS;
     if (T < 0 || j0 >= T) return;  // combine reads only chunks below ceil(T / CS)
-    const int j1 = min(j0 + CS, T);
+    const int n = min(CS, T - j0);
     const int p = T - 1;  // the new position
-    const float* qrow = q + (int64_t)b * ldq;
     const float* kn = knew + (int64_t)b * ldq;
     const float* vn = vnew + (int64_t)b * ldq;
-    float* kcb = kc + (int64_t)b * max_tokens * D;
-    float* vcb = vc + (int64_t)b * max_tokens * D;
+    const float* kcb = kc + (int64_t)b * max_tokens * D;
+    const float* vcb = vc + (int64_t)b * max_tokens * D;
     const int64_t D4 = D / 4;
-
-    for (int64_t i = threadIdx.x; i < D4; i += kBlock) ((float4*)qs)[i] = ((const float4*)qrow)[i];
-    if (p >= j0 && p < j1) {  // this chunk holds the new position: append it to the cache
-        for (int64_t i = threadIdx.x; i < D4; i += kBlock) {
-            ((float4*)(kcb + (int64_t)p * D))[i] = ((const float4*)kn)[i];
-            ((float4*)(vcb + (int64_t)p * D))[i] = ((const float4*)vn)[i];
-        }
-    }
-    __syncthreads();
-
-    // Scores: one wavefront per key.
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int j = j0 + wave; j < j1; j += kBlock / 64) {
-        const float* kr = (j == p) ? kn : kcb + (int64_t)j * D;
-        float acc = 0.0f;
-        for (int64_t i = lane; i < D4; i += 64) {
-            const float4 kv = ((const float4*)kr)[i];
-            const float4 qv = ((const float4*)qs)[i];
-            acc = fmaf(qv.x, kv.x, acc);
-            acc = fmaf(qv.y, kv.y, acc);
-            acc = fmaf(qv.z, kv.z, acc);
-            acc = fmaf(qv.w, kv.w, acc);
+
+    // Scores: wavefront w sums dims [w * D4 / 4, (w + 1) * D4 / 4) (float4
+    // units) of every key; lanes stride over that slice, KB keys' loads at a
+    // time.  Keys past the chunk's n read the new row (always written memory)
+    // and their scores are never used.
+    constexpr int KB = CS < 8 ? CS : 8;
+    // The first KB value rows of this thread's first PC float4 columns are
+    // loaded now, so their latency overlaps the scores and the softmax.
+    constexpr int PC = 2;
+    float4 vpre[PC][KB];
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) {
+        const int64_t i = threadIdx.x + ci * kBlock;
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int j = j0 + u;
+            const float* vr = (u >= n || j == p) ? vn : vcb + (int64_t)j * D;
+            vpre[ci][u] = i < D4 ? ((const float4*)vr)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) sc[j - j0] = acc * scale;
+    }
+    const int64_t s0 = wave * ((D4 + NWV - 1) / NWV), s1 = min(D4, s0 + (D4 + NWV - 1) / NWV);
+    const float4* q4 = (const float4*)(q + (int64_t)b * ldq);
+    for (int t0 = 0; t0 < n; t0 += KB) {
+        float acc[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) acc[u] = 0.0f;
+        for (int64_t i = s0 + lane; i < s1; i += 64) {
+            const float4 qv = q4[i];
+            float4 kv[KB];
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                const int t = t0 + u, j = j0 + t;
+                const float* kr = (t >= n || j == p) ? kn : kcb + (int64_t)j * D;
+                kv[u] = ((const float4*)kr)[i];
+            }
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                acc[u] = fmaf(qv.x, kv[u].x, acc[u]);
+                acc[u] = fmaf(qv.y, kv[u].y, acc[u]);
+                acc[u] = fmaf(qv.z, kv[u].z, acc[u]);
+                acc[u] = fmaf(qv.w, kv[u].w, acc[u]);
+            }
+        }
+        // Halving butterfly over the wavefront (DPP / permlane steps): lane
+        // group `base` ends with the total of key t0 + base.
+        int base = 0;
+        lane_reduce<KB, 0>(acc, lane, base);
+        if ((lane & red_dup_mask(KB)) == 0) red[wave][t0 + base] = acc[0];
+    }
+    // The chunk holding the new position appends it to the cache (no other
+    // workgroup reads that row: they take it from knew / vnew).
+    if (p >= j0 && p < j0 + n) {
+        float4* kd = (float4*)(kc + ((int64_t)b * max_tokens + p) * D);
+        float4* vd = (float4*)(vc + ((int64_t)b * max_tokens + p) * D);
+        for (int64_t i = threadIdx.x; i < D4; i += kBlock) {
+            kd[i] = ((const float4*)kn)[i];
+            vd[i] = ((const float4*)vn)[i];
+        }
     }
     __syncthreads();
-
-    const int n = j1 - j0;
-    float m = -INFINITY;
-    for (int t = 0; t < n; ++t) m = fmaxf(m, sc[t]);
+    if (threadIdx.x < CS) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) v += red[w][threadIdx.x];
+        red[0][threadIdx.x] = v * scale;
+    }
     __syncthreads();
-    for (int t = threadIdx.x; t < n; t += kBlock) sc[t] = expf(sc[t] - m);
+    float m = -INFINITY;
+    for (int t = 0; t < n; ++t) m = fmaxf(m, red[0][t]);
+    if (threadIdx.x < CS) ex[threadIdx.x] = threadIdx.x < n ? expf(red[0][threadIdx.x] - m) : 0.0f;
     __syncthreads();
     float l = 0.0f;
-    for (int t = 0; t < n; ++t) l += sc[t];
+    for (int t = 0; t < n; ++t) l += ex[t];
 
-    // o_c[d] = sum_j e_j v_j[d], four dims per thread per step.
+    // o_c[d] = sum_j e_j v_j[d]: each thread owns float4 columns i, keys in
+    // batches of KB with all of a batch's loads issued first.
     const bool direct = nc == 1;
     float* dst = direct ? ctx + (int64_t)b * D : part + ((int64_t)b * nc + c) * (D + 4);
     const float inv_l = 1.0f / l;
-    for (int64_t i = threadIdx.x; i < D4; i += kBlock) {
-        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int t = 0; t < n; ++t) {
-            const int j = j0 + t;
-            const float4 vv = ((const float4*)((j == p) ? vn : vcb + (int64_t)j * D))[i];
-            const float e = sc[t];
-            o.x = fmaf(e, vv.x, o.x);
-            o.y = fmaf(e, vv.y, o.y);
-            o.z = fmaf(e, vv.z, o.z);
-            o.w = fmaf(e, vv.w, o.w);
+    // Column i of o_c: batch t0 of KB value rows is vv (loaded by the caller).
+    auto fma_batch = [&](float4& o, const float4* vv, int t0) {
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            if (t0 + u < n) {  // uniform over the workgroup
+                const float e = ex[t0 + u];
+                o.x = fmaf(e, vv[u].x, o.x);
+                o.y = fmaf(e, vv[u].y, o.y);
+                o.z = fmaf(e, vv[u].z, o.z);
+                o.w = fmaf(e, vv[u].w, o.w);
+            }
+        }
+    };
+    auto rest_and_store = [&](float4 o, int64_t i, int t_start) {
+        for (int t0 = t_start; t0 < n; t0 += KB) {
+            float4 vv[KB];
+#pragma unroll
+            for (int u = 0; u < KB; ++u) {
+                const int t = t0 + u, j = j0 + t;
+                const float* vr = (t >= n || j == p) ? vn : vcb + (int64_t)j * D;
+                vv[u] = ((const float4*)vr)[i];
+            }
+            fma_batch(o, vv, t0);
         }
         if (direct) {
             o.x = o.x * inv_l;
@@ -160,7 +219,18 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
             o.w = o.w * inv_l;
         }
         ((float4*)dst)[i] = o;
+    };
+#pragma unroll
+    for (int ci = 0; ci < PC; ++ci) {
+        const int64_t i = threadIdx.x + ci * kBlock;
+        if (i < D4) {
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+            fma_batch(o, vpre[ci], 0);
+            rest_and_store(o, i, KB);
+        }
     }
+    for (int64_t i = threadIdx.x + PC * kBlock; i < D4; i += kBlock)
+        rest_and_store(make_float4(0.f, 0.f, 0.f, 0.f), i, 0);
     if (!direct && threadIdx.x == 0) {
         dst[D] = m;
         dst[D + 1] = l;
@@ -168,38 +238,74 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
 }
 
 // ctx[b] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) over the chunks
-// that hold keys (M = max_c m_c).  Grid (ceil(D / (4 * kBlock)), B).  A
-// sequence with an invalid position gets a NaN row.
+// that hold keys (M = max_c m_c).  Grid (ceil(D / (4 * kBlock)), B).  The
+// chunk weights are computed once into LDS; each thread then sums its float4
+// column over the chunks, eight chunks' loads at a time.  A sequence with an
+// invalid position gets a NaN row.
 __global__ __launch_bounds__(kBlock) void k_attn_combine(const float* __restrict__ part, int nc, int CS, int64_t D,
                                                          const int32_t* __restrict__ pos, int64_t max_tokens,
                                                          int64_t max_len, float* __restrict__ ctx) {
+    __shared__ float wgt[kAttnMaxChunks];
+    __shared__ float lsum[kAttnMaxChunks];
+    __shared__ float red[kBlock / 64];
     const int b = blockIdx.y;
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;  // float4 index
-    if (i * 4 >= D) return;
-    float4* out = (float4*)(ctx + (int64_t)b * D) + i;
     const int T = seq_keys(pos, b, max_tokens, max_len);
     if (T < 0) {
-        *out = make_float4(NAN, NAN, NAN, NAN);
+        if (i * 4 < D) ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(NAN, NAN, NAN, NAN);
         return;
     }
     const int used = (T + CS - 1) / CS;
     const float* pb = part + (int64_t)b * nc * (D + 4);
-    float M = -INFINITY;
-    for (int c = 0; c < used; ++c) M = fmaxf(M, pb[(int64_t)c * (D + 4) + D]);
+    const bool col = i * 4 < D;
+    // The first eight chunks' values of this column load now, under the
+    // weight computation below.
+    float4 v0[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int cc = u < used ? u : 0;
+        v0[u] = col ? ((const float4*)(pb + (int64_t)cc * (D + 4)))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mx = -INFINITY;
+    for (int cc = threadIdx.x; cc < used; cc += kBlock) {
+        const float v = pb[(int64_t)cc * (D + 4) + D];
+        lsum[cc] = pb[(int64_t)cc * (D + 4) + D + 1];
+        wgt[cc] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w) M = fmaxf(M, red[w]);
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < used; cc += kBlock) wgt[cc] = expf(wgt[cc] - M);
+    __syncthreads();
     float L = 0.0f;
+    for (int cc = 0; cc < used; ++cc) L = fmaf(lsum[cc], wgt[cc], L);
+    if (!col) return;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c = 0; c < used; ++c) {
-        const float* pc = pb + (int64_t)c * (D + 4);
-        const float w = expf(pc[D] - M);
-        L = fmaf(pc[D + 1], w, L);
-        const float4 v = ((const float4*)pc)[i];
-        o.x = fmaf(v.x, w, o.x);
-        o.y = fmaf(v.y, w, o.y);
-        o.z = fmaf(v.z, w, o.z);
-        o.w = fmaf(v.w, w, o.w);
+    for (int c0 = 0; c0 < used; c0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int cc = c0 + u < used ? c0 + u : c0;
+            v[u] = c0 == 0 ? v0[u] : ((const float4*)(pb + (int64_t)cc * (D + 4)))[i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (c0 + u < used) {  // uniform over the workgroup
+                const float w = wgt[c0 + u];
+                o.x = fmaf(v[u].x, w, o.x);
+                o.y = fmaf(v[u].y, w, o.y);
+                o.z = fmaf(v[u].z, w, o.z);
+                o.w = fmaf(v[u].w, w, o.w);
+            }
+        }
     }
     const float inv = 1.0f / L;
-    *out = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
 }
 
 // Poisons the output rows of sequences with an invalid position (so the
@@ -230,15 +336,17 @@ hipError_t launch_add(const float* a, const float* b, float* y, int64_t n, hipSt
 }
 
 AttnPlan attn_plan(int64_t B, int64_t max_len) {
+    // About 512 workgroups over all sequences; chunks of 8, 16, 32 or 64 keys
+    // (kAttnMaxChunk), at most kAttnMaxChunks chunks per sequence.
+    int64_t cs = 8;
+    while (cs < kAttnMaxChunk && (ceil_div(max_len, cs) * B > 512 || ceil_div(max_len, cs) > kAttnMaxChunks)) cs *= 2;
     AttnPlan p;
-    // About 512 workgroups over all sequences, at least 8 and at most
-    // kAttnMaxChunk keys per chunk.
-    int64_t cs = ceil_div(max_len * B, 512);
-    cs = cs < 8 ? 8 : (cs > kAttnMaxChunk ? kAttnMaxChunk : cs);
     p.CS = (int)cs;
     p.NC = (int)ceil_div(max_len, cs);
     return p;
 }
+
+int64_t attn_max_len() { return kAttnMaxChunk * kAttnMaxChunks; }
 
 int64_t attn_workspace_floats(int64_t B, int64_t D, int64_t max_len) {
     const AttnPlan p = attn_plan(B, max_len);
@@ -249,10 +357,23 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
                                    int64_t D, float* kc, float* vc, int64_t max_tokens, const int32_t* pos,
                                    int64_t max_len, float scale, float* part, float* ctx, hipStream_t s) {
     if (B <= 0) return hipSuccess;
+    if (max_len > attn_max_len()) return hipErrorInvalidValue;
     const AttnPlan p = attn_plan(B, max_len);
-    const size_t lds = (size_t)(D + kAttnMaxChunk) * sizeof(float);
-    k_attn_partial<<<dim3((unsigned)p.NC, (unsigned)B), kBlock, lds, s>>>(q, knew, vnew, ldq, D, kc, vc, max_tokens,
-                                                                        pos, max_len, p.CS, scale, part, ctx);
+    const dim3 grid((unsigned)p.NC, (unsigned)B);
+#define SGQ_ATTN(CS_)                                                                                                 \
+    case CS_:                                                                                                         \
+        k_attn_partial<CS_><<<grid, kBlock, 0, s>>>(q, knew, vnew, ldq, D, kc, vc, max_tokens, pos, max_len, scale, \
+                                                    part, ctx);                                                       \
+        break;
+    switch (p.CS) {
+        SGQ_ATTN(8)
+        SGQ_ATTN(16)
+        SGQ_ATTN(32)
+        SGQ_ATTN(64)
+        default:
+            return hipErrorInvalidValue;
+    }
+#undef SGQ_ATTN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.NC > 1) {

@@ -103,10 +103,11 @@ hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
 // nw (1..3) tiled INT4 weights of one shape [K, N] side by side on one input:
 // weight w writes y[m * ldy + w * N + n] (+ res at the same index when res is
-// set).  Strip layout only; M <= kGemvMaxM.
+// set).  gamma (optional): the input is rms_norm(x, gamma, eps), applied
+// inside the kernel.  Strip layout only; M <= kGemvMaxM.
 hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N, int nw, const void* const* packed,
                                 const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
-                                int64_t ldy, const float* res, hipStream_t s);
+                                int64_t ldy, const float* res, const float* gamma, float eps, hipStream_t s);
 // MFMA GEMM (M > kGemvMaxM).  Grids with fewer 128x128 tiles than CUs split K
 // over workgroups; their partial tiles go to ws (gemm_workspace_bytes(M, K, N)
 // bytes, 0 when K is not split) and a second kernel adds them in fixed order.
@@ -134,7 +135,7 @@ hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N
 hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
-                                 hipStream_t s);
+                                 hipStream_t s, const float* gamma = nullptr, float eps = 0.0f);
 hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s);
 
 // ---- LLaMA block decode step (sgq_decode.hip) ---------------------------
@@ -143,11 +144,13 @@ hipError_t launch_rms_norm(const float* x, int64_t rows, int64_t D, const float*
 hipError_t launch_add(const float* a, const float* b, float* y, int64_t n, hipStream_t s);
 // Attention of one new token per sequence over its cache: keys split into
 // NC chunks of CS, combined by a second kernel when NC > 1.
-constexpr int kAttnMaxChunk = 64;
+constexpr int kAttnMaxChunk = 64;     // keys per chunk
+constexpr int kAttnMaxChunks = 1024;  // chunks per sequence (max_len <= 65536)
 struct AttnPlan {
     int CS, NC;
 };
 AttnPlan attn_plan(int64_t B, int64_t max_len);
+int64_t attn_max_len();
 int64_t attn_workspace_floats(int64_t B, int64_t D, int64_t max_len);
 // q, knew, vnew: rows of B sequences with row stride ldq; kc, vc: [B][max_tokens][D];
 // pos[b]: cached positions of sequence b before this step (the new row goes

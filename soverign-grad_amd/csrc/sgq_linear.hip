@@ -18,6 +18,7 @@
 // a time; codes are dequantized on the way into LDS (code * scale, the
 // reference's own product) and fed to v_mfma_f32_16x16x4_f32.
 #include "sgq_internal.h"
+#include "sgq_lanes.h"
 
 namespace sgq {
 namespace {
@@ -78,98 +79,6 @@ __device__ __forceinline__ float4 buf_load4f(__amdgpu_buffer_rsrc_t r, int voff,
     }
 }
 
-// Value of `v` held by the lane whose index differs from this lane's in bit O,
-// with VALU-latency cross-lane ops where gfx950 has them: DPP quad_perm for
-// bits 0-1, ds_swizzle (xor mode) for bits 2-3, v_permlane16/32_swap for bits
-// 4-5.  All lanes of the wavefront must be active.
-template <int O>
-__device__ __forceinline__ float xor_lane(float v, int lane) {
-    const int iv = __float_as_int(v);
-    if constexpr (O == 1) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
-    } else if constexpr (O == 2) {
-        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
-    } else if constexpr (O == 4 || O == 8) {
-        return __int_as_float(__builtin_amdgcn_ds_swizzle(iv, (O << 10) | 0x1F));  // xor O within 32 lanes
-    } else if constexpr (O == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
-        return __int_as_float((lane & 16) ? r[0] : r[1]);
-    } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
-        return __int_as_float((lane & 32) ? r[0] : r[1]);
-    }
-}
-
-// Halving step across lane bit O (16 or 32) with v_permlane16/32_swap, two
-// VALU ops per pair of values: swapping (x, y) = (v[i], v[i+h]) between the
-// two lane halves leaves, in a lane with bit O clear, its own v[i] and the
-// partner's v[i]; with bit O set, the partner's v[i+h] and its own.  Either
-// way x + y is the pair total of the index that lane keeps (i or i+h).
-template <int O>
-__device__ __forceinline__ float swap_add(float x, float y) {
-    const int xi = __float_as_int(x), yi = __float_as_int(y);
-    if constexpr (O == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(xi, yi, false, false);
-        return __int_as_float(r[0]) + __int_as_float(r[1]);
-    } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(xi, yi, false, false);
-        return __int_as_float(r[0]) + __int_as_float(r[1]);
-    }
-}
-
-// Lane bits in the order the reduction consumes them: cheapest exchange per
-// pair first (permlane swaps, 2 ops; then DPP, then ds_swizzle, 4 ops),
-// because the first steps move the most values.
-constexpr int red_bit(int i) { return i == 0 ? 32 : i == 1 ? 16 : i == 2 ? 1 : i == 3 ? 2 : i == 4 ? 4 : 8; }
-
-// Sums v[0..H) (H a power of two) over the 64 lanes of a wavefront.  While a
-// lane carries more than one value, each step halves them: the lane with bit
-// O set keeps the upper half plus its partner's upper half, the other keeps
-// the lower half (every value is exchanged once).  With one value left, the
-// remaining bits are plain butterflies.  On return v[0..red_left(H)) holds
-// the totals of indices base + i.
-template <int H, int I>
-__device__ __forceinline__ void lane_reduce(float* v, int lane, int& base) {
-    static_assert((H & (H - 1)) == 0, "halving needs a power of two");
-    if constexpr (I < 6) {
-        constexpr int O = red_bit(I);
-        if constexpr (H > 1) {
-            constexpr int h = H / 2;
-            const bool upper = (lane & O) != 0;
-            if constexpr (O >= 16) {
-#pragma unroll
-                for (int i = 0; i < h; ++i) v[i] = swap_add<O>(v[i], v[i + h]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < h; ++i) {
-                    const float send = upper ? v[i] : v[i + h];
-                    const float keep = upper ? v[i + h] : v[i];
-                    v[i] = keep + xor_lane<O>(send, lane);
-                }
-            }
-            if (upper) base += h;
-            lane_reduce<h, I + 1>(v, lane, base);
-        } else {
-            v[0] += xor_lane<O>(v[0], lane);
-            lane_reduce<1, I + 1>(v, lane, base);
-        }
-    }
-}
-
-// Values a lane holds after lane_reduce, and the lane bits whose lanes then
-// hold identical totals.
-constexpr int red_left(int H) { return H >= 64 ? H / 64 : 1; }
-constexpr int red_dup_mask(int H) {
-    int m = 0;
-    for (int i = 0; i < 6; ++i) {
-        if (H > 1)
-            H /= 2;
-        else
-            m |= red_bit(i);
-    }
-    return m;
-}
-
 // silu(v) = v / (1 + exp(-v)), as simd::vec_silu (simd.hpp:103-108); the
 // device expf differs from libm's by at most a few ulp, the division is
 // correctly rounded.
@@ -199,6 +108,8 @@ struct GemvArgs {
     const float* res;        // added to the output (same indexing), or null
     float* y;
     int ldy;                 // row stride of y and res
+    const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
+    float eps;
 };
 
 // ---------------------------------------------------------------------------
@@ -226,7 +137,14 @@ struct GemvArgs {
 // output (a LLaMA block's q, k and v projections of one input): workgroup
 // strips run over all of them and weight w writes columns w*N .. w*N+N-1 of
 // y.  a.res, when set, is added to every output (a residual connection).
-template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW>
+//
+// NORM: the input rows are first RMS-normalised (rms_norm, src/ops.cpp:
+// 1532-1556: x * inv_rms * gamma, inv_rms = 1 / sqrt(sum(x^2) / K + eps)).
+// inv_rms is one factor per row, so it comes out of the K sum: the workgroup
+// accumulates (x * gamma * s) * q and sum(x^2) of the x rows it reads anyway
+// (all of K), and multiplies by inv_rms in the epilogue.  No separate norm
+// launch and no normed copy of x.
+template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW, bool NORM>
 __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     static_assert(NG == 1 || SPW == 1, "the gated form takes one strip of each weight");
     const float* __restrict__ x = a.x;
@@ -236,6 +154,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     constexpr int CW = SPW * SW;             // columns per workgroup
     constexpr int V = MT * CW;               // accumulators per lane
     __shared__ float red[NG * NW][V];
+    __shared__ float sqr[NORM ? NG * NW : 1][MT];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
@@ -270,6 +189,12 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) rX[m] = make_rsrc(x + (int64_t)m * K, m < M ? (uint32_t)K * 4u : 0u);
 
+    __amdgpu_buffer_rsrc_t rG;
+    if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
+    float sq[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) sq[m] = 0.0f;
+
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
@@ -278,6 +203,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     for (int it0 = 0; it0 < nit; it0 += U) {
         uint4 w[U][SPW];
         float4 sv[U];
+        float4 gv[NORM ? U : 1];
         float4 xv[U][MT];  // x is loaded with the codes (measured 4-7% faster for M >= 4 than at use)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -291,6 +217,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
             }
 #pragma unroll
             for (int m = 0; m < MT; ++m) xv[u][m] = buf_load4f<KALIGN4>(rX[m], voff, soff);
+            if constexpr (NORM) gv[u] = buf_load4f<KALIGN4>(rG, voff, soff);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -308,8 +235,16 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
             for (int m = 0; m < MT; ++m) {
                 const float4 xm = xv[u][m];
                 float xs[4];
+                if constexpr (NORM) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
+                    for (int r = 0; r < 4; ++r) {
+                        sq[m] = fmaf(f4get(xm, r), f4get(xm, r), sq[m]);
+                        xs[r] = f4get(xm, r) * (f4get(gv[u], r) * f4get(sv[u], r));
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
+                }
 #pragma unroll
                 for (int s = 0; s < SPW; ++s) {
                     const uint32_t dw[4] = {w[u][s].x, w[u][s].y, w[u][s].z, w[u][s].w};
@@ -345,6 +280,14 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < left; ++i) red[wave][base + i] = acc[i];
     }
+    if constexpr (NORM) {
+        int sbase = 0;
+        lane_reduce<MT, 0>(sq, lane, sbase);
+        if ((lane & red_dup_mask(MT)) == 0) {
+#pragma unroll
+            for (int i = 0; i < red_left(MT); ++i) sqr[wave][sbase + i] = sq[i];
+        }
+    }
     __syncthreads();
 
     // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
@@ -357,13 +300,22 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
             float r = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) r += red[w][v];
+            float inv = 1.0f;
+            if constexpr (NORM) {  // every group read all of x: group 0's waves hold the full sum
+                float ss = 0.0f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) ss += sqr[w][m];
+                inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+            }
             r = r * post;
+            if constexpr (NORM) r = r * inv;
             if (bias) r = r + bias[n];
             if constexpr (NG == 2) {
                 float r2 = 0.0f;
 #pragma unroll
                 for (int w = NW; w < 2 * NW; ++w) r2 += red[w][v];
                 r2 = r2 * post;
+                if constexpr (NORM) r2 = r2 * inv;
                 if (bias2) r2 = r2 + bias2[n];
                 r = silu_f32(r) * r2;
             }
@@ -646,10 +598,21 @@ bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
     const dim3 grid((unsigned)(nw * ((a.NS + SPW - 1) / SPW)));
-    if (a.K % 4 == 0)
-        k_gemv<BITS, MT, NW, U, true, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(a);
+    const bool k4 = a.K % 4 == 0;
+    if constexpr (BITS == 4 && SPW == 1) {  // the norm-fused form serves the INT4 LLaMA block
+        if (a.gamma) {
+            if (k4)
+                k_gemv<BITS, MT, NW, U, true, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(a);
+            else
+                k_gemv<BITS, MT, NW, U, false, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(a);
+            return hipGetLastError();
+        }
+    }
+    if (a.gamma) return hipErrorInvalidValue;
+    if (k4)
+        k_gemv<BITS, MT, NW, U, true, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(a);
     else
-        k_gemv<BITS, MT, NW, U, false, NG, SPW><<<grid, NG * NW * 64, 0, s>>>(a);
+        k_gemv<BITS, MT, NW, U, false, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
@@ -678,9 +641,10 @@ hipError_t gemv_launch_spw(const GemvArgs& a, int nw, hipStream_t s) {
     constexpr int UMAX = (MT * SPW <= 2) ? 4 : (MT * SPW <= 4 ? 2 : 1);
     const int per_lane = (a.RQ + NW * 64 - 1) / (NW * 64);
     const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
-#define SGQ_GEMV_NU(U_)                                        \
-    if ((u >= U_ || U_ == 1) && U_ <= UMAX)                  \
-        return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s);
+#define SGQ_GEMV_NU(U_)                                                   \
+    if constexpr (U_ <= UMAX) {                                          \
+        if (u >= U_ || U_ == 1) return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s); \
+    }
     SGQ_GEMV_NU(4)
     SGQ_GEMV_NU(2)
     SGQ_GEMV_NU(1)
@@ -743,14 +707,16 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
 
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
-    return launch_gemv_i4_multi(x, M, K, N, 1, &packed, &devscales, &bias, g, y, N, nullptr, s);
+    return launch_gemv_i4_multi(x, M, K, N, 1, &packed, &devscales, &bias, g, y, N, nullptr, nullptr, 0.0f, s);
 }
 
 hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N, int nw, const void* const* packed,
                                 const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
-                                int64_t ldy, const float* res, hipStream_t s) {
+                                int64_t ldy, const float* res, const float* gamma, float eps, hipStream_t s) {
     if (nw < 1 || nw > 3) return hipErrorInvalidValue;
     GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, y, ldy, res);
+    a.gamma = gamma;
+    a.eps = eps;
     for (int w = 0; w < nw; ++w) {
         a.W[w] = (const uint4*)packed[w];
         a.SC[w] = devscales[w];
@@ -772,8 +738,10 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
 hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
-                                 hipStream_t s) {
+                                 hipStream_t s, const float* gamma, float eps) {
     GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, h, N, nullptr);
+    a.gamma = gamma;
+    a.eps = eps;
     a.W[0] = (const uint4*)packed_g;
     a.W[1] = (const uint4*)packed_u;
     a.SC[0] = devscales_g;
