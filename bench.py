@@ -551,6 +551,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
+    ap.add_argument("--block-decode", type=int, default=0, metavar="CTX",
+                    help="only time the 22-layer block decode step at CTX cached positions (for profiling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -566,6 +568,12 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.block_decode:
+        r = block_decode_step(pkg, dev, Oracle(), max(2, min(10, args.steps)), args.block_decode)
+        if r["rel_err_vs_oracle"] > 1e-5:
+            raise SystemExit("parity failure in bench (block decode)")
+        print(json.dumps(r), flush=True)
+        return 0
     c = CONFIGS[args.config]
     nbytes = alg_bytes(c)
     copies = args.copies or max(1, min(64, -(-300_000_000 // nbytes)))
