@@ -52,6 +52,16 @@ Tensor dequantize_int8(const QuantizedTensor& qx);
 QuantizedTensor quantize_int4(const Tensor& x, int64_t group_size = 32);
 Tensor dequantize_int4(const QuantizedTensor& qx);
 
+// The packed device form of q (built, or rebuilt after qdata/scales changed,
+// on demand) for callers of the C ABI such as the LLaMA block decode step.
+// The handle keeps the device buffers alive while it is held.
+struct PackedHandle {
+    std::shared_ptr<Storage> codes;
+    Tensor devscales;  // INT4 strip-major layout
+    Tensor scales;     // reference-layout scales on the GPU
+};
+PackedHandle packed_weight(const QuantizedTensor& q);
+
 // Direct Low-Bit Matrix Multiplication: x[B,K] . deq(W[K,N]) (+ bias[1,N])
 Tensor quantized_matmul_int8(const Tensor& x, const QuantizedTensor& q_weight, const Tensor& bias = Tensor());
 Tensor quantized_matmul_int4(const Tensor& x, const QuantizedTensor& q_weight, const Tensor& bias = Tensor());

@@ -110,6 +110,11 @@ void check_linear_args(const Tensor& x, const QuantizedTensor& w, const Tensor& 
 
 }  // namespace
 
+PackedHandle packed_weight(const QuantizedTensor& q) {
+    const PackedView v = packed_of(q);
+    return PackedHandle{v.codes, v.devscales, v.scales_dev};
+}
+
 QuantizedTensor quantize_int8(const Tensor& x, QuantizationScheme scheme) {
     const View2D v = view2d(x.shape());
     const int eff = (scheme == QuantizationScheme::PerTensorSymmetric || x.shape().size() < 2)

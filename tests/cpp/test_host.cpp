@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "sovereigngrad/allocator.hpp"
+#include "sovereigngrad/models.hpp"
 #include "sovereigngrad/nn.hpp"
 #include "sovereigngrad/quantization.hpp"
 #include "sovereigngrad/safetensors.hpp"
@@ -396,6 +397,112 @@ static void test_allocator_gpu() {
     std::cout << "  * " << A.get_memory_summary(Device::CUDA) << ": PASSED\n";
 }
 
+// The quantized LLaMA block decode step against a double-precision CPU
+// composition of the same quantized weights (the oracle-level parity of the
+// kernels is pinned by the Python tests; this checks the host wiring: module
+// tree, packed weights, biases, norms, cache and positions).
+static void test_llama_block_decode() {
+    std::cout << "--- quantized LLaMA block decode\n";
+    Tensor::manual_seed(2024);
+    const int64_t D = 64, H = 128, heads = 4, G = 32, B = 2, T = 3;
+    std::vector<std::unique_ptr<nn::Linear>> lin;
+    const int64_t shapes[7][2] = {{D, D}, {D, D}, {D, D}, {D, D}, {D, H}, {D, H}, {H, D}};
+    std::vector<const nn::Linear*> ptrs;
+    for (auto& sh : shapes) {
+        lin.emplace_back(new nn::Linear(sh[0], sh[1], Device::CUDA));
+        lin.back()->b.copy_from(Tensor::randn({1, sh[1]}, 0.0f, 0.05f, Device::CUDA));
+        ptrs.push_back(lin.back().get());
+    }
+    Tensor n1 = Tensor::randn({D}, 1.0f, 0.1f, Device::CUDA), n2 = Tensor::randn({D}, 1.0f, 0.1f, Device::CUDA);
+    auto blk = models::QuantizedLLaMABlock::from_float(ptrs, n1, n2, heads, G);
+    auto sd = blk->state_dict();
+    CHECK(sd.count("norm1.weight") && sd.count("attn.q_proj.qdata") && sd.count("attn.out_proj.bias") &&
+          sd.count("mlp.w_gate.scales") && sd.count("mlp.w_down.qdata") && !sd.count("attn.q_proj.weight"));
+
+    // Dequantized weights and biases on the host for the reference.
+    const std::shared_ptr<nn::QuantizedLinear4Bit> ql[7] = {blk->attn->q_proj, blk->attn->k_proj, blk->attn->v_proj,
+                                                           blk->attn->out_proj, blk->mlp->w_gate, blk->mlp->w_up,
+                                                           blk->mlp->w_down};
+    std::vector<std::vector<float>> Wd(7), bd(7);
+    for (int i = 0; i < 7; ++i) {
+        Wd[i] = host(quantization::dequantize_int4(ql[i]->q_weight));
+        bd[i] = host(ql[i]->bias);
+    }
+    const std::vector<float> g1 = host(n1), g2 = host(n2);
+    auto proj = [&](const std::vector<double>& in, int p) {
+        const int64_t K = shapes[p][0], N = shapes[p][1];
+        std::vector<double> o(N);
+        for (int64_t n = 0; n < N; ++n) {
+            double a = bd[p][n];
+            for (int64_t k = 0; k < K; ++k) a += in[k] * Wd[p][k * N + n];
+            o[n] = a;
+        }
+        return o;
+    };
+    auto rms = [&](const std::vector<double>& in, const std::vector<float>& g) {
+        double ss = 0.0;
+        for (double v : in) ss += v * v;
+        const double inv = 1.0 / std::sqrt(ss / (double)D + 1e-5);
+        std::vector<double> o(D);
+        for (int64_t d = 0; d < D; ++d) o[d] = in[d] * inv * g[d];
+        return o;
+    };
+    const double scale = 1.0 / std::sqrt((double)(D / heads));
+
+    models::KVCache cache(B, 8, D);
+    models::DecodePositions pos(B);
+    std::vector<std::vector<std::vector<double>>> kc(B), vc(B);
+    double worst = 0.0;
+    for (int64_t t = 0; t < T; ++t) {
+        pos.set(std::vector<int32_t>(B, (int32_t)t));
+        Tensor x = Tensor::randn({B, D}, 0.0f, 1.0f, Device::CPU);  // CPU input: returned on the CPU
+        Tensor y = blk->decode(x, cache, pos);
+        CHECK(y.device() == Device::CPU && y.shape()[0] == B && y.shape()[1] == D);
+        const std::vector<float> xh = host(x), yh = host(y);
+        for (int64_t b = 0; b < B; ++b) {
+            std::vector<double> xv(xh.begin() + b * D, xh.begin() + (b + 1) * D);
+            const auto a = rms(xv, g1);
+            const auto q = proj(a, 0);
+            kc[b].push_back(proj(a, 1));
+            vc[b].push_back(proj(a, 2));
+            std::vector<double> s(t + 1), ctx(D, 0.0);
+            double mx = -1e300, sum = 0.0;
+            for (int64_t j = 0; j <= t; ++j) {
+                double dot = 0.0;
+                for (int64_t d = 0; d < D; ++d) dot += q[d] * kc[b][j][d];
+                s[j] = dot * scale;
+                mx = std::max(mx, s[j]);
+            }
+            for (int64_t j = 0; j <= t; ++j) sum += std::exp(s[j] - mx);
+            for (int64_t j = 0; j <= t; ++j)
+                for (int64_t d = 0; d < D; ++d) ctx[d] += std::exp(s[j] - mx) / sum * vc[b][j][d];
+            const auto o = proj(ctx, 3);
+            std::vector<double> h(D);
+            for (int64_t d = 0; d < D; ++d) h[d] = xv[d] + o[d];
+            const auto n2v = rms(h, g2);
+            const auto gt = proj(n2v, 4), up = proj(n2v, 5);
+            std::vector<double> hid(H);
+            for (int64_t i = 0; i < H; ++i) hid[i] = gt[i] / (1.0 + std::exp(-gt[i])) * up[i];
+            const auto dn = proj(hid, 6);
+            double num = 0.0, den = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+                num = std::max(num, std::fabs(yh[b * D + d] - (h[d] + dn[d])));
+                den = std::max(den, std::fabs(h[d] + dn[d]));
+            }
+            worst = std::max(worst, num / den);
+        }
+    }
+    CHECK(worst <= 1e-5);
+    // A sequence outside the cache comes back NaN; the other one is unaffected.
+    pos.set({(int32_t)T, -1});
+    Tensor y = blk->decode(Tensor::randn({B, D}, 0.0f, 1.0f, Device::CUDA), cache, pos);
+    auto yh = host(y);
+    CHECK(std::isfinite(yh[0]) && std::isnan(yh[D]));
+    CHECK(throws([&] { blk->decode(Tensor::randn({B + 1, D}, 0.0f, 1.0f, Device::CUDA), cache, pos); }));
+    std::cout << "  * D=64 H=128 B=2, 3 tokens, worst rel err " << worst << ": "
+              << (worst <= 1e-5 ? "PASSED" : "FAILED") << "\n";
+}
+
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     std::vector<std::pair<std::string, std::function<void()>>> tests;
@@ -412,7 +519,8 @@ int main(int argc, char** argv) {
                  {"forward_composition", test_forward_matches_composition},
                  {"persistence_bridge", test_persistence_bridge},
                  {"module_to_device", test_module_to_device},
-                 {"concurrent_forward", test_concurrent_forward}};
+                 {"concurrent_forward", test_concurrent_forward},
+                 {"llama_block_decode", test_llama_block_decode}};
     } else {
         std::cerr << "usage: test_host cpu|gpu\n";
         return 2;
