@@ -110,6 +110,7 @@ struct GemvArgs {
     int ldy;                 // row stride of y and res
     const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
     float eps;
+    int P;                   // row groups: M rows split into P groups of MT (one workgroup each)
 };
 
 // ---------------------------------------------------------------------------
@@ -147,8 +148,7 @@ struct GemvArgs {
 template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW, bool NORM>
 __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     static_assert(NG == 1 || SPW == 1, "the gated form takes one strip of each weight");
-    const float* __restrict__ x = a.x;
-    const int M = a.M, K = a.K, N = a.N, mode = a.mode, Kpad = a.Kpad, RQ = a.RQ, NS = a.NS;
+    const int K = a.K, N = a.N, mode = a.mode, Kpad = a.Kpad, RQ = a.RQ, NS = a.NS;
     constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
     constexpr int RQ_IT = NW * 64;           // row quads per group iteration
     constexpr int CW = SPW * SW;             // columns per workgroup
@@ -162,7 +162,15 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // Strips of a scale column share an XCD's L2.  Workgroups of one weight
     // cover (NS + SPW - 1) / SPW strip groups; with several weights side by
     // side (NG == 1), wt selects the weight.
-    const int jg = xcd_swizzle(blockIdx.x, gridDim.x);
+    // Workgroup v covers row group p = v % P of strip group v / P: the row
+    // groups of one strip are neighbours in v, so they run on one XCD and the
+    // second read of the strip's codes hits its L2.
+    const int vg = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int prow = a.P > 1 ? vg % a.P : 0;
+    const int jg = a.P > 1 ? vg / a.P : vg;
+    const int m0 = prow * MT;
+    const float* __restrict__ x = a.x + (int64_t)m0 * K;
+    const int M = min(MT, a.M - m0);
     const int per_w = (NS + SPW - 1) / SPW;
     const int wt = NG == 1 ? jg / per_w : 0;
     const int j0 = SPW * (jg - wt * per_w);
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
         const int m = v / CW, e = v - m * CW;
         const int n = j0 * SW + e;
         if (m < M && n < N) {
-            const int64_t o = (int64_t)m * a.ldy + (int64_t)wt * N + n;
+            const int64_t o = (int64_t)(m0 + m) * a.ldy + (int64_t)wt * N + n;
             float r = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) r += red[w][v];
@@ -597,7 +605,7 @@ bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x
 
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
-    const dim3 grid((unsigned)(nw * ((a.NS + SPW - 1) / SPW)));
+    const dim3 grid((unsigned)(nw * ((a.NS + SPW - 1) / SPW) * a.P));
     const bool k4 = a.K % 4 == 0;
     if constexpr (BITS == 4 && SPW == 1) {  // the norm-fused form serves the INT4 LLaMA block
         if (a.gamma) {
@@ -664,39 +672,41 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
     // each SIMD holds more than one wavefront to hide load latency.  Measured
     // on MI355X: 5632 -> 2048 at M=8 9.1 -> 7.7 us, M=1 4.8 -> 4.6 us;
     // 2048 -> 2048 at M=4 3.9 -> 3.7 us.
-    if ((int64_t)nw * a.NS < 2 * kCus && a.RQ >= 8 * 64)
+    if ((int64_t)nw * a.NS * a.P < 2 * kCus && a.RQ >= 8 * 64)
         return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
     return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(a, nw, s);
 }
 
-// Batches up to 8 rows run in one pass; larger batches in passes of 8 rows.
 template <int BITS, int NG>
 hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
-    const float* x = a.x;
-    float* y = a.y;
-    const float* res = a.res;
-    for (int64_t m0 = 0; m0 < M; m0 += 8) {
-        a.M = (int)((M - m0) < 8 ? (M - m0) : 8);
-        a.x = x + m0 * a.K;
-        a.y = y + m0 * a.ldy;
-        a.res = res ? res + m0 * a.ldy : nullptr;
-        hipError_t e;
-        if (a.M <= 1)
-            e = gemv_launch<BITS, 1, NG>(a, nw, s);
-        else if (a.M <= 2)
-            e = gemv_launch<BITS, 2, NG>(a, nw, s);
-        else if (a.M <= 4)
-            e = gemv_launch<BITS, 4, NG>(a, nw, s);
-        else
-            e = gemv_launch<BITS, 8, NG>(a, nw, s);
-        if (e != hipSuccess) return e;
+    a.M = (int)M;
+#ifdef SGQ_ROWS4
+    constexpr int kRowsMax = 4;
+#else
+    constexpr int kRowsMax = 8;
+#endif
+    // All rows in one launch: M <= 4 as one row group, larger M in row groups
+    // of kRowsMax (each a workgroup of its own over the same strip).
+    if (M <= 1) {
+        a.P = 1;
+        return gemv_launch<BITS, 1, NG>(a, nw, s);
     }
-    return hipSuccess;
+    if (M <= 2) {
+        a.P = 1;
+        return gemv_launch<BITS, 2, NG>(a, nw, s);
+    }
+    if (M <= 4) {
+        a.P = 1;
+        return gemv_launch<BITS, 4, NG>(a, nw, s);
+    }
+    a.P = (int)((M + kRowsMax - 1) / kRowsMax);
+    return gemv_launch<BITS, kRowsMax, NG>(a, nw, s);
 }
 
 GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad, int64_t RQ, int64_t NS, float* y,
                    int64_t ldy, const float* res) {
     GemvArgs a{};
+    a.P = 1;
     a.x = x;
     a.K = (int)K;
     a.N = (int)N;
