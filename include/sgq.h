@@ -270,6 +270,12 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* block, const float* 
                                 float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,
                                 int64_t max_len, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Replaces embedding (src/ops.cpp:2624-2650): out[i, :] = weight[(int)indices[i], :]
+ * for the n fp32 token ids in `indices` (truncated to int, as the reference
+ * reads them), a zero row for an id outside [0, num_embeddings). */
+int sgq_embedding(const float* indices, int64_t n, const float* weight, int64_t num_embeddings,
+                  int64_t embedding_dim, float* out, void* stream);
+
 /* Replaces rms_norm (src/ops.cpp:1532-1556) for rows of [rows, D]:
  * out = x * (1 / sqrt(sum(x^2) / D + eps)) * g.  out may be x. */
 int sgq_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float eps, float* out, void* stream);

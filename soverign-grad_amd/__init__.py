@@ -70,6 +70,7 @@ SIGNATURES = {
     "sgq_llama_decode_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "sgq_llama_block_decode_int4": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "sgq_rms_norm": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp]),
+    "sgq_embedding": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
 }
 
 _lib = None

@@ -519,6 +519,17 @@ int sgq_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float 
     return ok();
 }
 
+int sgq_embedding(const float* indices, int64_t n, const float* weight, int64_t num_embeddings,
+                  int64_t embedding_dim, float* out, void* stream) {
+    if (n < 0 || bad_dims(num_embeddings, embedding_dim) || bad_dims(n, embedding_dim) || n > 0x7fffffff)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_embedding: bad shape");
+    if (n == 0 || embedding_dim == 0) return ok();
+    if (!indices || !weight || !out) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_embedding: null pointer");
+    SGQ_HIP(launch_embedding(indices, n, weight, num_embeddings, embedding_dim, out, (hipStream_t)stream),
+            "embedding");
+    return ok();
+}
+
 int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x, float* out, int64_t B,
                                 float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,
                                 int64_t max_len, void* workspace, int64_t workspace_bytes, void* stream) {

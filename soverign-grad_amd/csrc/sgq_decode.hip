@@ -65,6 +65,20 @@ __global__ __launch_bounds__(kBlock) void k_add(const float* __restrict__ a, con
         y[i] = a[i] + b[i];
 }
 
+// out[i, :] = w[(int)idx[i], :], or zeros for an id outside [0, V)
+// (embedding, src/ops.cpp:2624-2650: ids are fp32 values truncated to int).
+__global__ __launch_bounds__(kBlock) void k_embedding(const float* __restrict__ idx, const float* __restrict__ w,
+                                                      int64_t V, int64_t E, float* __restrict__ out) {
+    const float f = idx[blockIdx.x];
+    // (int) of a float outside int's range is undefined in C++; such ids are
+    // out of [0, V) anyway, so they are tested as floats first.
+    const bool ok = f > -1.0f && f < (float)V;
+    const int64_t id = ok ? (int64_t)(int)f : -1;
+    float* o = out + (int64_t)blockIdx.x * E;
+    const float* r = w + (id >= 0 && id < V ? id : 0) * E;
+    for (int64_t e = threadIdx.x; e < E; e += kBlock) o[e] = (id >= 0 && id < V) ? r[e] : 0.0f;
+}
+
 // Sequence b's keys this step: positions 0 .. pos[b] (pos[b] were cached
 // before, the new one is pos[b]).  Invalid when pos[b] is negative or does
 // not fit the cache or the caller's bound.
@@ -324,6 +338,13 @@ hipError_t launch_rms_norm(const float* x, int64_t rows, int64_t D, const float*
                            hipStream_t s) {
     if (rows <= 0 || D <= 0) return hipSuccess;
     k_rms_norm<<<(unsigned)rows, kBlock, 0, s>>>(x, D, g, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_embedding(const float* idx, int64_t n, const float* w, int64_t V, int64_t E, float* out,
+                            hipStream_t s) {
+    if (n <= 0 || E <= 0) return hipSuccess;
+    k_embedding<<<(unsigned)n, kBlock, 0, s>>>(idx, w, V, E, out);
     return hipGetLastError();
 }
 

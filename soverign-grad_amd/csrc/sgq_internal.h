@@ -142,6 +142,8 @@ hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s);
 hipError_t launch_rms_norm(const float* x, int64_t rows, int64_t D, const float* g, float eps, float* out,
                            hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, float* y, int64_t n, hipStream_t s);
+hipError_t launch_embedding(const float* idx, int64_t n, const float* w, int64_t V, int64_t E, float* out,
+                            hipStream_t s);
 // Attention of one new token per sequence over its cache: keys split into
 // NC chunks of CS, combined by a second kernel when NC > 1.
 constexpr int kAttnMaxChunk = 64;     // keys per chunk

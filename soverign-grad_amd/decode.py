@@ -161,5 +161,73 @@ def decode_layers(blocks: Sequence[QuantizedLLaMABlock], x: torch.Tensor, cache:
     return h
 
 
+def embedding(indices: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """embedding (src/ops.cpp:2624-2650) on the device: fp32 token ids in, rows of weight out."""
+    lib = load_library()
+    idx = _dev_f32(indices).reshape(-1)
+    w = _dev_f32(weight)
+    y = out if out is not None else torch.empty((idx.numel(), w.shape[1]), dtype=torch.float32, device=w.device)
+    _check(lib.sgq_embedding(_ptr(idx), idx.numel(), _ptr(w), w.shape[0], w.shape[1], _ptr(y), _stream(w.device)))
+    return y
+
+
+class QuantizedNanoLLaMA:
+    """NanoLLaMA (include/sovereigngrad/models.hpp:226-303) with quantized
+    blocks and an INT4 lm_head, decoding with a KV cache:
+
+      h = token_embeddings(ids); h = layer(h) for each layer; h = norm_f(h);
+      logits = lm_head(h)                                  (models.hpp:257-266)
+
+    generate() follows NanoLLaMA::generate's greedy choice (models.hpp:270-302:
+    softmax of logits / temperature, then the first index of the largest
+    probability); the argmax of the logits is the same index, so the softmax is
+    not formed."""
+
+    def __init__(self, tok_emb: torch.Tensor, blocks: Sequence[QuantizedLLaMABlock], norm_f: torch.Tensor,
+                 lm_head: QuantizedTensor, lm_bias: Optional[torch.Tensor] = None, eps: float = 1e-5):
+        self.tok_emb = _dev_f32(tok_emb)
+        self.blocks = list(blocks)
+        self.norm_f = _dev_f32(norm_f).reshape(-1)
+        self.lm_head, self.lm_bias, self.eps = lm_head, lm_bias, eps
+        self.D = self.tok_emb.shape[1]
+        self.V = lm_head.cols
+
+    def new_cache(self, B: int, max_tokens: int) -> KVCache:
+        return KVCache(B, max_tokens, self.D, self.tok_emb.device, layers=len(self.blocks))
+
+    def step(self, token_ids: torch.Tensor, cache: KVCache, max_len: int) -> torch.Tensor:
+        """One token per sequence (fp32 ids [B]) at positions cache.pos; returns
+        logits [B, V].  The caller advances cache.pos."""
+        from . import quantized_matmul_int4
+
+        x = embedding(token_ids, self.tok_emb)
+        h = decode_layers(self.blocks, x, cache, max_len)
+        return quantized_matmul_int4(rms_norm(h, self.norm_f, self.eps), self.lm_head, self.lm_bias)
+
+    def generate(self, prompts: Sequence[Sequence[int]], max_new_tokens: int) -> list:
+        """Greedy continuation of each prompt (all prompts of one length), one
+        decode step per token: the prompt is fed token by token, then each new
+        token is chosen from the last logits."""
+        B, L = len(prompts), len(prompts[0])
+        if any(len(p) != L for p in prompts) or L == 0:
+            raise ValueError("prompts must be non-empty and of one length")
+        dev = self.tok_emb.device
+        cache = self.new_cache(B, L + max_new_tokens)
+        out = [list(p) for p in prompts]
+        cur = torch.tensor([p[0] for p in prompts], dtype=torch.float32, device=dev)
+        for t in range(L + max_new_tokens - 1):
+            cache.pos.fill_(t)
+            logits = self.step(cur, cache, t + 1)
+            if t + 1 < L:
+                cur = torch.tensor([p[t + 1] for p in prompts], dtype=torch.float32, device=dev)
+                continue
+            # The reference picks on the host, keeping the first maximum.
+            nxt = logits.cpu().numpy().argmax(axis=1).tolist()
+            for b in range(B):
+                out[b].append(int(nxt[b]))
+            cur = torch.tensor(nxt, dtype=torch.float32, device=dev)
+        return out
+
+
 __all__ = ["PROJECTIONS", "Int4Linear", "LlamaBlockInt4", "projection_shapes", "attention_scale", "rms_norm",
-           "KVCache", "QuantizedLLaMABlock", "decode_layers"]
+           "KVCache", "QuantizedLLaMABlock", "decode_layers", "embedding", "QuantizedNanoLLaMA"]

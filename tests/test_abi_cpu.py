@@ -145,6 +145,9 @@ def test_llama_decode_sizes_and_errors(lib, sgq):
     assert lib.sgq_rms_norm(None, -1, 4, None, ctypes.c_float(1e-5), None, None) == 1
     assert lib.sgq_rms_norm(None, 0, 4, None, ctypes.c_float(1e-5), None, None) == 0
     assert lib.sgq_rms_norm(None, 2, 4, 16, ctypes.c_float(1e-5), 16, None) == 1
+    assert lib.sgq_embedding(None, -1, None, 4, 4, None, None) == 1
+    assert lib.sgq_embedding(None, 0, None, 4, 4, None, None) == 0
+    assert lib.sgq_embedding(16, 3, None, 4, 4, 16, None) == 1 and b"null" in lib.sgq_last_error()
 
 
 def test_argument_errors_before_gpu(lib, sgq):

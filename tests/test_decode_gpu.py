@@ -253,3 +253,63 @@ def test_block_decode_invalid_positions(sgq, dev, oracle, synth):
     cache.pos.copy_(torch.tensor([2, 3, 0, 0], dtype=torch.int32))
     y = _np(blk.decode(_dev(x, dev), cache.k[0], cache.v[0], cache.pos, 3))
     assert np.all(np.isfinite(y[0])) and np.all(np.isnan(y[1]))
+
+
+def test_embedding_golden(sgq, dev, golden):
+    dm = _decode_mod(sgq)
+    n = 0
+    for c in golden:
+        if c["kind"] != "embedding":
+            continue
+        y = _np(dm.embedding(_dev(c["idx"], dev), _dev(c["w"], dev)))
+        assert helpers.same_bits(y, c["y"])
+        n += 1
+    assert n >= 1
+
+
+def _oracle_model_logits(oracle, ids, emb, layers, normf, lm, G, scale):
+    """NanoLLaMA::forward (models.hpp:257-266) on one sequence, composed from
+    the oracle's pinned pieces: embedding, quantized blocks, rms_norm, INT4 lm_head."""
+    h = oracle.embedding(np.asarray(ids, np.float32), emb)
+    for (codes, scales, biases, g1, g2) in layers:
+        h = _oracle_rows(oracle, h, codes, scales, biases, g1, g2, scale, G)
+    return oracle.quantized_matmul_int4(oracle.rms_norm(h, normf), lm[0], lm[1], G, lm[2])
+
+
+def test_nanollama_generate(sgq, dev, oracle, synth):
+    # A 2-layer quantized NanoLLaMA: every step's logits match the oracle's
+    # full-sequence forward on the same prefix, and greedy generation picks the
+    # same tokens (prompts of 3 tokens, 6 new tokens, batch 3).
+    dm = _decode_mod(sgq)
+    V, D, H, G, heads, nl = 50, 64, 128, 32, 4, 2
+    emb = synth.normal((V, D), 1700, synth.STREAM_W, 0.0, 1.0)
+    layers = [_random_block(oracle, synth, D, H, G, 1710 + 20 * i) for i in range(nl)]
+    normf = (1.0 + synth.normal((D,), 1790, synth.STREAM_BIAS, 0.0, 0.1)).astype(np.float32)
+    lq, ls = oracle.quantize_int4(synth.normal((D, V), 1791, synth.STREAM_W, 0.0, 0.3), G)
+    lb = synth.normal((V,), 1792, synth.STREAM_BIAS, 0.0, 0.02)
+    blocks = [_block_from_case(sgq, dev, *ly, heads, G) for ly in layers]
+    lm = sgq.pack_int4(_dev(lq, dev), _dev(ls, dev), G)
+    model = dm.QuantizedNanoLLaMA(_dev(emb, dev), blocks, _dev(normf, dev), lm, _dev(lb, dev))
+    scale = dm.attention_scale(D, heads)
+    prompts = [[3, 17, 42], [0, 49, 5], [7, 7, 7]]
+    out = model.generate(prompts, 6)
+    for b, seq in enumerate(out):
+        assert seq[:3] == prompts[b]
+        for t in range(3, len(seq)):
+            logits = _oracle_model_logits(oracle, seq[:t], emb, layers, normf, (lq, ls, lb), G, scale)[-1]
+            top = np.sort(logits)[::-1]
+            if top[0] - top[1] > 1e-4 * np.abs(logits).max():  # not a near-tie
+                assert seq[t] == int(np.argmax(logits)), (b, t)
+    # Logits of one step against the oracle, batch of two sequences at different positions.
+    cache = model.new_cache(2, 8)
+    seqs = [[5, 6, 7, 8], [9, 10]]
+    logits = None
+    for t in range(4):
+        pos = np.array([t if t < len(s) else -1 for s in seqs], np.int32)
+        cache.pos.copy_(torch.from_numpy(pos))
+        ids = torch.tensor([float(s[t]) if t < len(s) else 0.0 for s in seqs], device=dev)
+        logits = _np(model.step(ids, cache, t + 1))
+        for b, s in enumerate(seqs):
+            if t < len(s):
+                ref = _oracle_model_logits(oracle, s[: t + 1], emb, layers, normf, (lq, ls, lb), G, scale)[-1]
+                assert _row_err(logits[b], ref) <= TOL, (b, t)
