@@ -25,6 +25,13 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Batches of up to this many rows decode INT4 with the offset-binary fma_mix
+// form; larger batches share one convert per code over their rows instead.
+#ifndef SGQ_GEMV_MIX_MAXMT
+#define SGQ_GEMV_MIX_MAXMT 2
+#endif
+constexpr int kGemvMixMaxRows = SGQ_GEMV_MIX_MAXMT;
+
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -42,6 +49,40 @@ __device__ __forceinline__ float cvt_sbyte(uint32_t w) {
 
 __device__ __forceinline__ float i8_byte(uint32_t w, int b) {
     return b == 0 ? cvt_sbyte<0>(w) : (b == 1 ? cvt_sbyte<1>(w) : (b == 2 ? cvt_sbyte<2>(w) : cvt_sbyte<3>(w)));
+}
+
+// INT4 decode of the GEMV.  A two's-complement nibble q in [-8, 7] XOR 8 is
+// its offset-binary form u = q + 8 in [0, 15].  Masked into the low bits of a
+// 16-bit half with the exponent bits clear, u reads as the fp16 subnormal
+// u * 2^-24 (u at bits 4-7: u * 2^-20), exactly.  fmaf on the half converted
+// to float compiles to one v_fma_mix_f32 (the fp16 operand is converted
+// inside the FMA, op_sel picks the half), so a code costs one VALU op plus
+// 6/8 op of masking, against a convert plus an FMA otherwise.  The kernel
+// accumulates sum(u * xs) and undoes the offset with -8 * sum(xs) at the end.
+__device__ __forceinline__ float half_lo(uint32_t p) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(p & 0xFFFFu));
+}
+__device__ __forceinline__ float half_hi(uint32_t p) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16));
+}
+
+// One INT4 output summed in k order as code * (x * s) (NORM: x * (gamma * s)),
+// reading strip j of the strip-major layout, whose dword k is row k.  The
+// GEMV falls back to this when its offset-corrected sum is not finite (an
+// infinite or NaN input, or an overflow), so that infinities and NaNs come
+// out as in the reference's x . (q * s) rather than as inf - inf.
+template <bool NORM>
+__device__ float i4_column_exact(const uint4* W, const float* SC, int j, int e, int spc, int Kpad, int RQ,
+                                 const float* xrow, const float* gamma, int K) {
+    const uint32_t* wd = reinterpret_cast<const uint32_t*>(W + (int64_t)j * RQ);
+    const float* sc = SC + (int64_t)(j / spc) * Kpad;
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const int q = ((int)(wd[k] << (28 - 4 * e))) >> 28;
+        const float s = NORM ? gamma[k] * sc[k] : sc[k];
+        acc = fmaf((float)q, xrow[k] * s, acc);
+    }
+    return acc;
 }
 
 __device__ __forceinline__ float f4get(const float4& v, int i) {
@@ -110,7 +151,8 @@ struct GemvArgs {
     int ldy;                 // row stride of y and res
     const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
     float eps;
-    int P;                   // row groups: M rows split into P groups of MT (one workgroup each)
+    int P;                   // row groups: M rows split into P = 1 or 2 groups of MT (one workgroup each)
+    int spc_shift;           // INT4: log2(mode) when mode is a power of two, else -1
 };
 
 // ---------------------------------------------------------------------------
@@ -153,6 +195,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     constexpr int RQ_IT = NW * 64;           // row quads per group iteration
     constexpr int CW = SPW * SW;             // columns per workgroup
     constexpr int V = MT * CW;               // accumulators per lane
+    constexpr bool MIX = BITS == 4 && MT <= kGemvMixMaxRows;  // offset-binary fma_mix decode
     __shared__ float red[NG * NW][V];
     __shared__ float sqr[NORM ? NG * NW : 1][MT];
 
@@ -160,20 +203,22 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
     const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
     // Strips of a scale column share an XCD's L2.  Workgroups of one weight
-    // cover (NS + SPW - 1) / SPW strip groups; with several weights side by
-    // side (NG == 1), wt selects the weight.
-    // Workgroup v covers row group p = v % P of strip group v / P: the row
-    // groups of one strip are neighbours in v, so they run on one XCD and the
-    // second read of the strip's codes hits its L2.
+    // cover (NS + SPW - 1) / SPW strip groups (x of the grid); with several
+    // weights side by side (NG == 1), y of the grid selects the weight.
+    // Workgroup v covers row group p = v % P of strip group v / P (P is 1 or 2):
+    // the row groups of one strip are neighbours in v, so they run on one XCD
+    // and the second read of the strip's codes hits its L2.  No integer
+    // division on the way to the first load: every index here is a shift, a
+    // mask or a grid coordinate (a runtime division costs about 30 dependent
+    // instructions, all of them ahead of the loads).
     const int vg = xcd_swizzle(blockIdx.x, gridDim.x);
-    const int prow = a.P > 1 ? vg % a.P : 0;
-    const int jg = a.P > 1 ? vg / a.P : vg;
+    const int prow = vg & (a.P - 1);
+    const int jg = a.P > 1 ? vg >> 1 : vg;
     const int m0 = prow * MT;
     const float* __restrict__ x = a.x + (int64_t)m0 * K;
     const int M = min(MT, a.M - m0);
-    const int per_w = (NS + SPW - 1) / SPW;
-    const int wt = NG == 1 ? jg / per_w : 0;
-    const int j0 = SPW * (jg - wt * per_w);
+    const int wt = NG == 1 ? (int)blockIdx.y : 0;
+    const int j0 = SPW * jg;
     const int widx = NG == 1 ? wt : grp;
     const uint4* __restrict__ Wm = widx == 0 ? a.W[0] : (widx == 1 ? a.W[1] : a.W[2]);
     const float* __restrict__ SCm = widx == 0 ? a.SC[0] : (widx == 1 ? a.SC[1] : a.SC[2]);
@@ -188,7 +233,8 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     __amdgpu_buffer_rsrc_t rS;
     float s_all = 0.0f;
     if constexpr (BITS == 4) {
-        rS = make_rsrc(SCm + (int64_t)(j0 / mode) * Kpad, (uint32_t)Kpad * 4u);
+        const int sc = a.spc_shift >= 0 ? (j0 >> a.spc_shift) : j0 / mode;
+        rS = make_rsrc(SCm + (int64_t)sc * Kpad, (uint32_t)Kpad * 4u);
     } else {
         rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
         if (mode) s_all = SCm[0];
@@ -199,9 +245,10 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 
     __amdgpu_buffer_rsrc_t rG;
     if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
-    float sq[MT];
+    float sq[MT];  // NORM: sum of x^2 per row
+    float sx[MT];  // INT4: sum of xs per row (the offset correction)
 #pragma unroll
-    for (int m = 0; m < MT; ++m) sq[m] = 0.0f;
+    for (int m = 0; m < MT; ++m) sq[m] = 0.0f, sx[m] = 0.0f;
 
     float acc[V];
 #pragma unroll
@@ -215,6 +262,9 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
         float4 xv[U][MT];  // x is loaded with the codes (measured 4-7% faster for M >= 4 than at use)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            // Row quads past the strip read as zero (buffer range).  No guard on
+            // a partial last batch: a branch here would make the compiler wait
+            // for every load before the first use instead of one batch entry at a time.
             const int soff = (it0 + u) * RQ_IT * 16;
 #pragma unroll
             for (int s = 0; s < SPW; ++s) w[u][s] = buf_load16(rW[s], voff, soff);
@@ -253,11 +303,30 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
                 }
+                if constexpr (MIX) sx[m] += (xs[0] + xs[1]) + (xs[2] + xs[3]);
 #pragma unroll
                 for (int s = 0; s < SPW; ++s) {
                     const uint32_t dw[4] = {w[u][s].x, w[u][s].y, w[u][s].z, w[u][s].w};
                     float* a = acc + m * CW + s * SW;
-                    if constexpr (BITS == 4) {
+                    if constexpr (MIX) {
+                        // Nibble e (column e of the strip) as u * 2^-24 (even e) or
+                        // u * 2^-20 (odd e); the masks are shared by all rows m.
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t ob = dw[r] ^ 0x88888888u;
+                            const uint32_t p04 = ob & 0x000F000Fu, p15 = ob & 0x00F000F0u;
+                            const uint32_t ob8 = ob >> 8;
+                            const uint32_t p26 = ob8 & 0x000F000Fu, p37 = ob8 & 0x00F000F0u;
+                            a[0] = fmaf(half_lo(p04), xs[r], a[0]);
+                            a[4] = fmaf(half_hi(p04), xs[r], a[4]);
+                            a[1] = fmaf(half_lo(p15), xs[r], a[1]);
+                            a[5] = fmaf(half_hi(p15), xs[r], a[5]);
+                            a[2] = fmaf(half_lo(p26), xs[r], a[2]);
+                            a[6] = fmaf(half_hi(p26), xs[r], a[6]);
+                            a[3] = fmaf(half_lo(p37), xs[r], a[3]);
+                            a[7] = fmaf(half_hi(p37), xs[r], a[7]);
+                        }
+                    } else if constexpr (BITS == 4) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const uint32_t hi = dw[r] & 0xF0F0F0F0u;         // columns 2b+1, as 16*q
@@ -276,6 +345,19 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
                     }
                 }
             }
+        }
+    }
+
+    if constexpr (MIX) {
+        // Undo the scaling (exact) and the offset per lane: the reduction below
+        // is a plain sum, so correcting each lane's partial sums before it gives
+        // the corrected total with no second reduction for sum(xs).
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float off = -8.0f * sx[m];
+#pragma unroll
+            for (int c = 0; c < CW; ++c)
+                acc[m * CW + c] = fmaf(acc[m * CW + c], (c & 1) ? 1048576.0f : 16777216.0f, off);
         }
     }
 
@@ -298,8 +380,9 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     }
     __syncthreads();
 
-    // Codes of INT4 were read as 16*q: scale the sum back by 1/16 (exact).
-    const float post = (BITS == 4) ? 0.0625f : 1.0f;
+    // MIX: a non-finite total (an infinite or NaN input, or an overflow) takes
+    // the exact k-order sum instead.  INT4 without MIX read its codes as
+    // 16 * q: scale by 1/16 (exact).
     for (int v = threadIdx.x; v < V; v += NG * NW * 64) {
         const int m = v / CW, e = v - m * CW;
         const int n = j0 * SW + e;
@@ -315,14 +398,22 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
                 for (int w = 0; w < NW; ++w) ss += sqr[w][m];
                 inv = 1.0f / sqrtf(ss / (float)K + a.eps);
             }
-            r = r * post;
+            auto i4_total = [&](float t, const uint4* Wg, const float* SCg) {
+                if (!isfinite(t))
+                    t = i4_column_exact<NORM>(Wg, SCg, j0 + e / SW, e % SW, mode, Kpad, RQ,
+                                              a.x + (int64_t)(m0 + m) * K, a.gamma, K);
+                return t;
+            };
+            if constexpr (MIX) r = i4_total(r, NG == 1 ? Wm : a.W[0], NG == 1 ? SCm : a.SC[0]);
+            if constexpr (BITS == 4 && !MIX) r = r * 0.0625f;
             if constexpr (NORM) r = r * inv;
             if (bias) r = r + bias[n];
             if constexpr (NG == 2) {
                 float r2 = 0.0f;
 #pragma unroll
                 for (int w = NW; w < 2 * NW; ++w) r2 += red[w][v];
-                r2 = r2 * post;
+                if constexpr (MIX) r2 = i4_total(r2, a.W[1], a.SC[1]);
+                if constexpr (BITS == 4 && !MIX) r2 = r2 * 0.0625f;
                 if constexpr (NORM) r2 = r2 * inv;
                 if (bias2) r2 = r2 + bias2[n];
                 r = silu_f32(r) * r2;
@@ -605,7 +696,7 @@ bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x
 
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
-    const dim3 grid((unsigned)(nw * ((a.NS + SPW - 1) / SPW) * a.P));
+    const dim3 grid((unsigned)(((a.NS + SPW - 1) / SPW) * a.P), (unsigned)nw);
     const bool k4 = a.K % 4 == 0;
     if constexpr (BITS == 4 && SPW == 1) {  // the norm-fused form serves the INT4 LLaMA block
         if (a.gamma) {
@@ -643,16 +734,23 @@ constexpr int kGemvWaves = 4;
 #define SGQ_GEMV_SPW_MAXMT 2
 #endif
 
+// Row quads a lane keeps in flight at most (each holds codes, a scale quad and
+// an x quad per row): all of K = 4096 (M = 1, four wavefronts) or 8192 (eight)
+// in one batch at M = 1, less as the rows multiply.
+constexpr int gemv_umax(int rows) { return rows <= 1 ? 8 : (rows <= 2 ? 4 : (rows <= 4 ? 2 : 1)); }
+
 template <int BITS, int MT, int NG, int SPW, int NW>
 hipError_t gemv_launch_spw(const GemvArgs& a, int nw, hipStream_t s) {
-    // Register budget: row quads in flight per lane shrink as the batch grows.
-    constexpr int UMAX = (MT * SPW <= 2) ? 4 : (MT * SPW <= 4 ? 2 : 1);
+    // Row quads in flight per lane: enough for all of K in one batch where the
+    // register budget allows (gemv_umax), else batches of UMAX.
+    constexpr int UMAX = gemv_umax(MT * SPW);
     const int per_lane = (a.RQ + NW * 64 - 1) / (NW * 64);
-    const int u = per_lane >= 4 ? 4 : (per_lane >= 2 ? 2 : 1);
-#define SGQ_GEMV_NU(U_)                                                   \
-    if constexpr (U_ <= UMAX) {                                          \
-        if (u >= U_ || U_ == 1) return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s); \
+#define SGQ_GEMV_NU(U_)                                                                              \
+    if constexpr (U_ <= UMAX) {                                                                      \
+        if (per_lane > (U_ == 8 ? 6 : (U_ == 6 ? 4 : U_ / 2)) || U_ == 1) return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s); \
     }
+    SGQ_GEMV_NU(8)
+    SGQ_GEMV_NU(6)
     SGQ_GEMV_NU(4)
     SGQ_GEMV_NU(2)
     SGQ_GEMV_NU(1)
@@ -674,17 +772,22 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
     // 2048 -> 2048 at M=4 3.9 -> 3.7 us.
     if ((int64_t)nw * a.NS * a.P < 2 * kCus && a.RQ >= 8 * 64)
         return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
+    // A K too long for one batch of four wavefronts but within one batch of
+    // eight: eight wavefronts, so that every load is in flight at once instead
+    // of batches that each wait a full memory latency (measured on MI355X,
+    // 11008 -> 4096 at M=1: 8.2 -> 7.8 us).
+    if constexpr (MT == 1) {
+        constexpr int um = gemv_umax(1);
+        if (a.RQ > um * kGemvWaves * 64 && a.RQ <= um * 2 * kGemvWaves * 64)
+            return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
+    }
     return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(a, nw, s);
 }
 
 template <int BITS, int NG>
 hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.M = (int)M;
-#ifdef SGQ_ROWS4
-    constexpr int kRowsMax = 4;
-#else
-    constexpr int kRowsMax = 8;
-#endif
+    constexpr int kRowsMax = 8;  // kGemvMaxM = 16 rows make at most two row groups
     // All rows in one launch: M <= 4 as one row group, larger M in row groups
     // of kRowsMax (each a workgroup of its own over the same strip).
     if (M <= 1) {
@@ -700,6 +803,7 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }
     a.P = (int)((M + kRowsMax - 1) / kRowsMax);
+    if (a.P > 2) return hipErrorInvalidValue;  // the kernel's row-group index takes P = 1 or 2
     return gemv_launch<BITS, kRowsMax, NG>(a, nw, s);
 }
 
@@ -711,6 +815,9 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
     a.K = (int)K;
     a.N = (int)N;
     a.mode = mode;
+    a.spc_shift = -1;
+    for (int sh = 0; sh < 31; ++sh)
+        if (mode == (1 << sh)) a.spc_shift = sh;
     a.Kpad = (int)Kpad;
     a.RQ = (int)RQ;
     a.NS = (int)NS;

@@ -255,6 +255,41 @@ def test_nonfinite_propagates(sgq, dev):
         assert torch.isnan(y).all()
 
 
+def _same_nonfinite(y, yref):
+    """NaN where the reference has NaN, +-inf with its sign, finite entries within TOL."""
+    assert np.array_equal(np.isnan(y), np.isnan(yref))
+    assert np.array_equal(np.isposinf(y), np.isposinf(yref))
+    assert np.array_equal(np.isneginf(y), np.isneginf(yref))
+    fin = np.isfinite(yref)
+    if fin.any():
+        err = np.max(np.abs(y[fin].astype(np.float64) - yref[fin]))
+        assert err <= TOL * max(np.max(np.abs(yref[fin])), 1e-30)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_infinite_activation_matches_reference(sgq, dev, oracle, synth, M):
+    # An infinite activation gives +-inf in every column whose code is nonzero
+    # and NaN where it meets a zero code (inf * 0), as in the reference's
+    # x . (q * s); a row with both signs of infinity is NaN.  The INT4 decode
+    # path sums an offset form of the codes, so it must hand such rows to its
+    # exact k-order fallback rather than produce inf - inf.
+    K, N, G = 1024, 512, 128
+    W = synth.normal((K, N), 91, 0, 0.0, 0.02)
+    x = synth.normal((M, K), 91, 1)
+    x[0, 17] = np.inf
+    if M > 1:
+        x[M - 1, 600] = -np.inf
+    if M > 2:
+        x[1, 3] = np.inf
+        x[1, 900] = -np.inf
+    q, s = oracle.quantize_int4(W, G)
+    qw = sgq.quantize_int4(_to_dev(W, dev), G)
+    y = _np(sgq.quantized_matmul(_to_dev(x, dev), qw))
+    yref = oracle.quantized_matmul_int4(x, q, s, G)
+    assert np.isinf(yref).any() and np.isnan(yref).any()
+    _same_nonfinite(y, yref)
+
+
 def test_dequantize_matches_reference_product(sgq, dev, oracle, synth):
     W = synth.normal((130, 72), 51, 0, 0.0, 0.02)
     qx = sgq.quantize_int8(_to_dev(W, dev), 1)

@@ -114,6 +114,30 @@ def test_swiglu_vs_oracle(sgq, dev, oracle, synth, name, bits_, M, K, N, G, sche
     assert e <= TOL
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_swiglu_infinite_activation(sgq, dev, oracle, synth, M):
+    # +-inf in x reaches the gate and up sums of the fused INT4 GEMV: NaN and
+    # +-inf must land where the reference's silu(x.Wg + bg) * (x.Wu + bu) has
+    # them (both weights take the exact fallback of the offset-binary decode).
+    K, N, G = 1024, 384, 128
+    Wg, Wu, bg, bu = _weights(synth, K, N, 13)
+    x = synth.normal((M, K), 13, 1)
+    x[0, 40] = np.inf
+    x[M - 1, 700] = -np.inf if M > 1 else x[M - 1, 700]
+    qg, sg = oracle.quantize_int4(Wg, G)
+    qu, su = oracle.quantize_int4(Wu, G)
+    href = oracle.swiglu_int4(x, qg, sg, qu, su, G, bg, bu)
+    wg, wu = sgq.quantize_int4(_to_dev(Wg, dev), G), sgq.quantize_int4(_to_dev(Wu, dev), G)
+    h = _np(sgq.quantized_swiglu(_to_dev(x, dev), wg, wu, _to_dev(bg, dev), _to_dev(bu, dev)))
+    assert not np.isfinite(href).all()
+    assert np.array_equal(np.isnan(h), np.isnan(href))
+    assert np.array_equal(np.isposinf(h), np.isposinf(href))
+    assert np.array_equal(np.isneginf(h), np.isneginf(href))
+    fin = np.isfinite(href)
+    if fin.any():
+        assert np.max(np.abs(h[fin] - href[fin])) <= TOL * max(np.max(np.abs(href[fin])), 1e-30)
+
+
 @pytest.mark.parametrize("bits_,M", [(4, 1), (4, 7), (4, 16), (8, 3), (8, 16), (4, 48), (8, 40)])
 def test_swiglu_matches_two_linears(sgq, dev, oracle, synth, bits_, M):
     # The fused form and two separate library projections followed by the
