@@ -35,6 +35,27 @@ namespace sgq {
 constexpr int64_t kPadK = 16;  // rows are padded to a multiple of this
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Division of n in [0, 2^31) by a divisor d >= 1 fixed at launch, as a
+// multiply-high, an add and a shift (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", 1994: m = floor(2^32 (2^l - d) / d)
+// + 1 with l = ceil(log2 d); then n / d = (mulhi(n, m) + n) >> l, where the sum
+// stays below 2^32 because n < 2^31).  Kernels use it for indices that would
+// otherwise need a runtime integer division (about 30 dependent instructions).
+struct FastDiv {
+    uint32_t m;
+    int l;
+    __host__ __device__ FastDiv() : m(1), l(0) {}
+    __host__ explicit FastDiv(uint32_t d) {
+        l = 0;
+        while ((1ull << l) < d) ++l;
+        m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    }
+    __host__ __device__ int div(int n) const {
+        const uint32_t hi = (uint32_t)(((uint64_t)(uint32_t)n * m) >> 32);
+        return (int)((hi + (uint32_t)n) >> l);
+    }
+};
 __host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
 struct I8Geom {

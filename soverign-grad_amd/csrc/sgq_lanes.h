@@ -85,6 +85,63 @@ __device__ __forceinline__ void lane_reduce(float* v, int lane, int& base) {
     }
 }
 
+// As lane_reduce, but a one-value step on lane bit 4 or 8 is a DPP row_shr
+// accumulation (v += v of lane - O within the 16-lane row, zero below the row
+// start) instead of an xor butterfly through ds_swizzle: VALU latency instead
+// of an LDS round trip per step.  The totals are then only in the lanes with
+// those bits set (the last lanes of each row); red_tail_writer(H) tells which
+// lanes hold a total (once).
+template <int H, int I>
+__device__ __forceinline__ void lane_reduce_tail(float* v, int lane, int& base) {
+    static_assert((H & (H - 1)) == 0, "halving needs a power of two");
+    if constexpr (I < 6) {
+        constexpr int O = red_bit(I);
+        if constexpr (H > 1) {
+            constexpr int h = H / 2;
+            const bool upper = (lane & O) != 0;
+            if constexpr (O >= 16) {
+#pragma unroll
+                for (int i = 0; i < h; ++i) v[i] = swap_add<O>(v[i], v[i + h]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < h; ++i) {
+                    const float send = upper ? v[i] : v[i + h];
+                    const float keep = upper ? v[i + h] : v[i];
+                    v[i] = keep + xor_lane<O>(send, lane);
+                }
+            }
+            if (upper) base += h;
+            lane_reduce_tail<h, I + 1>(v, lane, base);
+        } else if constexpr (O == 4 || O == 8) {
+            v[0] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[0]), 0x110 + O, 0xF, 0xF, true));
+            lane_reduce_tail<1, I + 1>(v, lane, base);
+        } else {
+            v[0] += xor_lane<O>(v[0], lane);
+            lane_reduce_tail<1, I + 1>(v, lane, base);
+        }
+    }
+}
+
+// Lanes holding a total after lane_reduce_tail<H>: (lane & mask) == value.
+// Bits 4 and 8 reduced by row_shr must be set; bits reduced by a butterfly
+// must be clear (their lanes hold copies).
+struct LaneSel {
+    int mask, value;
+};
+constexpr LaneSel red_tail_writer(int H) {
+    LaneSel s{0, 0};
+    for (int i = 0; i < 6; ++i) {
+        const int o = red_bit(i);
+        if (H > 1) {
+            H /= 2;
+        } else {
+            s.mask |= o;
+            if (o == 4 || o == 8) s.value |= o;
+        }
+    }
+    return s;
+}
+
 // Values a lane holds after lane_reduce, and the lane bits whose lanes then
 // hold identical totals.
 constexpr int red_left(int H) { return H >= 64 ? H / 64 : 1; }

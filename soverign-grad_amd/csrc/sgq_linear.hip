@@ -134,8 +134,8 @@ __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)
 constexpr int kXcds = 8;
 __device__ __forceinline__ int xcd_swizzle(int b, int n) {
     const int per = n / kXcds;
-    if (b >= per * kXcds) return b;
-    return (b % kXcds) * per + b / kXcds;
+    const int sw = (b % kXcds) * per + b / kXcds;
+    return b >= per * kXcds ? b : sw;  // a select, not a branch, ahead of the first loads
 }
 
 // Arguments of one GEMV launch (passed by value in the kernel arguments).
@@ -152,7 +152,9 @@ struct GemvArgs {
     const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
     float eps;
     int P;                   // row groups: M rows split into P = 1 or 2 groups of MT (one workgroup each)
-    int spc_shift;           // INT4: log2(mode) when mode is a power of two, else -1
+    FastDiv spc;             // INT4: division by mode (strips per scale column)
+    int nblk;                // grid x (passed here: reading the hidden gridDim argument cost a second
+                             // dependent round of kernel-argument loads ahead of the first data load)
 };
 
 // ---------------------------------------------------------------------------
@@ -211,9 +213,9 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // division on the way to the first load: every index here is a shift, a
     // mask or a grid coordinate (a runtime division costs about 30 dependent
     // instructions, all of them ahead of the loads).
-    const int vg = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int vg = xcd_swizzle(blockIdx.x, a.nblk);
     const int prow = vg & (a.P - 1);
-    const int jg = a.P > 1 ? vg >> 1 : vg;
+    const int jg = vg >> (a.P - 1);
     const int m0 = prow * MT;
     const float* __restrict__ x = a.x + (int64_t)m0 * K;
     const int M = min(MT, a.M - m0);
@@ -233,8 +235,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     __amdgpu_buffer_rsrc_t rS;
     float s_all = 0.0f;
     if constexpr (BITS == 4) {
-        const int sc = a.spc_shift >= 0 ? (j0 >> a.spc_shift) : j0 / mode;
-        rS = make_rsrc(SCm + (int64_t)sc * Kpad, (uint32_t)Kpad * 4u);
+        rS = make_rsrc(SCm + (int64_t)a.spc.div(j0) * Kpad, (uint32_t)Kpad * 4u);
     } else {
         rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
         if (mode) s_all = SCm[0];
@@ -363,10 +364,10 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 
     // Combine the 64 lanes of each wavefront, then the NW wavefronts.
     int base = 0;
-    lane_reduce<V, 0>(acc, lane, base);
+    lane_reduce_tail<V, 0>(acc, lane, base);
     constexpr int left = red_left(V);
-    constexpr int dup_mask = red_dup_mask(V);
-    if ((lane & dup_mask) == 0) {
+    constexpr LaneSel wsel = red_tail_writer(V);
+    if ((lane & wsel.mask) == wsel.value) {
 #pragma unroll
         for (int i = 0; i < left; ++i) red[wave][base + i] = acc[i];
     }
@@ -697,21 +698,23 @@ bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
     const dim3 grid((unsigned)(((a.NS + SPW - 1) / SPW) * a.P), (unsigned)nw);
+    GemvArgs ag = a;
+    ag.nblk = (int)grid.x;
     const bool k4 = a.K % 4 == 0;
     if constexpr (BITS == 4 && SPW == 1) {  // the norm-fused form serves the INT4 LLaMA block
         if (a.gamma) {
             if (k4)
-                k_gemv<BITS, MT, NW, U, true, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(a);
+                k_gemv<BITS, MT, NW, U, true, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(ag);
             else
-                k_gemv<BITS, MT, NW, U, false, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(a);
+                k_gemv<BITS, MT, NW, U, false, NG, SPW, true><<<grid, NG * NW * 64, 0, s>>>(ag);
             return hipGetLastError();
         }
     }
     if (a.gamma) return hipErrorInvalidValue;
     if (k4)
-        k_gemv<BITS, MT, NW, U, true, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(a);
+        k_gemv<BITS, MT, NW, U, true, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(ag);
     else
-        k_gemv<BITS, MT, NW, U, false, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(a);
+        k_gemv<BITS, MT, NW, U, false, NG, SPW, false><<<grid, NG * NW * 64, 0, s>>>(ag);
     return hipGetLastError();
 }
 
@@ -815,9 +818,7 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
     a.K = (int)K;
     a.N = (int)N;
     a.mode = mode;
-    a.spc_shift = -1;
-    for (int sh = 0; sh < 31; ++sh)
-        if (mode == (1 << sh)) a.spc_shift = sh;
+    a.spc = FastDiv((uint32_t)(mode > 0 ? mode : 1));
     a.Kpad = (int)Kpad;
     a.RQ = (int)RQ;
     a.NS = (int)NS;
