@@ -724,19 +724,6 @@ hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
 // cross-wave LDS reduction short.
 constexpr int kGemvWaves = 4;
 
-// Strips per workgroup for MT <= SGQ_GEMV_SPW_MAXMT.  Measured on MI355X at
-// M=1: 2 strips x 8 wavefronts is 7% faster on 4096->11008 but 13-18% slower
-// on 11008->4096 and 2048->2048 (half the workgroups), so the default is 1.
-#ifndef SGQ_GEMV_SPW
-#define SGQ_GEMV_SPW 1
-#endif
-#ifndef SGQ_GEMV_SPW_WAVES
-#define SGQ_GEMV_SPW_WAVES 4
-#endif
-#ifndef SGQ_GEMV_SPW_MAXMT
-#define SGQ_GEMV_SPW_MAXMT 2
-#endif
-
 // Row quads a lane keeps in flight at most (each holds codes, a scale quad and
 // an x quad per row): all of K = 4096 (M = 1, four wavefronts) or 8192 (eight)
 // in one batch at M = 1, less as the rows multiply.
@@ -763,10 +750,20 @@ hipError_t gemv_launch_spw(const GemvArgs& a, int nw, hipStream_t s) {
 
 template <int BITS, int MT, int NG>
 hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
-    if constexpr (NG == 1 && SGQ_GEMV_SPW > 1 && MT <= SGQ_GEMV_SPW_MAXMT) {
-        // INT4 strips of one workgroup must share a scale column.
-        if (nw == 1 && (BITS == 8 || a.mode % SGQ_GEMV_SPW == 0))
-            return gemv_launch_spw<BITS, MT, NG, SGQ_GEMV_SPW, SGQ_GEMV_SPW_WAVES>(a, nw, s);
+    if constexpr (BITS == 4 && NG == 1 && MT <= 2) {
+        // Two strips per workgroup (they must share a scale column) load each
+        // x and scale quad once for both: a third fewer load instructions per
+        // code byte, which is what the one- and two-row GEMV waits on.  Only
+        // where that still leaves a workgroup per CU, and with enough
+        // wavefronts to keep all of K in one batch of loads.  Measured on
+        // MI355X at M=1: 4096->4096 4.30 -> 4.21 us, 4096->11008 7.67 -> 6.93,
+        // 11008->4096 7.39 -> 7.22 (16 wavefronts); M=2 4096->11008 9.11 -> 8.52.
+        if (nw == 1 && a.mode % 2 == 0 && a.NS >= 2 * kCus) {
+            constexpr int um = gemv_umax(2 * MT);
+            if (a.RQ <= um * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, kGemvWaves>(a, nw, s);
+            if (a.RQ <= um * 2 * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, 2 * kGemvWaves>(a, nw, s);
+            if (a.RQ <= um * 4 * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, 4 * kGemvWaves>(a, nw, s);
+        }
     }
     // Few strips for the GPU (under two workgroups per CU) and a K long enough
     // for eight wavefronts: split K over eight wavefronts instead of four, so
