@@ -138,6 +138,12 @@ __device__ __forceinline__ int xcd_swizzle(int b, int n) {
     return b >= per * kXcds ? b : sw;  // a select, not a branch, ahead of the first loads
 }
 
+// Workgroup barrier ordering LDS accesses only: waits for this wave's LDS
+// operations, not for its global loads.  __syncthreads() is a release fence
+// as well, and gfx950 counts loads and stores on one counter (vmcnt), so it
+// waits for every load in flight -- prefetched data included.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Arguments of one GEMV launch (passed by value in the kernel arguments).
 struct GemvArgs {
     const float* x;  // [M, K] rows of this pass
@@ -457,8 +463,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // mode: INT8 -> per_tensor flag; INT4 -> strips per scale column (spc).
     // Workgroup b computes split b % KS (stages [kt0, kt1) of sps each) of
     // tile b / KS; with KS > 1 it writes part[split][M][N] instead of y.
+    constexpr int SW = (BITS == 4) ? 8 : 4;
+    constexpr int KQ = kBK / 4;                 // row quads per stage
+    constexpr int kStrips = kBN / SW;           // strips per tile: 16 (INT4) or 32 (INT8)
+    // INT4: B dequantized to fp32 [n][k].  INT8: B as the raw 16-byte chunks
+    // (strip, row quad), each dword four consecutive k of one column -- what
+    // an MFMA lane consumes -- with the strip stride padded to KQ*4 + 8 dwords
+    // so the 32 lanes of a half-wave read 32 different banks.
     __shared__ __attribute__((aligned(16))) float As[2][kBM][kLdsStride];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kBN][kLdsStride];
+    __shared__ __attribute__((aligned(16))) float Bs[BITS == 4 ? 2 : 1][BITS == 4 ? kBN : 1][kLdsStride];
+    __shared__ __attribute__((aligned(16))) uint4 Bq[BITS == 8 ? 2 : 1][BITS == 8 ? kStrips : 1][KQ + 2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int ntn = (N + kBN - 1) / kBN;
@@ -473,9 +487,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         make_rsrc(S, BITS == 8 ? (mode ? 4u : (uint32_t)K * 4u) : (uint32_t)(((NS + mode - 1) / mode) * Kpad) * 4u);
     const float s_all = (BITS == 8 && mode) ? S[0] : 0.0f;
 
-    constexpr int SW = (BITS == 4) ? 8 : 4;
-    constexpr int KQ = kBK / 4;                 // row quads per stage
-    constexpr int kStrips = kBN / SW;           // strips per tile: 16 (INT4) or 32 (INT8)
     constexpr int kBChunks = kStrips * KQ;      // chunks of B per stage
     constexpr int kAVec = kBM * kBK / 4 / kThreads;  // float4 of A per thread per stage
     constexpr int kBPer = (kBChunks + kThreads - 1) / kThreads;  // chunks of B per thread per stage
@@ -488,6 +499,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     struct Regs {
         float4 a[kAVec];
         uint4 b[kBPer];
+        float4 s;  // INT8 per-channel: scales of this thread's four A columns k
     };
     // Buffer resources over this tile's rows of x and strips of W: rows past
     // M and strips past NS read as zero; k past K and row quads past RQ (which
@@ -522,13 +534,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             const int vo = ((t / KQ) * RQ + t % KQ) * 16;
             rg.b[i] = buf_load16(rW, (t < kBChunks && rq < RQ) ? vo : kOobOff, soffB);
         }
+        // Every A float4 of this thread sits at column quad tid % KQ of the stage.
+        if constexpr (BITS == 8)
+            if (!mode) rg.s = buf_load4f<KALIGN4>(rS, (tid % KQ) * 16, kt * kBK * 4);  // zero past K
     };
     auto store = [&](const Regs& rg, int buf, int kt) {
+        // INT8: the scale of row k of W goes into column k of A, (x * s) * q
+        // (the reference forms x * (q * s): the same products up to one
+        // rounding); columns past K are exactly zero, also for a non-finite
+        // per-tensor scale.
+        float4 sa = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        if constexpr (BITS == 8) {
+            if (mode) {
+                const int k = kt * kBK + (tid % KQ) * 4;
+                sa = make_float4(k < K ? s_all : 0.0f, k + 1 < K ? s_all : 0.0f, k + 2 < K ? s_all : 0.0f,
+                                 k + 3 < K ? s_all : 0.0f);
+            } else {
+                sa = rg.s;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < kAVec; ++i) {
             const int idx = tid + kThreads * i;
             const int row = idx / KQ, kq = idx % KQ;
-            *(float4*)&As[buf][row][kq * 4] = rg.a[i];
+            if constexpr (BITS == 8)
+                *(float4*)&As[buf][row][kq * 4] =
+                    make_float4(rg.a[i].x * sa.x, rg.a[i].y * sa.y, rg.a[i].z * sa.z, rg.a[i].w * sa.w);
+            else
+                *(float4*)&As[buf][row][kq * 4] = rg.a[i];
         }
 #pragma unroll
         for (int i = 0; i < kBPer; ++i) {
@@ -537,25 +570,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             const int jl = t / KQ, kl = (t % KQ) * 4;
             const int k = kt * kBK + kl;
             const uint32_t dw[4] = {rg.b[i].x, rg.b[i].y, rg.b[i].z, rg.b[i].w};
-            if (BITS == 8) {
-                float sc[4];
-                if (mode) {
-                    // Rows past K must be exactly zero, also for a non-finite per-tensor scale.
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) sc[r] = (k + r < K) ? s_all : 0.0f;
-                } else {
-                    const float4 s4 = buf_load4f<KALIGN4>(rS, kl * 4, kt * kBK * 4);  // zero past K
-                    sc[0] = s4.x, sc[1] = s4.y, sc[2] = s4.z, sc[3] = s4.w;
-                }
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    float4 v;
-                    v.x = i8_byte(dw[d], 0) * sc[0];
-                    v.y = i8_byte(dw[d], 1) * sc[1];
-                    v.z = i8_byte(dw[d], 2) * sc[2];
-                    v.w = i8_byte(dw[d], 3) * sc[3];
-                    *(float4*)&Bs[buf][jl * 4 + d][kl] = v;
-                }
+            if constexpr (BITS == 8) {
+                (void)dw;
+                (void)k;
+                Bq[buf][jl][kl / 4] = rg.b[i];
             } else {
                 const int bj = n0 / SW + jl;
                 const int jc = bj < NS ? bj : NS - 1;
@@ -594,7 +612,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // the MFMAs), `fill` is free and receives the loads of stage kt+2.
     auto stage = [&](int kt, const Regs& next, Regs& fill) {
         const int buf = kt & 1;
-        if (kt + 2 < kt1) load(fill, kt + 2);
+        // Unconditional: past the last stage the loads read zeros (k past K,
+        // row quads past RQ); a guard here would make the compiler wait for
+        // these loads at the join, before the next stage's LDS store.
+        load(fill, kt + 2);
 #pragma unroll
         for (int sb = 0; sb < kBK / 16; ++sb) {
             if (sb == kStoreBlock && kt + 1 < kt1) store(next, buf ^ 1, kt + 1);
@@ -602,8 +623,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             float4 a[4], b[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] = *(const float4*)&As[buf][wm * 64 + i * 16 + lr][lk];
+            if constexpr (BITS == 8) {
+                // one dword: column n, rows lk .. lk+3, converted here
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = *(const float4*)&Bs[buf][wn * 64 + j * 16 + lr][lk];
+                for (int j = 0; j < 4; ++j) {
+                    const int nl = wn * 64 + j * 16 + lr;
+                    const uint32_t bd = ((const uint32_t*)&Bq[buf][nl >> 2][lk >> 2])[nl & 3];
+                    b[j] = make_float4(cvt_sbyte<0>(bd), cvt_sbyte<1>(bd), cvt_sbyte<2>(bd), cvt_sbyte<3>(bd));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = *(const float4*)&Bs[buf][wn * 64 + j * 16 + lr][lk];
+            }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
@@ -613,14 +644,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4get(a[i], kk), f4get(b[j], kk), acc[i][j],
                                                                          0, 0, 0);
         }
-        __syncthreads();
+        lds_barrier();
     };
 
     Regs r0, r1;
     load(r0, kt0);
     if (kt0 + 1 < kt1) load(r1, kt0 + 1);
     store(r0, kt0 & 1, kt0);
-    __syncthreads();
+    lds_barrier();
     for (int kt = kt0; kt < kt1; kt += 2) {
         stage(kt, r1, r0);
         if (kt + 1 < kt1) stage(kt + 1, r0, r1);
