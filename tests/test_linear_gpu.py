@@ -78,6 +78,8 @@ def _case(sgq, dev, oracle, synth, bits_, M, K, N, G=128, scheme=0, bias=False, 
         ("C1_int8_pt_bias_M128", 8, 128, 1024, 1024, 0, 0, True, 0),
         ("C2_int4_g128_M1", 4, 1, 4096, 4096, 128, 0, False, 1),
         ("C3_gate_M1", 4, 1, 4096, 11008, 128, 0, False, 2),
+        ("C3_gate_M2", 4, 2, 4096, 11008, 128, 0, False, 2),
+        ("C3_down_M2", 4, 2, 11008, 4096, 128, 0, False, 2),
         ("C3_gate_M4", 4, 4, 4096, 11008, 128, 0, False, 2),
         ("C3_gate_M8", 4, 8, 4096, 11008, 128, 0, False, 2),
         ("C3_gate_M16", 4, 16, 4096, 11008, 128, 0, False, 2),
