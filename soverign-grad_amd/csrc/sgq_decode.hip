@@ -252,38 +252,47 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
 }
 
 // ctx[b] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) over the chunks
-// that hold keys (M = max_c m_c).  Grid (ceil(D / (4 * kBlock)), B).  The
-// chunk weights are computed once into LDS; each thread then sums its float4
-// column over the chunks, eight chunks' loads at a time.  A sequence with an
-// invalid position gets a NaN row.
+// that hold keys (M = max_c m_c).  Grid (ceil(D / (4 * kCombCols)), B): a
+// workgroup owns kCombCols float4 columns of one sequence, and its
+// kBlock / kCombCols thread groups split the chunks (group g takes chunks g,
+// g + groups, ...), so each thread's loads of a batch are all in flight and
+// many workgroups share the work even for one long sequence.  The chunk
+// weights exp(m_c - M) go to LDS first; the group partial sums are added in
+// group order through LDS (deterministic).  A sequence with an invalid
+// position gets a NaN row.
+constexpr int kCombCols = 16;
+constexpr int kCombGroups = kBlock / kCombCols;  // 16
 __global__ __launch_bounds__(kBlock) void k_attn_combine(const float* __restrict__ part, int nc, int CS, int64_t D,
                                                          const int32_t* __restrict__ pos, int64_t max_tokens,
                                                          int64_t max_len, float* __restrict__ ctx) {
     __shared__ float wgt[kAttnMaxChunks];
-    __shared__ float lsum[kAttnMaxChunks];
+    __shared__ float4 grp[kCombGroups][kCombCols];
     __shared__ float red[kBlock / 64];
+    __shared__ float lred[kBlock / 64];
     const int b = blockIdx.y;
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;  // float4 index
+    const int g = threadIdx.x / kCombCols, col = threadIdx.x % kCombCols;
+    const int64_t D4 = D / 4;
+    const int64_t i = (int64_t)blockIdx.x * kCombCols + col;  // float4 column
+    const bool ok = i < D4;
     const int T = seq_keys(pos, b, max_tokens, max_len);
     if (T < 0) {
-        if (i * 4 < D) ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(NAN, NAN, NAN, NAN);
+        if (g == 0 && ok) ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(NAN, NAN, NAN, NAN);
         return;
     }
     const int used = (T + CS - 1) / CS;
     const float* pb = part + (int64_t)b * nc * (D + 4);
-    const bool col = i * 4 < D;
-    // The first eight chunks' values of this column load now, under the
-    // weight computation below.
-    float4 v0[8];
+    // The first batch of this thread's chunk values loads now, under the
+    // weight computation.
+    constexpr int CB = 8;  // chunks per thread per batch
+    float4 v0[CB];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int cc = u < used ? u : 0;
-        v0[u] = col ? ((const float4*)(pb + (int64_t)cc * (D + 4)))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < CB; ++u) {
+        const int cc = g + u * kCombGroups;
+        v0[u] = (ok && cc < used) ? ((const float4*)(pb + (int64_t)cc * (D + 4)))[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float mx = -INFINITY;
     for (int cc = threadIdx.x; cc < used; cc += kBlock) {
         const float v = pb[(int64_t)cc * (D + 4) + D];
-        lsum[cc] = pb[(int64_t)cc * (D + 4) + D + 1];
         wgt[cc] = v;
         mx = fmaxf(mx, v);
     }
@@ -293,24 +302,33 @@ __global__ __launch_bounds__(kBlock) void k_attn_combine(const float* __restrict
     float M = red[0];
 #pragma unroll
     for (int w = 1; w < kBlock / 64; ++w) M = fmaxf(M, red[w]);
-    __syncthreads();
-    for (int cc = threadIdx.x; cc < used; cc += kBlock) wgt[cc] = expf(wgt[cc] - M);
+    float lp = 0.0f;  // this thread's share of L = sum_c l_c w_c, in chunk order per thread
+    for (int cc = threadIdx.x; cc < used; cc += kBlock) {
+        const float w = expf(wgt[cc] - M);
+        wgt[cc] = w;
+        lp = fmaf(pb[(int64_t)cc * (D + 4) + D + 1], w, lp);
+    }
+    lp = wave_sum(lp);
+    if ((threadIdx.x & 63) == 0) lred[threadIdx.x >> 6] = lp;
     __syncthreads();
     float L = 0.0f;
-    for (int cc = 0; cc < used; ++cc) L = fmaf(lsum[cc], wgt[cc], L);
-    if (!col) return;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = 0; c0 < used; c0 += 8) {
-        float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int cc = c0 + u < used ? c0 + u : c0;
-            v[u] = c0 == 0 ? v0[u] : ((const float4*)(pb + (int64_t)cc * (D + 4)))[i];
+    for (int w = 0; w < kBlock / 64; ++w) L += lred[w];
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = 0; c0 < used; c0 += CB * kCombGroups) {
+        float4 v[CB];
+#pragma unroll
+        for (int u = 0; u < CB; ++u) {
+            const int cc = c0 + g + u * kCombGroups;
+            v[u] = c0 == 0 ? v0[u]
+                           : ((ok && cc < used) ? ((const float4*)(pb + (int64_t)cc * (D + 4)))[i]
+                                                : make_float4(0.f, 0.f, 0.f, 0.f));
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (c0 + u < used) {  // uniform over the workgroup
-                const float w = wgt[c0 + u];
+        for (int u = 0; u < CB; ++u) {
+            const int cc = c0 + g + u * kCombGroups;
+            if (cc < used) {
+                const float w = wgt[cc];
                 o.x = fmaf(v[u].x, w, o.x);
                 o.y = fmaf(v[u].y, w, o.y);
                 o.z = fmaf(v[u].z, w, o.z);
@@ -318,8 +336,18 @@ __global__ __launch_bounds__(kBlock) void k_attn_combine(const float* __restrict
             }
         }
     }
-    const float inv = 1.0f / L;
-    ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    grp[g][col] = o;
+    __syncthreads();
+    if (g == 0 && ok) {
+        float4 t = grp[0][col];
+#pragma unroll
+        for (int gg = 1; gg < kCombGroups; ++gg) {
+            const float4 u = grp[gg][col];
+            t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+        }
+        const float inv = 1.0f / L;
+        ((float4*)(ctx + (int64_t)b * D))[i] = make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv);
+    }
 }
 
 // Poisons the output rows of sequences with an invalid position (so the
@@ -356,11 +384,19 @@ hipError_t launch_add(const float* a, const float* b, float* y, int64_t n, hipSt
     return hipGetLastError();
 }
 
+#ifndef SGQ_ATTN_WGS
+#define SGQ_ATTN_WGS 2048
+#endif
 AttnPlan attn_plan(int64_t B, int64_t max_len) {
-    // About 512 workgroups over all sequences; chunks of 8, 16, 32 or 64 keys
-    // (kAttnMaxChunk), at most kAttnMaxChunks chunks per sequence.
+    // Up to SGQ_ATTN_WGS workgroups over all sequences; chunks of 8, 16, 32 or
+    // 64 keys (kAttnMaxChunk), at most kAttnMaxChunks chunks per sequence.
+    // Short chunks keep every load of a workgroup's phase in flight at once
+    // (a chunk of 8 keys is one batch); the combine kernel splits the chunks
+    // over thread groups, so many chunks cost it little.
     int64_t cs = 8;
-    while (cs < kAttnMaxChunk && (ceil_div(max_len, cs) * B > 512 || ceil_div(max_len, cs) > kAttnMaxChunks)) cs *= 2;
+    while (cs < kAttnMaxChunk &&
+           (ceil_div(max_len, cs) * B > SGQ_ATTN_WGS || ceil_div(max_len, cs) > kAttnMaxChunks))
+        cs *= 2;
     AttnPlan p;
     p.CS = (int)cs;
     p.NC = (int)ceil_div(max_len, cs);
@@ -398,7 +434,7 @@ hipError_t launch_attention_decode(const float* q, const float* knew, const floa
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.NC > 1) {
-        k_attn_combine<<<dim3((unsigned)ceil_div(D, 4 * kBlock), (unsigned)B), kBlock, 0, s>>>(
+        k_attn_combine<<<dim3((unsigned)ceil_div(D, 4 * kCombCols), (unsigned)B), kBlock, 0, s>>>(
             part, p.NC, p.CS, D, pos, max_tokens, max_len, ctx);
     } else {
         k_poison_rows<<<dim3((unsigned)ceil_div(D, kBlock), (unsigned)B), kBlock, 0, s>>>(pos, max_tokens, max_len, D,
