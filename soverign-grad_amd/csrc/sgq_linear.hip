@@ -677,6 +677,278 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 }
 
+// ---------------------------------------------------------------------------
+// Three-term bf16 MFMA GEMM (prefill).  The fp32 products of the reference's
+// matmul run on the bf16 matrix cores, which gfx950 issues at 16 times the
+// fp32 MFMA rate, without giving up fp32 results:
+//   - every operand of the bf16 MFMAs is exact.  A code q (|q| <= 127) is a
+//     bf16 integer.  The activation xs = x * s (the weight's scale folded in,
+//     one rounding as in the fp32 kernels) is split as xs = h + m + l, where
+//     h keeps the leading 8 significant bits of xs (truncation), m the next 8
+//     of the remainder and l the rest, which is at most 8 bits: the three are
+//     bf16 numbers and their sum is xs exactly;
+//   - a bf16 x bf16 product is exact in fp32, and v_mfma_f32_16x16x32_bf16
+//     sums into an fp32 accumulator, so acc += h.q, m.q and l.q (three MFMAs
+//     per 16x16x32 block) computes sum(xs * q) with fp32 accumulation.
+//     (Measured on the box: a 32-term dot product of split fp32 values and
+//     codes came out within 5e-9 of fp64, against 1.6e-8 for an fp32 FMA chain.)
+// An output whose total is not finite (an infinite or NaN input, or an
+// overflow, where h + m + l would be inf - inf) is recomputed by its thread
+// as the reference's x . (q * s) in k order, so infinities and NaNs land
+// where the reference puts them.
+//
+// Tile 128x128, four wavefronts in 2x2, each 64x64 as 4x4 MFMA blocks; one
+// 32-k stage per LDS buffer, double-buffered, global loads two stages ahead
+// (as k_gemm).  LDS entries are 16 bytes, eight consecutive k of one row (A
+// planes) or one column (B): one MFMA operand.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kB3BK = 32;           // k per stage: one 16x16x32 MFMA step
+constexpr int kB3KG = kB3BK / 8;    // 8-k groups per stage
+constexpr int kB3RQ = kB3BK / 4;    // row quads per stage
+
+// Upper halves (bf16 bits) of two floats in one dword, lo in bits 0-15.
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+__device__ __forceinline__ float trunc_bf16(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFF0000u); }
+
+// Splits eight floats into the bf16 planes h, m, l (four dwords each).
+__device__ __forceinline__ void split3(const float* v, uint4& h, uint4& m, uint4& l) {
+    uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        ph[i] = pack_hi16(a, b);
+        const float ra = a - trunc_bf16(a), rb = b - trunc_bf16(b);
+        pm[i] = pack_hi16(ra, rb);
+        pl[i] = pack_hi16(ra - trunc_bf16(ra), rb - trunc_bf16(rb));
+    }
+    h = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    m = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+    l = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+}
+
+// One output of the forward as the reference forms it: sum over k in
+// [k0, k1) of x[k] * (q[k][n] * s), in k order (the non-finite fallback).
+template <int BITS>
+__device__ float output_exact(const float* xrow, const uint4* W, const float* S, int mode, int Kpad, int RQ, int n,
+                              int k0, int k1) {
+    float acc = 0.0f;
+    for (int k = k0; k < k1; ++k) {
+        float q, s;
+        if constexpr (BITS == 8) {
+            q = (float)reinterpret_cast<const signed char*>(W)[((int64_t)(n >> 2) * RQ + (k >> 2)) * 16 + (n & 3) * 4 +
+                                                                (k & 3)];
+            s = mode ? S[0] : S[k];
+        } else {
+            const uint32_t d = reinterpret_cast<const uint32_t*>(W + (int64_t)(n >> 3) * RQ)[k];
+            q = (float)(((int)(d << (28 - 4 * (n & 7)))) >> 28);
+            s = S[(int64_t)((n >> 3) / mode) * Kpad + k];
+        }
+        acc = fmaf(xrow[k], q * s, acc);
+    }
+    return acc;
+}
+
+// NWN: wavefronts along N (2 or 4), each 64 columns: the tile is 128 x
+// 64 * NWN, with 128 * NWN threads.  The wider tile splits each x quad once
+// for twice the columns (half the split work per MFMA); INT4 keeps 128
+// columns, the width of one scale column at group 128.
+template <int NWN>
+constexpr int gemm3_threads() { return 128 * NWN; }
+
+template <int BITS, bool KALIGN4, bool PT, int NWN>
+__global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(
+    const float* __restrict__ x, int M, int K, int N, const uint4* __restrict__ W, const float* __restrict__ S,
+    int mode, int Kpad, int RQ, int NS, int KS, int sps, const float* __restrict__ bias, float* __restrict__ y,
+    float* __restrict__ part) {
+    // mode: INT8 -> per-tensor flag (also the template flag PT, so that no
+    // stage holds a branch); INT4 -> strips per scale column (a multiple of
+    // 16: one scale column per 128-column tile).  Workgroup b computes split
+    // b % KS (stages [kt0, kt1) of sps each) of tile b / KS.
+    constexpr int SW = (BITS == 4) ? 8 : 4;
+    constexpr int NT = gemm3_threads<NWN>();
+    constexpr int BN = 64 * NWN;
+    constexpr int EA = kBM * kB3KG / NT;  // A entries (row, k group) per thread: 2 or 1
+    constexpr int EB = BN * kB3KG / NT;   // B entries (column, k group) per thread: 2
+    static_assert(BITS == 8 || NWN == 2, "an INT4 tile spans one scale column");
+    __shared__ uint4 As[2][3][kB3KG][kBM];
+    __shared__ uint4 Bs[2][kB3KG][BN];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int ntn = (N + BN - 1) / BN;
+    const int tile = blockIdx.x / KS, split = blockIdx.x - tile * KS;
+    const int tm = tile / ntn, tn = tile - tm * ntn;
+    const int m0 = tm * kBM, n0 = tn * BN;
+    const int KT = (Kpad + kB3BK - 1) / kB3BK;
+    const int kt0 = split * sps, kt1 = (kt0 + sps) < KT ? (kt0 + sps) : KT;
+
+    // LDS access rule measured on gfx950: a 16-lane group of a 128-bit LDS
+    // access runs at full rate when it touches 16 consecutive 16-byte slots in
+    // lane order; other orders cost up to 8x.  So entry e of a stage (A: row,
+    // k group; B: column, k group) is row/column (e % 16) + 16 * (e / 64) of k
+    // group (e / 16) % 4, thread t takes entries t, t + NT, ..., and the MFMA
+    // operand reads are the same 16-slot runs.
+    const int akg = (tid >> 4) & 3, ar = (tid & 15) + 16 * (tid >> 6);
+    constexpr int kStep = NT / 4;  // rows or columns between a thread's entries
+    const int mrows = (M - m0) < kBM ? (M - m0) : kBM;
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
+    // Scale of column k of A (zero past K): per-channel scales[k], INT4 the
+    // tile's scale column devscales[sc][k].  Per-tensor: x itself goes into A
+    // (zero past K) and the epilogue multiplies by scales[0].
+    __amdgpu_buffer_rsrc_t rS;
+    if constexpr (BITS == 8)
+        rS = make_rsrc(S, PT ? 4u : (uint32_t)K * 4u);
+    else
+        rS = make_rsrc(S + (int64_t)((n0 / SW) / mode) * Kpad, (uint32_t)K * 4u);
+    // B side: an entry holds the eight k of its k group for one column, read
+    // from the two chunks (strip, row quads 2 * kg and 2 * kg + 1) that hold
+    // them: INT8 the column's dword of each chunk, INT4 the whole chunks (a
+    // nibble of every dword).  Strips past NS read as zero.
+    const int nstr = (NS - n0 / SW) < (BN / SW) ? (NS - n0 / SW) : (BN / SW);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
+
+    struct Regs {
+        float4 a[EA][2];                      // [entry][quad]
+        float4 s[2];                          // scales of the thread's eight k
+        uint4 b[EB][BITS == 8 ? 1 : 2];       // [entry]: INT8 {lo, hi} dwords in .x/.y, INT4 the two chunks
+    };
+    auto load = [&](Regs& rg, int kt) {
+        const int kb = kt * kB3BK + akg * 8;
+        const int soff = kt * kB3BK * 4;
+#pragma unroll
+        for (int h = 0; h < EA; ++h)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int vo = ((ar + kStep * h) * K + akg * 8 + 4 * q) * 4;
+                if (KALIGN4) {
+                    rg.a[h][q] = buf_load4f<true>(rX, kb + 4 * q < K ? vo : kOobOff, soff);
+                } else {
+                    float t[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        t[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rX, kb + 4 * q + r < K ? vo + 4 * r : kOobOff, soff, 0));
+                    rg.a[h][q] = make_float4(t[0], t[1], t[2], t[3]);
+                }
+            }
+        if constexpr (!PT) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) rg.s[q] = buf_load4f<KALIGN4>(rS, (akg * 8 + 4 * q) * 4, soff);
+        }
+        // RQ is a multiple of 4, so both row quads of the pair are in or out together.
+        const bool in = kt * kB3RQ + 2 * akg < RQ;
+        const int bsoff = kt * kB3RQ * 16;
+#pragma unroll
+        for (int c = 0; c < EB; ++c) {
+            const int n = ar + kStep * c;
+            const int vo = ((n / SW) * RQ + 2 * akg) * 16;
+            if constexpr (BITS == 8) {
+                const int vd = vo + (n & 3) * 4;
+                rg.b[c][0].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, bsoff, 0);
+                rg.b[c][0].y = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd + 16 : kOobOff, bsoff, 0);
+            } else {
+                rg.b[c][0] = buf_load16(rW, in ? vo : kOobOff, bsoff);
+                rg.b[c][1] = buf_load16(rW, in ? vo + 16 : kOobOff, bsoff);
+            }
+        }
+    };
+    auto store = [&](const Regs& rg, int buf) {
+#pragma unroll
+        for (int h = 0; h < EA; ++h) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[i] = PT ? f4get(rg.a[h][i >> 2], i & 3) : f4get(rg.a[h][i >> 2], i & 3) * f4get(rg.s[i >> 2], i & 3);
+            const int row = ar + kStep * h;
+            split3(v, As[buf][0][akg][row], As[buf][1][akg][row], As[buf][2][akg][row]);
+        }
+#pragma unroll
+        for (int c = 0; c < EB; ++c) {
+            float f[8];
+            if constexpr (BITS == 8) {
+                // bytes of the column's dword in each chunk: k = 0..3, then 4..7
+                const uint32_t lo = rg.b[c][0].x, hi = rg.b[c][0].y;
+                f[0] = cvt_sbyte<0>(lo), f[1] = cvt_sbyte<1>(lo), f[2] = cvt_sbyte<2>(lo), f[3] = cvt_sbyte<3>(lo);
+                f[4] = cvt_sbyte<0>(hi), f[5] = cvt_sbyte<1>(hi), f[6] = cvt_sbyte<2>(hi), f[7] = cvt_sbyte<3>(hi);
+            } else {
+                // dword r of a chunk is row r of it; nibble e the column
+                const int sh = 28 - 4 * ((ar + kStep * c) & 7);
+                const uint32_t dw[8] = {rg.b[c][0].x, rg.b[c][0].y, rg.b[c][0].z, rg.b[c][0].w,
+                                        rg.b[c][1].x, rg.b[c][1].y, rg.b[c][1].z, rg.b[c][1].w};
+#pragma unroll
+                for (int r = 0; r < 8; ++r) f[r] = (float)(((int)(dw[r] << sh)) >> 28);
+            }
+            Bs[buf][akg][ar + kStep * c] = make_uint4(pack_hi16(f[0], f[1]), pack_hi16(f[2], f[3]),
+                                                       pack_hi16(f[4], f[5]), pack_hi16(f[6], f[7]));
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int lr = lane & 15, lkg = lane >> 4;
+    auto stage = [&](int kt, const Regs& next, Regs& fill) {
+        const int buf = kt & 1;
+        load(fill, kt + 2);  // past the last stage these read zeros
+        uint4 bq[4], af[3][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bq[j] = Bs[buf][lkg][wn * 64 + j * 16 + lr];
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[p][i] = As[buf][p][lkg][wm * 64 + i * 16 + lr];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i == 2 && kt + 1 < kt1) store(next, buf ^ 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[p][i]),
+                                                                        __builtin_bit_cast(bf16x8, bq[j]), acc[i][j],
+                                                                        0, 0, 0);
+        }
+        lds_barrier();
+    };
+
+    Regs r0, r1;
+    load(r0, kt0);
+    if (kt0 + 1 < kt1) load(r1, kt0 + 1);
+    store(r0, kt0 & 1);
+    lds_barrier();
+    for (int kt = kt0; kt < kt1; kt += 2) {
+        stage(kt, r1, r0);
+        if (kt + 1 < kt1) stage(kt + 1, r0, r1);
+    }
+
+    // D layout of 16x16x32: lane l, element r -> row 4*(l/16) + r, column l%16.
+    const int klo = kt0 * kB3BK, khi = (kt1 * kB3BK) < K ? (kt1 * kB3BK) : K;
+    const float s_all = PT ? S[0] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + wn * 64 + j * 16 + lr;
+            if (n >= N) continue;
+            const float bv = (bias && KS == 1) ? bias[n] : 0.0f;
+            float* out = KS == 1 ? y : part + (int64_t)split * M * N;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 64 + i * 16 + lkg * 4 + r;
+                if (m < M) {
+                    float v = PT ? acc[i][j][r] * s_all : acc[i][j][r];
+                    if (!isfinite(v)) v = output_exact<BITS>(x + (int64_t)m * K, W, S, mode, Kpad, RQ, n, klo, khi);
+                    out[(int64_t)m * N + n] = (bias && KS == 1) ? v + bv : v;
+                }
+            }
+        }
+}
+
 // h[i] = silu(h[i]) * u[i]: the gated MLP's elementwise tail after two
 // separate projections (mul of equal shapes is one multiply, ops.cpp:239-253).
 __global__ __launch_bounds__(kThreads) void k_silu_mul(float* __restrict__ h, const float* __restrict__ u, int64_t n) {
@@ -927,13 +1199,16 @@ hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N) {
-    const int64_t tiles = ceil_div(M, kBM) * ceil_div(N, kBN);
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, int64_t bn) {
+    const int64_t tiles = ceil_div(M, kBM) * ceil_div(N, bn);
     const int64_t KT = ceil_div(round_up(K, kPadK), kBK);
     GemmPlan p{1, (int)KT};
+    // Workgroups resident per CU: two of the 128-wide kernels, one of the
+    // 256-wide (eight wavefronts, its LDS and registers fill the CU).
+    const int64_t per_cu = bn > kBN ? 1 : 2;
     if (tiles < kCus && KT >= 4) {
-        int64_t ks = ceil_div(2 * kCus, tiles);  // about two workgroups per CU
-        if (ks > KT / 2) ks = KT / 2;             // at least two stages per split
+        int64_t ks = ceil_div(per_cu * kCus, tiles);
+        if (ks > KT / 2) ks = KT / 2;  // at least two stages per split
         if (ks > kMaxSplits) ks = kMaxSplits;
         if (ks > 1) {
             p.sps = (int)ceil_div(KT, ks);
@@ -944,23 +1219,49 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N) {
 }
 
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    const GemmPlan p = gemm_plan(M, K, N);
-    return p.KS > 1 ? (int64_t)p.KS * M * N * 4 : 0;
+    // Either tile width may run (INT8 256, INT4 128): room for the larger plan.
+    const GemmPlan a = gemm_plan(M, K, N, kBN), b = gemm_plan(M, K, N, 2 * kBN);
+    const int64_t ks = a.KS > b.KS ? a.KS : b.KS;
+    return ks > 1 ? ks * M * N * 4 : 0;
 }
 
 namespace {
 template <int BITS>
 hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc, int mode,
                        int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, void* ws, hipStream_t s) {
-    const GemmPlan p = gemm_plan(M, K, N);
+    // The three-term bf16 kernel folds the scale into A, so a tile's columns
+    // must share their scale: always for INT8 (256-column tiles), for INT4
+    // when a scale column spans a multiple of 16 strips (group a multiple of
+    // 128; 128-column tiles).  Other INT4 groups take the fp32-MFMA kernel.
+    const bool three = BITS == 8 || mode % 16 == 0;
+    const int64_t bn = (BITS == 8) ? 2 * kBN : kBN;
+    const GemmPlan p = gemm_plan(M, K, N, bn);
     float* part = p.KS > 1 ? (float*)ws : nullptr;
-    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, kBN) * p.KS));
-    if (x_aligned4(x, K))
+    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, bn) * p.KS));
+    const bool k4 = x_aligned4(x, K);
+    const bool pt = BITS == 8 && mode;
+    constexpr int nwn = BITS == 8 ? 4 : 2;
+    constexpr int nt = gemm3_threads<nwn>();
+#define SGQ_GEMM3(A4, PT_)                                                                              \
+    k_gemm3<BITS, A4, (PT_) && BITS == 8, nwn><<<grid, nt, 0, s>>>(x, (int)M, (int)K, (int)N,           \
+                                                                   (const uint4*)packed, sc, mode,       \
+                                                                   (int)Kpad, (int)RQ, (int)NS, p.KS,   \
+                                                                   p.sps, bias, y, part)
+    if (three && k4 && pt)
+        SGQ_GEMM3(true, true);
+    else if (three && k4)
+        SGQ_GEMM3(true, false);
+    else if (three && pt)
+        SGQ_GEMM3(false, true);
+    else if (three)
+        SGQ_GEMM3(false, false);
+    else if (k4)
         k_gemm<BITS, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
                                                      (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
     else
         k_gemm<BITS, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
                                                       (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
+#undef SGQ_GEMM3
     if (p.KS > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
