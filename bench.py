@@ -10,7 +10,8 @@ back to back as one captured hipGraph over `--copies` rotating weight copies
 `value` is algorithmic bytes per call * K / time (GB/s).
 
 The same line carries the M=2048 INT8 per-tensor GEMM (config 4) under
-"secondary" (TFLOP/s against the fp32 MFMA peak) and the reference's CPU path
+"secondary" (TFLOP/s against the roof of its three-term bf16 MFMA form, a third
+of the bf16 peak; the fraction of the fp32 MFMA peak rides along) and the reference's CPU path
 (compiled from its own sources into oracle/_ref, or the C port when that is
 absent) timed on this host under "cpu_baseline".
 """
@@ -33,6 +34,11 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, TFLOP/s
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, TFLOP/s
+# The prefill GEMM (M > 16) computes each fp32 product as three exact bf16
+# products on the bf16 matrix cores, so its roof is a third of the bf16 peak
+# in fp32 flops.
+GEMM3_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 METRIC = "QuantizedLinear GB/s at M=1 (% HBM peak); TFLOP/s at M=2048 (% MFMA)"
 
 # Shapes of BASELINE.json's configs.  scheme: 0 per-tensor, 1 per-channel.
@@ -599,8 +605,10 @@ def main() -> int:
         {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config)}
         if hbm_bound else
-        {"bound": "mfma", "achieved": round(tfl, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-         "frac": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+        {"bound": "mfma", "achieved": round(tfl, 3), "peak": round(GEMM3_PEAK_TFLOPS, 1), "unit": "TFLOP/s",
+         "frac": round(tfl / GEMM3_PEAK_TFLOPS, 4), "traffic": None,
+         "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
+         "frac_of_fp32_mfma_peak": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4)}
     )
     out = {
         "metric": METRIC,
@@ -629,18 +637,30 @@ def main() -> int:
     if not args.no_secondary and args.config == "c2":
         c4 = CONFIGS["c4"]
         case4 = Case(pkg, c4, dev, 1)
-        ms4 = case4.time_eager(max(3, min(20, args.steps // 100)), 2)
+        # A graph of back-to-back calls after a warm-up, replayed five times:
+        # the median per-call time (single short eager bursts ran before the
+        # clocks had settled and read up to 25% slow).
+        n4 = max(5, min(50, args.steps // 40))
+        first4 = case4.time_graph(n4, 10, extra_replays=4)
+        reps4 = sorted([first4] + case4.replay_ms)
+        ms4 = statistics.median(reps4)
         err4 = case4.check(Oracle(), rows=np.r_[0:8, 2040:2048])
         tfl4 = alg_flops(c4) / (ms4 * 1e-3) / 1e12
         log(f"[bench] c4: {ms4:.3f} ms/step, {tfl4:.2f} TFLOP/s, rel_err {err4:.2e}")
         if err4 > 1e-5:
             raise SystemExit(f"parity failure in bench (c4): rel err {err4}")
         out["secondary"] = {
-            "metric": "QuantizedLinear TFLOP/s at M=2048 (INT8 per-tensor 4096x4096, fp32 MFMA)",
+            "metric": "QuantizedLinear TFLOP/s at M=2048 (INT8 per-tensor 4096x4096; fp32 products as three exact "
+                      "bf16 products on the bf16 MFMA)",
             "value": round(tfl4, 3), "unit": "TFLOP/s", "ms_per_step": round(ms4, 4),
+            "launch": f"one hipGraph of {n4} back-to-back calls, median of 5 replays",
+            "ms_per_step_over_replays": {"min": round(reps4[0], 4), "median": round(ms4, 4),
+                                         "max": round(reps4[-1], 4)},
             "workload": c4["name"], "rel_err_vs_oracle": err4,
-            "roofline": {"bound": "mfma", "achieved": round(tfl4, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tfl4 / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+            "roofline": {"bound": "mfma", "achieved": round(tfl4, 3), "peak": round(GEMM3_PEAK_TFLOPS, 1),
+                         "unit": "TFLOP/s", "frac": round(tfl4 / GEMM3_PEAK_TFLOPS, 4), "traffic": None,
+                         "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
+                         "frac_of_fp32_mfma_peak": round(tfl4 / FP32_MFMA_PEAK_TFLOPS, 4)},
         }
         del case4
         torch.cuda.empty_cache()

@@ -171,9 +171,11 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  * and with it nn::QuantizedLinear::forward (include/sovereigngrad/nn.hpp:956-958):
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
- * Dispatch: M <= 16 runs the wavefront GEMV, larger M the LDS-staged
- * fp32-MFMA GEMM.  workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes,
- * else SGQ_ERR_WORKSPACE. */
+ * Dispatch: M <= 16 runs the wavefront GEMV, larger M the LDS-staged MFMA
+ * GEMM, whose fp32 products run on the bf16 matrix cores as three exact bf16
+ * products each (fp32 accumulation; as accurate as an fp32 product).
+ * workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes, else
+ * SGQ_ERR_WORKSPACE. */
 int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     int scheme, const float* bias, float* y, void* workspace, int64_t workspace_bytes,
                     void* stream);

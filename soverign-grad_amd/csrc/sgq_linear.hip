@@ -14,9 +14,12 @@
 // of a strip are combined by a butterfly that halves the values each lane
 // carries at every step, the four wavefronts through LDS.
 //
-// Prefill path (M > 16): 128x128 output tiles, K staged through LDS 16 rows at
-// a time; codes are dequantized on the way into LDS (code * scale, the
-// reference's own product) and fed to v_mfma_f32_16x16x4_f32.
+// Prefill path (M > 16): output tiles of 128 rows, K staged through LDS 32
+// rows at a time.  k_gemm3 runs the fp32 products on the bf16 matrix cores as
+// three exact bf16 products each (x * s split into three bf16 terms, codes
+// exact in bf16, fp32 accumulation); k_gemm (INT4 groups that are not a
+// multiple of 128) dequantizes codes on the way into LDS (code * scale, the
+// reference's own product) and feeds v_mfma_f32_16x16x4_f32.
 #include "sgq_internal.h"
 #include "sgq_lanes.h"
 

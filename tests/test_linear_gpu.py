@@ -292,6 +292,63 @@ def test_infinite_activation_matches_reference(sgq, dev, oracle, synth, M):
     _same_nonfinite(y, yref)
 
 
+@pytest.mark.parametrize("bits_,scheme,M", [(8, 0, 40), (8, 1, 40), (4, 0, 40), (8, 0, 300), (4, 0, 150)])
+def test_infinite_activation_gemm(sgq, dev, oracle, synth, bits_, scheme, M):
+    # The prefill GEMM splits x * s into three bf16 terms, which turns an
+    # infinite activation into inf - inf; such outputs must take the exact
+    # k-order fallback (per K split when the grid splits K: M = 40 and 150
+    # run split-K at this width) and land as the reference's x . (q * s).
+    K, N, G = 1024, 512, 128
+    W = synth.normal((K, N), 93, 0, 0.0, 0.02)
+    x = synth.normal((M, K), 93, 1)
+    x[0, 17] = np.inf
+    x[M - 1, 600] = -np.inf
+    x[1, 3] = np.inf
+    x[1, 900] = -np.inf
+    x[M // 2, 5] = np.nan
+    if bits_ == 8:
+        q, s = oracle.quantize_int8(W, scheme)
+        qw = sgq.quantize_int8(_to_dev(W, dev), scheme)
+        yref = oracle.quantized_matmul_int8(x, q, s, scheme)
+    else:
+        q, s = oracle.quantize_int4(W, G)
+        qw = sgq.quantize_int4(_to_dev(W, dev), G)
+        yref = oracle.quantized_matmul_int4(x, q, s, G)
+    y = _np(sgq.quantized_matmul(_to_dev(x, dev), qw))
+    assert np.isinf(yref).any() and np.isnan(yref).any()
+    _same_nonfinite(y, yref)
+
+
+@pytest.mark.parametrize("bits_,scheme,G", [(8, 0, 0), (8, 1, 0), (4, 0, 128)])
+def test_gemm_accuracy_vs_fp64(sgq, dev, oracle, synth, bits_, scheme, G):
+    # The prefill GEMM runs the fp32 products on bf16 matrix cores as three
+    # exact terms (x * s = h + m + l, codes exact, products exact, fp32
+    # sums).  Against an fp64 product with the reference's fp32 weights
+    # (q * s), it must be at least as accurate as the reference's own fp32
+    # dequantize-then-matmul (the oracle), not merely within the 1e-5 bar.
+    M, K, N = 256, 4096, 512
+    W = synth.normal((K, N), 95, 0, 0.0, 0.02)
+    x = synth.normal((M, K), 95, 1)
+    if bits_ == 8:
+        q, s = oracle.quantize_int8(W, scheme)
+        qw = sgq.quantize_int8(_to_dev(W, dev), scheme)
+        yref = oracle.quantized_matmul_int8(x, q, s, scheme)
+        w32 = oracle.dequantize_int8(q, s, scheme)
+    else:
+        q, s = oracle.quantize_int4(W, G)
+        qw = sgq.quantize_int4(_to_dev(W, dev), G)
+        yref = oracle.quantized_matmul_int4(x, q, s, G)
+        w32 = oracle.dequantize_int4(q, s, G)
+    y = _np(sgq.quantized_matmul(_to_dev(x, dev), qw))
+    y64 = x.astype(np.float64) @ np.asarray(w32, np.float64).reshape(K, N)
+    scale = np.max(np.abs(y64))
+    e_gpu = np.max(np.abs(y - y64)) / scale
+    e_ref = np.max(np.abs(yref - y64)) / scale
+    print(f"    max rel err vs fp64: gpu {e_gpu:.3e}, reference fp32 path {e_ref:.3e}", flush=True)
+    assert e_gpu <= TOL
+    assert e_gpu <= 2.0 * e_ref
+
+
 def test_dequantize_matches_reference_product(sgq, dev, oracle, synth):
     W = synth.normal((130, 72), 51, 0, 0.0, 0.02)
     qx = sgq.quantize_int8(_to_dev(W, dev), 1)
