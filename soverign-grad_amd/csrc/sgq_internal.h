@@ -135,8 +135,12 @@ hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N,
 struct GemmPlan {
     int KS, sps;  // splits of K, 32-row stages per split
 };
+struct GemmTile {
+    int64_t bm, bn, per_cu;  // tile rows and columns, workgroups resident per CU
+};
 constexpr int64_t kCus = 256;  // MI355X compute units
-GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, int64_t bn);  // bn: tile width
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t);
+GemmTile gemm_tile(int bits);
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, void* ws, hipStream_t s);

@@ -20,6 +20,8 @@
 // exact in bf16, fp32 accumulation); k_gemm (INT4 groups that are not a
 // multiple of 128) dequantizes codes on the way into LDS (code * scale, the
 // reference's own product) and feeds v_mfma_f32_16x16x4_f32.
+#include <type_traits>
+
 #include "sgq_internal.h"
 #include "sgq_lanes.h"
 
@@ -754,15 +756,23 @@ __device__ float output_exact(const float* xrow, const uint4* W, const float* S,
     return acc;
 }
 
-// NWN: wavefronts along N (2 or 4), each 64 columns: the tile is 128 x
-// 64 * NWN, with 128 * NWN threads.  The wider tile splits each x quad once
-// for twice the columns (half the split work per MFMA); INT4 keeps 128
-// columns, the width of one scale column at group 128.
-template <int NWN>
-constexpr int gemm3_threads() { return 128 * NWN; }
+// Tile shape: WM x WN wavefronts, each RB x CB blocks of 16x16 outputs, so
+// the tile is BM = 16 * RB * WM rows by BN = 16 * CB * WN columns.  A wider
+// tile splits each x value once for more columns (less split work per
+// MFMA); INT4 tiles are 128 columns, the width of one scale column at group
+// 128.
+template <int WM_, int RB_, int WN_, int CB_>
+struct G3Shape {
+    static constexpr int WM = WM_, RB = RB_, WN = WN_, CB = CB_;
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int BM = 16 * RB * WM, BN = 16 * CB * WN;
+    static constexpr int WPE = RB * CB >= 16 ? 2 : 1;  // minimum waves per SIMD the register budget keeps
+};
+using G3Wide = G3Shape<2, 4, 4, 4>;  // 128 x 256, 8 wavefronts: INT8
+using G3Tile = G3Shape<2, 4, 2, 4>;  // 128 x 128, 4 wavefronts: INT4
 
-template <int BITS, bool KALIGN4, bool PT, int NWN>
-__global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm3(
+template <int BITS, bool KALIGN4, bool PT, class SH>
+__global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(
     const float* __restrict__ x, int M, int K, int N, const uint4* __restrict__ W, const float* __restrict__ S,
     int mode, int Kpad, int RQ, int NS, int KS, int sps, const float* __restrict__ bias, float* __restrict__ y,
     float* __restrict__ part) {
@@ -771,19 +781,19 @@ __global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_p
     // 16: one scale column per 128-column tile).  Workgroup b computes split
     // b % KS (stages [kt0, kt1) of sps each) of tile b / KS.
     constexpr int SW = (BITS == 4) ? 8 : 4;
-    constexpr int NT = gemm3_threads<NWN>();
-    constexpr int BN = 64 * NWN;
-    constexpr int EA = kBM * kB3KG / NT;  // A entries (row, k group) per thread: 2 or 1
-    constexpr int EB = BN * kB3KG / NT;   // B entries (column, k group) per thread: 2
-    static_assert(BITS == 8 || NWN == 2, "an INT4 tile spans one scale column");
-    __shared__ uint4 As[2][3][kB3KG][kBM];
+    constexpr int NT = SH::NT, BM = SH::BM, BN = SH::BN, RB = SH::RB, CB = SH::CB;
+    constexpr int EA = BM * kB3KG / NT;  // A entries (row, k group) per thread
+    constexpr int EB = BN * kB3KG / NT;  // B entries (column, k group) per thread
+    static_assert(BM * kB3KG % NT == 0 && EA >= 1 && BN * kB3KG % NT == 0 && EB >= 1, "entries spread evenly");
+    static_assert(BITS == 8 || BN == 128, "an INT4 tile spans one scale column");
+    __shared__ uint4 As[2][3][kB3KG][BM];
     __shared__ uint4 Bs[2][kB3KG][BN];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % SH::WM, wn = wave / SH::WM;
     const int ntn = (N + BN - 1) / BN;
     const int tile = blockIdx.x / KS, split = blockIdx.x - tile * KS;
     const int tm = tile / ntn, tn = tile - tm * ntn;
-    const int m0 = tm * kBM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * BN;
     const int KT = (Kpad + kB3BK - 1) / kB3BK;
     const int kt0 = split * sps, kt1 = (kt0 + sps) < KT ? (kt0 + sps) : KT;
 
@@ -795,7 +805,7 @@ __global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_p
     // operand reads are the same 16-slot runs.
     const int akg = (tid >> 4) & 3, ar = (tid & 15) + 16 * (tid >> 6);
     constexpr int kStep = NT / 4;  // rows or columns between a thread's entries
-    const int mrows = (M - m0) < kBM ? (M - m0) : kBM;
+    const int mrows = (M - m0) < BM ? (M - m0) : BM;
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
     // Scale of column k of A (zero past K): per-channel scales[k], INT4 the
     // tile's scale column devscales[sc][k].  Per-tensor: x itself goes into A
@@ -888,28 +898,28 @@ __global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_p
         }
     };
 
-    floatx4 acc[4][4];
+    floatx4 acc[RB][CB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int lr = lane & 15, lkg = lane >> 4;
     auto stage = [&](int kt, const Regs& next, Regs& fill) {
         const int buf = kt & 1;
         load(fill, kt + 2);  // past the last stage these read zeros
-        uint4 bq[4], af[3][4];
+        uint4 bq[CB], af[3][RB];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bq[j] = Bs[buf][lkg][wn * 64 + j * 16 + lr];
+        for (int j = 0; j < CB; ++j) bq[j] = Bs[buf][lkg][wn * 16 * CB + j * 16 + lr];
 #pragma unroll
         for (int p = 0; p < 3; ++p)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) af[p][i] = As[buf][p][lkg][wm * 64 + i * 16 + lr];
+            for (int i = 0; i < RB; ++i) af[p][i] = As[buf][p][lkg][wm * 16 * RB + i * 16 + lr];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (i == 2 && kt + 1 < kt1) store(next, buf ^ 1);
+        for (int i = 0; i < RB; ++i) {
+            if (i == RB / 2 && kt + 1 < kt1) store(next, buf ^ 1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < CB; ++j)
 #pragma unroll
                 for (int p = 0; p < 3; ++p)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[p][i]),
@@ -933,16 +943,16 @@ __global__ __launch_bounds__(gemm3_threads<NWN>()) __attribute__((amdgpu_waves_p
     const int klo = kt0 * kB3BK, khi = (kt1 * kB3BK) < K ? (kt1 * kB3BK) : K;
     const float s_all = PT ? S[0] : 1.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + wn * 64 + j * 16 + lr;
+        for (int j = 0; j < CB; ++j) {
+            const int n = n0 + wn * 16 * CB + j * 16 + lr;
             if (n >= N) continue;
             const float bv = (bias && KS == 1) ? bias[n] : 0.0f;
             float* out = KS == 1 ? y : part + (int64_t)split * M * N;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * 64 + i * 16 + lkg * 4 + r;
+                const int m = m0 + wm * 16 * RB + i * 16 + lkg * 4 + r;
                 if (m < M) {
                     float v = PT ? acc[i][j][r] * s_all : acc[i][j][r];
                     if (!isfinite(v)) v = output_exact<BITS>(x + (int64_t)m * K, W, S, mode, Kpad, RQ, n, klo, khi);
@@ -1202,16 +1212,13 @@ hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, int64_t bn) {
-    const int64_t tiles = ceil_div(M, kBM) * ceil_div(N, bn);
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t) {
+    const int64_t tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
     const int64_t KT = ceil_div(round_up(K, kPadK), kBK);
     GemmPlan p{1, (int)KT};
-    // Workgroups resident per CU: two of the 128-wide kernels, one of the
-    // 256-wide (eight wavefronts, its LDS and registers fill the CU).
-    const int64_t per_cu = bn > kBN ? 1 : 2;
-    if (tiles < kCus && KT >= 4) {
-        int64_t ks = ceil_div(per_cu * kCus, tiles);
-        if (ks > KT / 2) ks = KT / 2;  // at least two stages per split
+    if (tiles < t.per_cu * kCus && KT >= 4) {
+        int64_t ks = ceil_div(t.per_cu * kCus, tiles);  // about per_cu workgroups per CU
+        if (ks > KT / 2) ks = KT / 2;                     // at least two stages per split
         if (ks > kMaxSplits) ks = kMaxSplits;
         if (ks > 1) {
             p.sps = (int)ceil_div(KT, ks);
@@ -1221,10 +1228,18 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, int64_t bn) {
     return p;
 }
 
+// Tile of the three-term GEMM for a code width (the fp32 kernel uses the
+// 128 x 128 tile), with the workgroups a CU holds at once: two of the
+// 128-wide tiles, one of the 256-wide (its LDS and registers fill the CU).
+GemmTile gemm_tile(int bits) { return bits == 8 ? GemmTile{kBM, 2 * kBN, 1} : GemmTile{kBM, kBN, 2}; }
+
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    // Either tile width may run (INT8 256, INT4 128): room for the larger plan.
-    const GemmPlan a = gemm_plan(M, K, N, kBN), b = gemm_plan(M, K, N, 2 * kBN);
-    const int64_t ks = a.KS > b.KS ? a.KS : b.KS;
+    // Either code width (and the fp32 kernel's 128 x 128 tile): room for the largest plan.
+    int64_t ks = gemm_plan(M, K, N, GemmTile{kBM, kBN, 2}).KS;
+    for (int bits : {4, 8}) {
+        const int64_t k = gemm_plan(M, K, N, gemm_tile(bits)).KS;
+        if (k > ks) ks = k;
+    }
     return ks > 1 ? ks * M * N * 4 : 0;
 }
 
@@ -1237,33 +1252,35 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
     // when a scale column spans a multiple of 16 strips (group a multiple of
     // 128; 128-column tiles).  Other INT4 groups take the fp32-MFMA kernel.
     const bool three = BITS == 8 || mode % 16 == 0;
-    const int64_t bn = (BITS == 8) ? 2 * kBN : kBN;
-    const GemmPlan p = gemm_plan(M, K, N, bn);
+    const GemmTile t = three ? gemm_tile(BITS) : GemmTile{kBM, kBN, 2};
+    const GemmPlan p = gemm_plan(M, K, N, t);
     float* part = p.KS > 1 ? (float*)ws : nullptr;
-    const dim3 grid((unsigned)(ceil_div(M, kBM) * ceil_div(N, bn) * p.KS));
+    const dim3 grid((unsigned)(ceil_div(M, t.bm) * ceil_div(N, t.bn) * p.KS));
     const bool k4 = x_aligned4(x, K);
     const bool pt = BITS == 8 && mode;
-    constexpr int nwn = BITS == 8 ? 4 : 2;
-    constexpr int nt = gemm3_threads<nwn>();
-#define SGQ_GEMM3(A4, PT_)                                                                              \
-    k_gemm3<BITS, A4, (PT_) && BITS == 8, nwn><<<grid, nt, 0, s>>>(x, (int)M, (int)K, (int)N,           \
-                                                                   (const uint4*)packed, sc, mode,       \
-                                                                   (int)Kpad, (int)RQ, (int)NS, p.KS,   \
-                                                                   p.sps, bias, y, part)
-    if (three && k4 && pt)
-        SGQ_GEMM3(true, true);
-    else if (three && k4)
-        SGQ_GEMM3(true, false);
-    else if (three && pt)
-        SGQ_GEMM3(false, true);
-    else if (three)
-        SGQ_GEMM3(false, false);
-    else if (k4)
+    using Big = typename std::conditional<BITS == 8, G3Wide, G3Tile>::type;
+#define SGQ_GEMM3(SH, A4, PT_)                                                                                 \
+    k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(x, (int)M, (int)K, (int)N,              \
+                                                                    (const uint4*)packed, sc, mode, (int)Kpad, \
+                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part)
+#define SGQ_GEMM3_SHAPE(SH)               \
+    if (k4 && pt)                         \
+        SGQ_GEMM3(SH, true, true);        \
+    else if (k4)                          \
+        SGQ_GEMM3(SH, true, false);       \
+    else if (pt)                          \
+        SGQ_GEMM3(SH, false, true);       \
+    else                                  \
+        SGQ_GEMM3(SH, false, false);
+    if (three) {
+        SGQ_GEMM3_SHAPE(Big)
+    } else if (k4)
         k_gemm<BITS, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
                                                      (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
     else
         k_gemm<BITS, false><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,
                                                       (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, y, part);
+#undef SGQ_GEMM3_SHAPE
 #undef SGQ_GEMM3
     if (p.KS > 1) {
         const hipError_t e = hipGetLastError();
