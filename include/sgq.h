@@ -87,8 +87,10 @@ int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size);
 int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size);
 
 /* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
- * Nonzero only for the GEMM (M > 16) when its grid of 128x128 output tiles
- * is smaller than the GPU: K is then split over workgroups, whose partial
+ * Nonzero only for the GEMM (M > 16, except batches of up to 128 rows with
+ * M * K * N <= 2^29, which run the GEMV) when its grid of output tiles (128
+ * rows by 256 columns for INT8, 128 for INT4) is smaller than the GPU: K is
+ * then split over workgroups, whose partial
  * tiles (KS * M * N floats) are summed by a second kernel in fixed order.
  * 0 otherwise (the GEMV and large GEMMs own whole outputs per workgroup), and
  * the workspace arguments may then be NULL/0.  The contents need no
@@ -171,7 +173,8 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  * and with it nn::QuantizedLinear::forward (include/sovereigngrad/nn.hpp:956-958):
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
- * Dispatch: M <= 16 runs the wavefront GEMV, larger M the LDS-staged MFMA
+ * Dispatch: M <= 16 runs the wavefront GEMV (row groups of 8), as do up to
+ * 128 rows when M * K * N <= 2^29; larger batches the LDS-staged MFMA
  * GEMM, whose fp32 products run on the bf16 matrix cores as three exact bf16
  * products each (fp32 accumulation; as accurate as an fp32 product).
  * workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes, else
@@ -196,8 +199,8 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
  *   h[M,N] = silu(x . Wg + bias_gate) * (x . Wu + bias_up)
  * silu(v) = v / (1 + exp(-v)) as Tensor::silu (src/ops.cpp:561-575,
  * include/sovereigngrad/simd.hpp:103-108), * as mul (src/ops.cpp:239-253).
- * The two weights share K, N, scheme / group_size.  M <= 16 with the tiled
- * layout runs both GEMVs in one launch (x read once per strip pair, no
+ * The two weights share K, N, scheme / group_size.  The batches the forward
+ * runs on the GEMV (above), with the tiled layout, run both GEMVs in one launch (x read once per strip pair, no
  * intermediate in HBM); otherwise two projections (GEMM or flat INT4) and an
  * elementwise kernel.  Biases may be NULL.  workspace:
  * sgq_swiglu_workspace_bytes(bits, M, K, N, group_size) bytes (group_size is

@@ -61,7 +61,7 @@ int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 
 // Only the GEMM uses a workspace, for split-K partial tiles when its tile
 // grid is smaller than the GPU (see gemm_plan); the GEMV owns whole columns.
 int64_t linear_ws_bytes(int, int64_t M, int64_t K, int64_t N) {
-    return M > kGemvMaxM ? gemm_workspace_bytes(M, K, N) : 0;
+    return linear_uses_gemv(M, K, N) ? 0 : gemm_workspace_bytes(M, K, N);
 }
 
 int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void* workspace, int64_t workspace_bytes) {
@@ -77,8 +77,9 @@ int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void*
 // [up projection: M*N floats, 256-byte aligned][split-K partials of either GEMM].
 // The flat INT4 layout always takes the two-projection form.
 int64_t swiglu_ws_bytes(bool flat, int64_t M, int64_t K, int64_t N) {
-    if (!flat && M <= kGemvMaxM && K > 0) return 0;
-    const int64_t split = (!flat && M > kGemvMaxM) ? gemm_workspace_bytes(M, K, N) : 0;
+    // The one-launch GEMV form takes the batches the plain forward runs on the GEMV.
+    if (!flat && linear_uses_gemv(M, K, N) && K > 0) return 0;
+    const int64_t split = (!flat && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
     return align_up(M * N * 4) + split;
 }
 
@@ -378,7 +379,7 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
     if (!aligned16(packed) || (!per_tensor && !aligned16(scales)))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: packed and per-channel scales must be 16-byte aligned");
-    if (M <= kGemvMaxM) {
+    if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
         const int st = check_linear_ws("sgq_linear_int8", M, K, N, workspace, workspace_bytes);
@@ -410,7 +411,7 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
     if (!aligned16(packed) || !aligned16(devscales))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: packed and devscales must be 16-byte aligned");
-    if (M <= kGemvMaxM) {
+    if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
         const int st = check_linear_ws("sgq_linear_int4", M, K, N, workspace, workspace_bytes);
@@ -447,7 +448,7 @@ int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (!aligned16(packed_gate) || !aligned16(packed_up) ||
         (!per_tensor && (!aligned16(scales_gate) || !aligned16(scales_up))))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and per-channel scales must be 16-byte aligned", fn);
-    if (M <= kGemvMaxM) {
+    if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i8(x, M, K, N, packed_gate, scales_gate, bias_gate, packed_up, scales_up, bias_up,
                                       per_tensor, h, s),
                 "swiglu_gemv_i8");
@@ -492,7 +493,7 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: tiled layout needs devscales", fn);
     if (!aligned16(packed_gate) || !aligned16(packed_up) || !aligned16(devscales_gate) || !aligned16(devscales_up))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
-    if (M <= kGemvMaxM) {
+    if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i4(x, M, K, N, packed_gate, devscales_gate, bias_gate, packed_up, devscales_up,
                                       bias_up, g, h, s),
                 "swiglu_gemv_i4");

@@ -80,7 +80,17 @@ struct I4Geom {
     int64_t devscale_count() const { return tiled ? nsc * Kpad : 0; }
 };
 
-constexpr int kGemvMaxM = 16;  // M <= this runs the GEMV, larger M the MFMA GEMM
+constexpr int kGemvMaxM = 16;  // M <= this runs the GEMV, larger M the MFMA GEMM (but see below)
+// The plain forward also runs the GEMV for batches of up to this many rows
+// (row groups of 8, one workgroup each) when the work is small: the GEMV's
+// time grows with M * K * N at the VALU rate from a fixed ~3 us, the GEMM's
+// from ~15 us of pipeline fill, split-K partials and reduce (measured on
+// MI355X: 128 x 1024 x 1024 INT8 took 20 us on the GEMM).
+constexpr int64_t kGemvRowsMax = 128;
+constexpr int64_t kGemvSmallWork = (int64_t)1 << 29;  // M * K * N
+inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
+    return M <= kGemvMaxM || (M <= kGemvRowsMax && M * K * N <= kGemvSmallWork);
+}
 
 // ---- launchers (return hipError_t of the launch) ----------------------
 hipError_t launch_fill_zero(void* p, int64_t bytes, hipStream_t s);

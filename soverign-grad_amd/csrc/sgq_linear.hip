@@ -162,7 +162,8 @@ struct GemvArgs {
     int ldy;                 // row stride of y and res
     const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
     float eps;
-    int P;                   // row groups: M rows split into P = 1 or 2 groups of MT (one workgroup each)
+    int P, Pshift;           // row groups: M rows in P = 2^Pshift groups of MT (one workgroup each;
+                             // groups past M return at once)
     FastDiv spc;             // INT4: division by mode (strips per scale column)
     int nblk;                // grid x (passed here: reading the hidden gridDim argument cost a second
                              // dependent round of kernel-argument loads ahead of the first data load)
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // Strips of a scale column share an XCD's L2.  Workgroups of one weight
     // cover (NS + SPW - 1) / SPW strip groups (x of the grid); with several
     // weights side by side (NG == 1), y of the grid selects the weight.
-    // Workgroup v covers row group p = v % P of strip group v / P (P is 1 or 2):
+    // Workgroup v covers row group p = v % P of strip group v / P (P a power of two):
     // the row groups of one strip are neighbours in v, so they run on one XCD
     // and the second read of the strip's codes hits its L2.  No integer
     // division on the way to the first load: every index here is a shift, a
@@ -226,10 +227,11 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // instructions, all of them ahead of the loads).
     const int vg = xcd_swizzle(blockIdx.x, a.nblk);
     const int prow = vg & (a.P - 1);
-    const int jg = vg >> (a.P - 1);
+    const int jg = vg >> a.Pshift;
     const int m0 = prow * MT;
-    const float* __restrict__ x = a.x + (int64_t)m0 * K;
     const int M = min(MT, a.M - m0);
+    if (M <= 0) return;  // a row group past M (P rounded up to a power of two); before any barrier
+    const float* __restrict__ x = a.x + (int64_t)m0 * K;
     const int wt = NG == 1 ? (int)blockIdx.y : 0;
     const int j0 = SPW * jg;
     const int widx = NG == 1 ? wt : grp;
@@ -1103,23 +1105,18 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
 template <int BITS, int NG>
 hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.M = (int)M;
-    constexpr int kRowsMax = 8;  // kGemvMaxM = 16 rows make at most two row groups
+    constexpr int kRowsMax = 8;  // rows per workgroup beyond four
     // All rows in one launch: M <= 4 as one row group, larger M in row groups
-    // of kRowsMax (each a workgroup of its own over the same strip).
-    if (M <= 1) {
-        a.P = 1;
-        return gemv_launch<BITS, 1, NG>(a, nw, s);
-    }
-    if (M <= 2) {
-        a.P = 1;
-        return gemv_launch<BITS, 2, NG>(a, nw, s);
-    }
-    if (M <= 4) {
-        a.P = 1;
-        return gemv_launch<BITS, 4, NG>(a, nw, s);
-    }
-    a.P = (int)((M + kRowsMax - 1) / kRowsMax);
-    if (a.P > 2) return hipErrorInvalidValue;  // the kernel's row-group index takes P = 1 or 2
+    // of kRowsMax (each a workgroup of its own over the same strip), their
+    // count rounded up to a power of two for the index arithmetic.
+    a.P = 1;
+    a.Pshift = 0;
+    if (M <= 1) return gemv_launch<BITS, 1, NG>(a, nw, s);
+    if (M <= 2) return gemv_launch<BITS, 2, NG>(a, nw, s);
+    if (M <= 4) return gemv_launch<BITS, 4, NG>(a, nw, s);
+    const int64_t groups = (M + kRowsMax - 1) / kRowsMax;
+    while (a.P < groups) a.P *= 2, ++a.Pshift;
+    if (a.P * kRowsMax > kGemvRowsMax) return hipErrorInvalidValue;
     return gemv_launch<BITS, kRowsMax, NG>(a, nw, s);
 }
 
@@ -1127,6 +1124,7 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
                    int64_t ldy, const float* res) {
     GemvArgs a{};
     a.P = 1;
+    a.Pshift = 0;
     a.x = x;
     a.K = (int)K;
     a.N = (int)N;

@@ -49,13 +49,15 @@ def test_int4_sizes(lib, K, N, G):
 
 
 def test_workspace_sizes(lib):
-    # The GEMV (M <= 16) and GEMMs with at least one 128x128 tile per CU need no
-    # workspace; smaller GEMM grids split K and keep KS * M * N fp32 partials.
+    # The GEMV (M <= 16, or up to 128 rows of small work) and GEMMs with at
+    # least one tile per CU need no workspace; smaller GEMM grids split K and
+    # keep KS * M * N fp32 partials.
     assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(4, 16, 4096, 4096) == 0
-    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0  # 512 tiles
-    ws = lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)  # 8 tiles: split K
-    assert ws > 0 and ws % (128 * 1024 * 4) == 0 and 2 <= ws // (128 * 1024 * 4) <= 16
+    assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0  # GEMV: 2^27 multiply-adds
+    assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0  # 256 or 512 tiles
+    ws = lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)  # GEMM of 8 or 16 tiles: split K
+    assert ws > 0 and ws % (256 * 1024 * 4) == 0 and 2 <= ws // (256 * 1024 * 4) <= 16
     assert lib.sgq_linear_workspace_bytes(4, 64, 96, 512) == 0  # three 32-row stages: too short to split
     assert lib.sgq_linear_workspace_bytes(3, 1, 4, 4) == -1
     assert lib.sgq_quantize_workspace_bytes(4, 4096, 4096, 128) >= 4096 * 4096 // 128 * 4
@@ -70,9 +72,10 @@ def test_swiglu_workspace_sizes(lib):
     # (M*N floats, 256-byte aligned) followed by the GEMM's split-K partials.
     assert lib.sgq_swiglu_workspace_bytes(4, 1, 4096, 11008, 128) == 0
     assert lib.sgq_swiglu_workspace_bytes(8, 16, 1024, 1024, 0) == 0
+    assert lib.sgq_swiglu_workspace_bytes(8, 128, 1024, 1024, 0) == 0  # GEMV form, as the plain forward
     assert lib.sgq_swiglu_workspace_bytes(4, 2048, 4096, 4096, 128) == 2048 * 4096 * 4
-    u = 128 * 1024 * 4
-    assert lib.sgq_swiglu_workspace_bytes(8, 128, 1024, 1024, 0) == u + lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)
+    u = 256 * 1024 * 4
+    assert lib.sgq_swiglu_workspace_bytes(8, 256, 4096, 1024, 0) == u + lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)
     assert lib.sgq_swiglu_workspace_bytes(4, 3, 60, 50, 7) == 768  # flat INT4: always two projections
     assert lib.sgq_swiglu_workspace_bytes(8, 3, 0, 5, 0) == 256  # K == 0: bias-only projections
     assert lib.sgq_swiglu_workspace_bytes(8, 0, 64, 64, 0) == 0
@@ -85,10 +88,12 @@ def test_swiglu_argument_errors_before_gpu(lib):
     assert lib.sgq_swiglu_int8(16, 1, 64, 64, 16, 16, None, None, 16, None, 0, 16, None, 0, None) == 1
     assert lib.sgq_swiglu_int8(16, 1, 64, 64, 16, 16, None, 24, 16, None, 0, 16, None, 0, None) == 1
     assert b"aligned" in lib.sgq_last_error()
-    need = lib.sgq_swiglu_workspace_bytes(8, 32, 64, 64, 0)
-    assert lib.sgq_swiglu_int8(16, 32, 64, 64, 16, 16, None, 16, 16, None, 0, 16, None, 0, None) == 3
+    # 200 rows: past the GEMV form, so the up projection needs the workspace
+    need = lib.sgq_swiglu_workspace_bytes(8, 200, 64, 64, 0)
+    assert need >= 200 * 64 * 4
+    assert lib.sgq_swiglu_int8(16, 200, 64, 64, 16, 16, None, 16, 16, None, 0, 16, None, 0, None) == 3
     assert str(need).encode() in lib.sgq_last_error()
-    assert lib.sgq_swiglu_int8(16, 32, 64, 64, 16, 16, None, 16, 16, None, 0, 16, 16, need - 4, None) == 3
+    assert lib.sgq_swiglu_int8(16, 200, 64, 64, 16, 16, None, 16, 16, None, 0, 16, 16, need - 4, None) == 3
     # int4: tiled layout needs devscales; flat layout needs scales and a workspace even for M = 1
     assert lib.sgq_swiglu_int4(16, 1, 64, 64, 16, 16, None, None, 16, 16, 16, None, 32, 16, None, 0, None) == 1
     assert b"devscales" in lib.sgq_last_error()
@@ -165,11 +170,13 @@ def test_argument_errors_before_gpu(lib, sgq):
     assert lib.sgq_linear_int8(16, 1, 64, 64, 16, 20, 1, None, 16, None, 0, None) == 1  # misaligned scales
     assert lib.sgq_quantize_int4(16, 4, 64, 32, None, 16, 24, 16, None, 0, None) == 1  # misaligned packed
     # A split-K GEMM checks its workspace before any launch.
-    need = lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024)
-    assert lib.sgq_linear_int8(16, 128, 1024, 1024, 16, 16, 0, None, 16, None, 0, None) == 3
+    need = lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)
+    need4 = lib.sgq_linear_workspace_bytes(4, 256, 4096, 1024)
+    assert need > 0 and need4 > 0
+    assert lib.sgq_linear_int8(16, 256, 4096, 1024, 16, 16, 0, None, 16, None, 0, None) == 3
     assert str(need).encode() in lib.sgq_last_error()
-    assert lib.sgq_linear_int8(16, 128, 1024, 1024, 16, 16, 0, None, 16, 256, need - 4, None) == 3
-    assert lib.sgq_linear_int4(16, 128, 1024, 1024, 16, 16, 16, 128, None, 16, 260, need, None) == 3  # misaligned
+    assert lib.sgq_linear_int8(16, 256, 4096, 1024, 16, 16, 0, None, 16, 256, need - 4, None) == 3
+    assert lib.sgq_linear_int4(16, 256, 4096, 1024, 16, 16, 16, 128, None, 16, 260, need4, None) == 3  # misaligned
     # empty outputs are a no-op success
     assert lib.sgq_linear_int8(None, 0, 4, 4, None, None, 0, None, None, None, 0, None) == 0
 

@@ -117,6 +117,25 @@ def test_batch_sizes(sgq, dev, oracle, synth, M, bits_):
 
 
 @pytest.mark.parametrize(
+    "bits_,M,K,N,G,scheme",
+    [
+        (4, 100, 1000, 1000, 128, 0),  # 13 row groups, padded to 16; one scale column per strip (N % G != 0)
+        (4, 72, 2048, 1024, 128, 0),  # 9 row groups -> 16
+        (4, 120, 512, 384, 64, 0),
+        (8, 128, 1024, 1024, 0, 0),  # C1's shape: 16 row groups
+        (8, 57, 777, 515, 0, 1),  # ragged K and N
+        (8, 17, 4099, 30, 0, 0),
+    ],
+)
+def test_mid_batches_on_gemv(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme):
+    # Batches of 17..128 rows with little work run the GEMV in row groups of 8
+    # (no workspace), not the split-K GEMM.
+    assert sgq.load_library().sgq_linear_workspace_bytes(bits_, M, K, N) == 0
+    y, yref = _case(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme, True, 12)
+    assert rel_err(y, yref) <= TOL
+
+
+@pytest.mark.parametrize(
     "M,K,N,G",
     [(1, 1, 8, 8), (3, 17, 24, 8), (5, 130, 77, 7), (2, 33, 40, 24), (19, 18, 200, 40), (7, 100, 12, 8),
      (40, 61, 136, 8), (1, 4099, 24, 8), (20, 45, 13, 5)],
