@@ -162,8 +162,8 @@ struct GemvArgs {
     int ldy;                 // row stride of y and res
     const float* gamma;      // RMSNorm weight [K]: the input is rms_norm(x, gamma, eps)
     float eps;
-    int P, Pshift;           // row groups: M rows in P = 2^Pshift groups of MT (one workgroup each;
-                             // groups past M return at once)
+    int Plog;                // row groups: M rows in 2^Plog groups of MT (one workgroup each; a
+                             // group past M reads zeros for x and writes nothing)
     FastDiv spc;             // INT4: division by mode (strips per scale column)
     int nblk;                // grid x (passed here: reading the hidden gridDim argument cost a second
                              // dependent round of kernel-argument loads ahead of the first data load)
@@ -219,19 +219,18 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // Strips of a scale column share an XCD's L2.  Workgroups of one weight
     // cover (NS + SPW - 1) / SPW strip groups (x of the grid); with several
     // weights side by side (NG == 1), y of the grid selects the weight.
-    // Workgroup v covers row group p = v % P of strip group v / P (P a power of two):
+    // Workgroup v covers row group p = v % P of strip group v / P (P = 2^Plog):
     // the row groups of one strip are neighbours in v, so they run on one XCD
     // and the second read of the strip's codes hits its L2.  No integer
     // division on the way to the first load: every index here is a shift, a
     // mask or a grid coordinate (a runtime division costs about 30 dependent
     // instructions, all of them ahead of the loads).
     const int vg = xcd_swizzle(blockIdx.x, a.nblk);
-    const int prow = vg & (a.P - 1);
-    const int jg = vg >> a.Pshift;
+    const int prow = vg & ((1 << a.Plog) - 1);
+    const int jg = vg >> a.Plog;
     const int m0 = prow * MT;
-    const int M = min(MT, a.M - m0);
-    if (M <= 0) return;  // a row group past M (P rounded up to a power of two); before any barrier
     const float* __restrict__ x = a.x + (int64_t)m0 * K;
+    const int M = min(MT, a.M - m0);  // <= 0 for a padding group: no x rows, no outputs
     const int wt = NG == 1 ? (int)blockIdx.y : 0;
     const int j0 = SPW * jg;
     const int widx = NG == 1 ? wt : grp;
@@ -1015,7 +1014,7 @@ bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x
 
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
-    const dim3 grid((unsigned)(((a.NS + SPW - 1) / SPW) * a.P), (unsigned)nw);
+    const dim3 grid((unsigned)(((a.NS + SPW - 1) / SPW) << a.Plog), (unsigned)nw);
     GemvArgs ag = a;
     ag.nblk = (int)grid.x;
     const bool k4 = a.K % 4 == 0;
@@ -1088,7 +1087,7 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
     // each SIMD holds more than one wavefront to hide load latency.  Measured
     // on MI355X: 5632 -> 2048 at M=8 9.1 -> 7.7 us, M=1 4.8 -> 4.6 us;
     // 2048 -> 2048 at M=4 3.9 -> 3.7 us.
-    if ((int64_t)nw * a.NS * a.P < 2 * kCus && a.RQ >= 8 * 64)
+    if (((int64_t)nw * a.NS << a.Plog) < 2 * kCus && a.RQ >= 8 * 64)
         return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
     // A K too long for one batch of four wavefronts but within one batch of
     // eight: eight wavefronts, so that every load is in flight at once instead
@@ -1109,22 +1108,20 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     // All rows in one launch: M <= 4 as one row group, larger M in row groups
     // of kRowsMax (each a workgroup of its own over the same strip), their
     // count rounded up to a power of two for the index arithmetic.
-    a.P = 1;
-    a.Pshift = 0;
+    a.Plog = 0;
     if (M <= 1) return gemv_launch<BITS, 1, NG>(a, nw, s);
     if (M <= 2) return gemv_launch<BITS, 2, NG>(a, nw, s);
     if (M <= 4) return gemv_launch<BITS, 4, NG>(a, nw, s);
     const int64_t groups = (M + kRowsMax - 1) / kRowsMax;
-    while (a.P < groups) a.P *= 2, ++a.Pshift;
-    if (a.P * kRowsMax > kGemvRowsMax) return hipErrorInvalidValue;
+    while ((int64_t)1 << a.Plog < groups) ++a.Plog;
+    if (((int64_t)kRowsMax << a.Plog) > kGemvRowsMax) return hipErrorInvalidValue;
     return gemv_launch<BITS, kRowsMax, NG>(a, nw, s);
 }
 
 GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad, int64_t RQ, int64_t NS, float* y,
                    int64_t ldy, const float* res) {
     GemvArgs a{};
-    a.P = 1;
-    a.Pshift = 0;
+    a.Plog = 0;
     a.x = x;
     a.K = (int)K;
     a.N = (int)N;
