@@ -268,8 +268,10 @@ int64_t sgq_llama_decode_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_
  *              and no cache write.
  *   workspace: sgq_llama_decode_workspace_bytes(B, D, H, max_len) bytes,
  *              16-byte aligned.
- * B <= 16 runs every projection on the GEMV (q, k, v in one launch; the
- * residual adds in the epilogues); larger B on the MFMA GEMM.  fp32 throughout;
+ * Batches the forward runs on the GEMV (B <= 16, or up to 128 when every
+ * projection's B * K * N <= 2^29) run every projection on it (q, k, v in one
+ * launch; the RMSNorms folded in; the residual adds in the epilogues);
+ * larger B on the MFMA GEMM.  fp32 results throughout;
  * outputs match the reference's full-sequence forward within 1e-5 relative. */
 int sgq_llama_block_decode_int4(const sgq_llama_block_int4* block, const float* x, float* out, int64_t B,
                                 float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,

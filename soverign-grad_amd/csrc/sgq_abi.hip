@@ -87,10 +87,16 @@ bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 // LLaMA block decode workspace, each region 256-byte aligned:
 //   n [B*D] | qkv [3*B*D] | ctx [B*D] | h [B*D] | hid [B*H] | tmp [B*max(D,H)]
-//   | attention partials | GEMM split-K partials (B > 16 only)
+//   | attention partials | GEMM split-K partials (the GEMM path only)
 struct DecodeWs {
     int64_t n, qkv, ctx, h, hid, tmp, part, split, total;
 };
+// The block's GEMV forms (RMSNorm folded in, q/k/v side by side, residual
+// epilogues) serve the batches on which every projection runs the GEMV.
+bool decode_uses_gemv(int64_t B, int64_t D, int64_t H) {
+    return linear_uses_gemv(B, D, 3 * D) && linear_uses_gemv(B, D, H) && linear_uses_gemv(B, H, D);
+}
+
 DecodeWs decode_ws(int64_t B, int64_t D, int64_t H, int64_t max_len) {
     DecodeWs w;
     int64_t o = 0;
@@ -107,7 +113,7 @@ DecodeWs decode_ws(int64_t B, int64_t D, int64_t H, int64_t max_len) {
     w.tmp = take(B * (D > H ? D : H));
     w.part = take(attn_workspace_floats(B, D, max_len));
     int64_t split = 0;
-    if (B > kGemvMaxM) {
+    if (!decode_uses_gemv(B, D, H)) {
         const int64_t a = gemm_workspace_bytes(B, D, D), b = gemm_workspace_bytes(B, D, H),
                       c = gemm_workspace_bytes(B, H, D);
         split = a > b ? a : b;
@@ -574,7 +580,8 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
 
     // attn->forward(norm1->forward(x)), then the residual: h = x + o(ctx).
     // The GEMV path applies each RMSNorm inside the projection that reads it.
-    if (B <= kGemvMaxM) {
+    const bool gemv = decode_uses_gemv(B, D, H);
+    if (gemv) {
         const void* pk[3] = {blk->q.packed, blk->k.packed, blk->v.packed};
         const float* ds[3] = {blk->q.devscales, blk->k.devscales, blk->v.devscales};
         const float* bs[3] = {blk->q.bias, blk->k.bias, blk->v.bias};
@@ -602,7 +609,7 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
         SGQ_HIP(launch_add(x, tmp, h, B * D, s), "add");
     }
     // h + mlp->forward(norm2->forward(h))
-    if (B <= kGemvMaxM) {
+    if (gemv) {
         SGQ_HIP(launch_swiglu_gemv_i4(h, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
                                       blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s, blk->norm2,
                                       blk->eps),

@@ -142,7 +142,8 @@ def _oracle_rows(oracle, x, codes, scales, biases, g1, g2, scale, G):
     (3, 256, 640, 64, 8, [4, 11, 7]),
     (8, 512, 1024, 128, 8, [5, 3, 12, 1, 8, 6, 2, 9]),
     (16, 128, 256, 32, 2, [3] * 16),
-    (20, 128, 256, 32, 2, [2 + (b % 5) for b in range(20)]),  # B > 16: GEMM projections
+    (20, 128, 256, 32, 2, [2 + (b % 5) for b in range(20)]),  # 3 row groups of 8 on the GEMV (padded to 4)
+    (130, 64, 128, 32, 2, [1 + (b % 3) for b in range(130)]),  # B > 128: GEMM projections
 ])
 def test_block_decode_batched(sgq, dev, oracle, synth, B, D, H, G, heads, lengths):
     dm = _decode_mod(sgq)
