@@ -703,10 +703,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 // as the reference's x . (q * s) in k order, so infinities and NaNs land
 // where the reference puts them.
 //
-// Tile 128x128, four wavefronts in 2x2, each 64x64 as 4x4 MFMA blocks; one
-// 32-k stage per LDS buffer, double-buffered, global loads two stages ahead
-// (as k_gemm).  LDS entries are 16 bytes, eight consecutive k of one row (A
-// planes) or one column (B): one MFMA operand.
+// Tiles (G3Shape): INT8 128x256 with eight wavefronts in 2x4, INT4 128x128
+// with four in 2x2; each wavefront owns 64x64 as 4x4 MFMA blocks.  One 32-k
+// stage per LDS buffer, double-buffered, global loads two stages ahead (as
+// k_gemm).  LDS entries are 16 bytes, eight consecutive k of one row (A
+// planes) or one column (B): one MFMA operand.  Per-tensor INT8 puts x itself
+// into A and multiplies by the scale in the epilogue.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int kB3BK = 32;           // k per stage: one 16x16x32 MFMA step
