@@ -794,7 +794,12 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % SH::WM, wn = wave / SH::WM;
     const int ntn = (N + BN - 1) / BN;
-    const int tile = blockIdx.x / KS, split = blockIdx.x - tile * KS;
+    // Without a K split, tiles of one x row block run on one XCD (workgroups
+    // go round-robin over the 8 XCDs, each with its own L2): C4's L2 misses
+    // had every XCD fetch nearly all of x.  Measured 1-2% faster on the large
+    // shapes; with a split (small grids) the plain order measured better.
+    const int bsw = KS == 1 ? xcd_swizzle(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+    const int tile = bsw / KS, split = bsw - tile * KS;
     const int tm = tile / ntn, tn = tile - tm * ntn;
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = (Kpad + kB3BK - 1) / kB3BK;
