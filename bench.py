@@ -606,7 +606,7 @@ def main() -> int:
          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config)}
         if hbm_bound else
         {"bound": "mfma", "achieved": round(tfl, 3), "peak": round(GEMM3_PEAK_TFLOPS, 1), "unit": "TFLOP/s",
-         "frac": round(tfl / GEMM3_PEAK_TFLOPS, 4), "traffic": None,
+         "frac": round(tfl / GEMM3_PEAK_TFLOPS, 4), "traffic": measured_traffic(args.config),
          "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
          "frac_of_fp32_mfma_peak": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4)}
     )
@@ -658,7 +658,8 @@ def main() -> int:
                                          "max": round(reps4[-1], 4)},
             "workload": c4["name"], "rel_err_vs_oracle": err4,
             "roofline": {"bound": "mfma", "achieved": round(tfl4, 3), "peak": round(GEMM3_PEAK_TFLOPS, 1),
-                         "unit": "TFLOP/s", "frac": round(tfl4 / GEMM3_PEAK_TFLOPS, 4), "traffic": None,
+                         "unit": "TFLOP/s", "frac": round(tfl4 / GEMM3_PEAK_TFLOPS, 4),
+                         "traffic": measured_traffic("c4"),
                          "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
                          "frac_of_fp32_mfma_peak": round(tfl4 / FP32_MFMA_PEAK_TFLOPS, 4)},
         }
