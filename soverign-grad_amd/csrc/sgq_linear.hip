@@ -723,6 +723,10 @@ __device__ __forceinline__ float trunc_bf16(float v) { return __uint_as_float(__
 
 // Splits eight floats into the bf16 planes h, m, l (four dwords each).
 __device__ __forceinline__ void split3(const float* v, uint4& h, uint4& m, uint4& l) {
+    // No fma: fused with the multiply that made v (x * s), a - trunc(a)
+    // would take the unrounded product, and h + m + l would miss v by up to
+    // an ulp.
+#pragma clang fp contract(off)
     uint32_t ph[4], pm[4], pl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -368,6 +368,36 @@ def test_gemm_accuracy_vs_fp64(sgq, dev, oracle, synth, bits_, scheme, G):
     assert e_gpu <= 2.0 * e_ref
 
 
+@pytest.mark.parametrize("bits_,scheme,k0", [(8, 0, 0), (8, 1, 0), (8, 1, 150), (4, 0, 0), (4, 0, 150)])
+def test_gemm_split_sums_to_rounded_product(sgq, dev, bits_, scheme, k0):
+    # The three bf16 planes of x * s must add up to x * s rounded once to
+    # fp32, exactly.  With one nonzero activation per row (column k0) and
+    # codes of 1 in weight row k0, every GEMM output is h + m + l (each sum
+    # exact), so y == float32(x * s) bit for bit -- whatever the rounding of
+    # the matrix cores' accumulation.  A split of the unrounded product (an
+    # fma fused into the split) misses by an ulp in about half the outputs.
+    # M = 256 takes the GEMM; K = 256 splits it over four K ranges.
+    M, K, N, G = 256, 256, 256, 128
+    rng = np.random.default_rng(1000 + k0 + bits_)
+    x = np.zeros((M, K), np.float32)
+    x[:, k0] = (rng.standard_normal(M) * 10.0 ** rng.uniform(-3, 3, M)).astype(np.float32)
+    lim = 127 if bits_ == 8 else 7
+    q = rng.integers(-lim, lim + 1, (K, N)).astype(np.float32)
+    q[k0, :] = 1.0
+    if bits_ == 8:
+        s = rng.uniform(1e-3, 1.0, 1 if scheme == 0 else K).astype(np.float32)
+        qw = sgq.pack_int8(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), scheme)
+        s_kn = np.broadcast_to(s[0] if scheme == 0 else s[k0], (N,))
+    else:
+        s = rng.uniform(1e-3, 1.0, K * N // G).astype(np.float32)
+        qw = sgq.pack_int4(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), G)
+        s_kn = s[(k0 * N + np.arange(N)) // G]
+    y = _np(sgq.quantized_matmul(_to_dev(x, dev), qw))
+    want = x[:, k0:k0 + 1] * s_kn[None, :].astype(np.float32)  # float32 products, one rounding
+    assert want.dtype == np.float32
+    assert helpers.same_bits(y, want), np.count_nonzero(y != want)
+
+
 def test_dequantize_matches_reference_product(sgq, dev, oracle, synth):
     W = synth.normal((130, 72), 51, 0, 0.0, 0.02)
     qx = sgq.quantize_int8(_to_dev(W, dev), 1)
