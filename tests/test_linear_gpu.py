@@ -375,7 +375,7 @@ def test_gemm_split_sums_to_rounded_product(sgq, dev, bits_, scheme, k0):
     # codes of 1 in weight row k0, every GEMM output is h + m + l (each sum
     # exact), so y == float32(x * s) bit for bit -- whatever the rounding of
     # the matrix cores' accumulation.  A split of the unrounded product (an
-    # fma fused into the split) misses by an ulp in about half the outputs.
+    # fma fused into the split) misses by an ulp in about a quarter of them.
     # M = 256 takes the GEMM; K = 256 splits it over four K ranges.
     M, K, N, G = 256, 256, 256, 128
     rng = np.random.default_rng(1000 + k0 + bits_)
