@@ -109,6 +109,26 @@ def test_config4_gemm_rows(sgq, dev, oracle, synth):
     assert e <= TOL
 
 
+# Prefill-sized GEMMs, checked on a row subset (first, middle and last rows).
+@pytest.mark.parametrize(
+    "name,bits_,M,K,N,G,scheme",
+    [
+        ("C3_down_prefill_int4_g128", 4, 512, 11008, 4096, 128, 0),  # long K
+        ("C3_gate_prefill_int4_g128_ragged_M", 4, 300, 4096, 11008, 128, 0),  # partial last row tile
+        ("int4_g256_M384", 4, 384, 2048, 2048, 256, 0),  # two 128-column tiles per scale column
+        ("int4_g64_M256", 4, 256, 2048, 1024, 64, 0),  # group not a multiple of 128: the fp32 GEMM
+        ("int8_pc_prefill", 8, 1024, 4096, 11008, 0, 1),
+    ],
+)
+def test_prefill_gemm_rows(sgq, dev, oracle, synth, name, bits_, M, K, N, G, scheme):
+    print(f"  case {name}", flush=True)
+    rows = np.r_[0:16, M // 2 - 8:M // 2 + 8, M - 16:M]
+    y, yref = _case(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme, True, 13, rows=rows)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 15, 16, 17, 31, 33, 64, 129])
 @pytest.mark.parametrize("bits_", [8, 4])
 def test_batch_sizes(sgq, dev, oracle, synth, M, bits_):
