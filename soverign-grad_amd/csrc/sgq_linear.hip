@@ -917,6 +917,14 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         for (int j = 0; j < CB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int lr = lane & 15, lkg = lane >> 4;
+    // Raised wave priority while a wavefront issues its MFMAs lets the two
+    // wavefronts of a SIMD drift out of phase: one in its MFMAs, the other
+    // loading and splitting.  Measured per form (two runs, builds
+    // interleaved): INT4 with the priority over all MFMAs of a stage, 4-5%
+    // faster; INT8 per-tensor over the first half (up to the store),
+    // 1.4-1.8%; INT8 per-channel, whose store does more VALU work, 1-5% slower
+    // with either, so without.  2: whole stage, 1: first half, 0: none.
+    constexpr int kPrio = BITS == 4 ? 2 : (PT ? 1 : 0);
     auto stage = [&](int kt, const Regs& next, Regs& fill) {
         const int buf = kt & 1;
         load(fill, kt + 2);  // past the last stage these read zeros
@@ -927,8 +935,10 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         for (int p = 0; p < 3; ++p)
 #pragma unroll
             for (int i = 0; i < RB; ++i) af[p][i] = As[buf][p][lkg][wm * 16 * RB + i * 16 + lr];
+        if constexpr (kPrio > 0) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
+            if (kPrio == 1 && i == RB / 2) __builtin_amdgcn_s_setprio(0);
             if (i == RB / 2 && kt + 1 < kt1) store(next, buf ^ 1);
 #pragma unroll
             for (int j = 0; j < CB; ++j)
@@ -938,6 +948,7 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
                                                                         __builtin_bit_cast(bf16x8, bq[j]), acc[i][j],
                                                                         0, 0, 0);
         }
+        if constexpr (kPrio == 2) __builtin_amdgcn_s_setprio(0);
         lds_barrier();
     };
 
