@@ -13,13 +13,16 @@ case through either and compare.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 from typing import Optional, Tuple
 
 import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
-ORACLE_LIB = ORACLE_DIR / "liboracle.so"
+# SGQ_ORACLE_LIB selects another build of sgq_oracle.c (the sanitizer build,
+# oracle/liboracle_san.so, loaded by tests/test_sanitize_cpu.py).
+ORACLE_LIB = Path(os.environ.get("SGQ_ORACLE_LIB", ORACLE_DIR / "liboracle.so"))
 REF_LIB = ORACLE_DIR / "_ref" / "libsgref.so"
 
 _i64, _int, _vp, _dbl = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
@@ -256,6 +259,15 @@ class Reference:
         L.ref_qllama_block_int4.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                                             ctypes.c_float, _i64, _vp]
         L.ref_mul.argtypes = [_vp, _vp, _i64, _vp]
+        L.ref_save_qlinear.argtypes = [_int, ctypes.c_char_p, _int, _vp, _i64, _i64, _i64, _vp, ctypes.c_char_p]
+        L.ref_load_qlinear_forward.argtypes = [_int, ctypes.c_char_p, _int, _i64, _i64, _i64, ctypes.c_char_p, _vp,
+                                               _i64, _vp]
+        L.ref_read_entry.argtypes = [_int, ctypes.c_char_p, ctypes.c_char_p, _vp, _i64, ctypes.POINTER(_i64),
+                                     ctypes.POINTER(_int)]
+        L.ref_read_entry.restype = _i64
+        L.ref_save_entries.argtypes = [_int, ctypes.c_char_p, _int, _vp, _vp, _vp, _vp]
+        L.ref_list_entries.argtypes = [_int, ctypes.c_char_p, ctypes.c_char_p, _i64]
+        L.ref_list_entries.restype = _i64
 
     @staticmethod
     def _rc(x: np.ndarray):
@@ -387,6 +399,71 @@ class Reference:
             raise RuntimeError("reference block raised")
         del keep
         return out
+
+    # ---- persistence (format 0: .sgrd, 1: .safetensors) -------------------
+
+    @staticmethod
+    def _fmt(path) -> int:
+        return 1 if str(path).endswith(".safetensors") else 0
+
+    def save_qlinear(self, path, bits: int, W, group_size: int = 32, bias=None, child: str = "") -> None:
+        """The reference's QuantizedLinear (bits 8, per-channel) or
+        QuantizedLinear4Bit (bits 4) built by from_float(W, bias) and saved
+        with save_module, optionally as submodule `child` of a parent module."""
+        W = _f32(W)
+        b = None if bias is None else _f32(bias).reshape(-1)
+        rc = self.lib.ref_save_qlinear(self._fmt(path), str(path).encode(), bits, _p(W), W.shape[0], W.shape[1],
+                                       group_size, _p(b), child.encode())
+        if rc != 0:
+            raise RuntimeError(f"reference save_module raised for {path}")
+
+    def load_qlinear_forward(self, path, bits: int, K: int, N: int, x, group_size: int = 32, child: str = ""):
+        """A fresh reference module of shape [K, N] loaded from `path` with the
+        strict load_module, then its forward on x."""
+        x = _f32(x)
+        out = np.empty((x.shape[0], N), np.float32)
+        rc = self.lib.ref_load_qlinear_forward(self._fmt(path), str(path).encode(), bits, K, N, group_size,
+                                               child.encode(), _p(x), x.shape[0], _p(out))
+        if rc != 0:
+            raise RuntimeError(f"reference load_module / forward raised for {path}")
+        return out
+
+    def read_entry(self, path, name: str):
+        """One tensor of a checkpoint read with the reference's loader."""
+        shape = (_i64 * 8)()
+        rank = _int(0)
+        n = self.lib.ref_read_entry(self._fmt(path), str(path).encode(), name.encode(), None, 0, shape,
+                                    ctypes.byref(rank))
+        if n == -2:
+            raise KeyError(name)
+        if n < 0:
+            raise RuntimeError(f"reference loader raised for {path}")
+        out = np.empty(max(n, 1), np.float32)
+        self.lib.ref_read_entry(self._fmt(path), str(path).encode(), name.encode(), _p(out), n, shape,
+                                ctypes.byref(rank))
+        return out[:n].reshape([shape[i] for i in range(rank.value)])
+
+    def save_entries(self, path, tensors: dict) -> None:
+        """Raw fp32 tensors saved with the reference's save_checkpoint /
+        safetensors::save_file."""
+        names = sorted(tensors)
+        arrs = [_f32(tensors[k]) for k in names]
+        shapes = [np.array(a.shape if a.ndim else (1,), np.int64) for a in arrs]
+        c_names = (ctypes.c_char_p * len(names))(*[k.encode() for k in names])
+        c_data = (ctypes.c_void_p * len(names))(*[a.ctypes.data for a in arrs])
+        c_shapes = (ctypes.c_void_p * len(names))(*[sh.ctypes.data for sh in shapes])
+        c_ranks = (_int * len(names))(*[len(sh) for sh in shapes])
+        rc = self.lib.ref_save_entries(self._fmt(path), str(path).encode(), len(names), c_names, c_data, c_shapes,
+                                       c_ranks)
+        if rc != 0:
+            raise RuntimeError(f"reference save raised for {path}")
+
+    def list_entries(self, path):
+        buf = ctypes.create_string_buffer(1 << 16)
+        n = self.lib.ref_list_entries(self._fmt(path), str(path).encode(), buf, len(buf))
+        if n < 0:
+            raise RuntimeError(f"reference loader raised for {path}")
+        return sorted(e for e in buf.value.decode().split("\n") if e)
 
     def omp_max_threads(self) -> int:
         return int(self.lib.ref_omp_max_threads())

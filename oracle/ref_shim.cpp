@@ -21,13 +21,28 @@
 //   ref_embedding             embedding (src/ops.cpp:2624-2650)
 //   ref_qllama_block_int4     LLaMABlock::forward (include/sovereigngrad/models.hpp:217-222)
 //                             written out with QuantizedLinear4Bit projections
+//   ref_save_qlinear          nn::QuantizedLinear(4Bit)::from_float (nn.hpp:946-954, 984-992), then
+//                             serialization::save_module (src/serialization.cpp:103-105) or
+//                             safetensors::save_module (src/safetensors.cpp:288-290)
+//   ref_load_qlinear_forward  a fresh nn::QuantizedLinear(4Bit) (nn.hpp:935-944, 973-982) loaded
+//                             with load_module (src/serialization.cpp:107-110,
+//                             src/safetensors.cpp:292-295), then forward (nn.hpp:956-958, 994-996)
+//   ref_save_entries          serialization::save_checkpoint / safetensors::save_file of raw tensors
+//   ref_read_entry            serialization::load_checkpoint (src/serialization.cpp:49-101) or
+//                             safetensors::load_file (src/safetensors.cpp:236-286), one entry
+#include "sovereigngrad/nn.hpp"
 #include "sovereigngrad/quantization.hpp"
 #include "sovereigngrad/ops.hpp"
+#include "sovereigngrad/safetensors.hpp"
+#include "sovereigngrad/serialization.hpp"
 
 #include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <exception>
+#include <memory>
+#include <string>
+#include <unordered_map>
 #include <vector>
 
 #ifdef _OPENMP
@@ -67,6 +82,33 @@ QuantizedTensor make_qt(const float* q, const float* scales, int64_t nscales, in
     qt.group_size = group_size;
     qt.bits = bits;
     return qt;
+}
+
+// A quantized linear layer of the reference, optionally registered under
+// `child` in a parent module (so its state_dict keys read "child.qdata").
+struct QLinearTree {
+    std::shared_ptr<nn::Module> root;
+};
+
+QLinearTree wrap(std::shared_ptr<nn::Module> layer, const char* child) {
+    if (!child || !*child) return QLinearTree{layer};
+    auto parent = std::make_shared<nn::Module>();
+    parent->register_module(child, layer);
+    return QLinearTree{parent};
+}
+
+void save_tree(const nn::Module& m, int format, const char* path) {
+    if (format == 0)
+        serialization::save_module(m, path);
+    else
+        safetensors::save_module(m, path);
+}
+
+void load_tree(nn::Module& m, int format, const char* path) {
+    if (format == 0)
+        serialization::load_module(m, path, true);
+    else
+        safetensors::load_module(m, path, true);
 }
 
 }  // namespace
@@ -306,6 +348,113 @@ int ref_qllama_block_int4(const float* x, int64_t L, int64_t D, int64_t H, const
         Tensor hidden = gate * up;
         to_host(h + proj(hidden, 6), out);
         return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Quantizes the fp32 weight W[K, N] with the reference's own module factory
+// (bits 8: QuantizedLinear::from_float, per-channel; bits 4:
+// QuantizedLinear4Bit::from_float with group_size), bias b[N] (or zeros), and
+// saves the module -- or a parent module holding it as `child` -- as .sgrd
+// (format 0) or .safetensors (format 1).  Returns 0, or -1 on error.
+int ref_save_qlinear(int format, const char* path, int bits, const float* W, int64_t K, int64_t N,
+                     int64_t group_size, const float* b, const char* child) {
+    try {
+        nn::Linear fl(K, N, Device::CPU);
+        std::memcpy(fl.W.data(), W, sizeof(float) * (size_t)(K * N));
+        if (b)
+            std::memcpy(fl.b.data(), b, sizeof(float) * (size_t)N);
+        else
+            std::memset(fl.b.data(), 0, sizeof(float) * (size_t)N);
+        std::shared_ptr<nn::Module> layer;
+        if (bits == 8)
+            layer = nn::QuantizedLinear::from_float(fl);
+        else
+            layer = nn::QuantizedLinear4Bit::from_float(fl, group_size);
+        QLinearTree t = wrap(layer, child);
+        save_tree(*t.root, format, path);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Builds a fresh reference module of the given shape (random weights), loads
+// the file into it with the strict load_module, and runs its forward on
+// x[M, K] into y[M, N]: the reference consuming a checkpoint written
+// elsewhere.  Returns 0, or -1 on error (a missing key, a shape mismatch, a
+// malformed file).
+int ref_load_qlinear_forward(int format, const char* path, int bits, int64_t K, int64_t N, int64_t group_size,
+                             const char* child, const float* x, int64_t M, float* y) {
+    try {
+        std::shared_ptr<nn::Module> layer;
+        std::shared_ptr<nn::QuantizedLinear> q8;
+        std::shared_ptr<nn::QuantizedLinear4Bit> q4;
+        if (bits == 8)
+            layer = q8 = std::make_shared<nn::QuantizedLinear>(K, N, Device::CPU);
+        else
+            layer = q4 = std::make_shared<nn::QuantizedLinear4Bit>(K, N, group_size, Device::CPU);
+        QLinearTree t = wrap(layer, child);
+        load_tree(*t.root, format, path);
+        Tensor tx = from_host(x, {M, K});
+        to_host(bits == 8 ? q8->forward(tx) : q4->forward(tx), y);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Reads one entry of a checkpoint with the reference's loader.  Writes up to
+// cap floats into out and the shape into shape[8]/rank; returns the entry's
+// element count, -2 when the name is absent, -1 on error.
+int64_t ref_read_entry(int format, const char* path, const char* name, float* out, int64_t cap, int64_t* shape,
+                       int* rank) {
+    try {
+        auto sd = format == 0 ? serialization::load_checkpoint(path) : safetensors::load_file(path);
+        auto it = sd.find(name);
+        if (it == sd.end()) return -2;
+        const Tensor& t = it->second;
+        *rank = (int)t.shape().size();
+        for (int i = 0; i < *rank && i < 8; ++i) shape[i] = t.shape()[i];
+        const int64_t n = t.numel();
+        if (n <= cap) to_host(t, out);
+        return n;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Saves n tensors (names[i], data[i] with shape shapes[i][0..ranks[i]-1])
+// with serialization::save_checkpoint (format 0, src/serialization.cpp:14-47)
+// or safetensors::save_file (format 1, src/safetensors.cpp:174-234).
+int ref_save_entries(int format, const char* path, int n, const char* const* names, const float* const* data,
+                     const int64_t* const* shapes, const int* ranks) {
+    try {
+        std::unordered_map<std::string, Tensor> sd;
+        for (int i = 0; i < n; ++i) {
+            std::vector<int64_t> shape(shapes[i], shapes[i] + ranks[i]);
+            sd[names[i]] = from_host(data[i], shape);
+        }
+        if (format == 0)
+            serialization::save_checkpoint(sd, path);
+        else
+            safetensors::save_file(sd, path);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Number of entries and their names, '\n'-separated, into names[cap].
+int64_t ref_list_entries(int format, const char* path, char* names, int64_t cap) {
+    try {
+        auto sd = format == 0 ? serialization::load_checkpoint(path) : safetensors::load_file(path);
+        std::string all;
+        for (const auto& kv : sd) all += kv.first + "\n";
+        if ((int64_t)all.size() + 1 > cap) return -1;
+        std::memcpy(names, all.c_str(), all.size() + 1);
+        return (int64_t)sd.size();
     } catch (const std::exception&) {
         return -1;
     }

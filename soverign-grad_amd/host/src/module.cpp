@@ -29,11 +29,19 @@ std::vector<Tensor> Module::parameters() const {
     return out;
 }
 
+// A name under a prefix: "prefix.name", or "name" alone for an empty prefix
+// (src/module.cpp:66,70,97,102).
+static std::string qualified(const std::string& prefix, const std::string& name) {
+    return prefix.empty() ? name : prefix + "." + name;
+}
+
 std::vector<std::pair<std::string, Tensor>> Module::named_parameters(const std::string& prefix) const {
     std::vector<std::pair<std::string, Tensor>> out;
-    for (const auto& kv : parameters_) out.emplace_back(prefix + kv.first, *kv.second);
+    for (const auto& kv : parameters_)
+        if (kv.second && kv.second->is_defined()) out.emplace_back(qualified(prefix, kv.first), *kv.second);
     for (const auto& kv : submodules_) {
-        auto sub = kv.second->named_parameters(prefix + kv.first + ".");
+        if (!kv.second) continue;
+        auto sub = kv.second->named_parameters(qualified(prefix, kv.first));
         out.insert(out.end(), sub.begin(), sub.end());
     }
     return out;
@@ -41,18 +49,24 @@ std::vector<std::pair<std::string, Tensor>> Module::named_parameters(const std::
 
 std::unordered_map<std::string, Tensor> Module::state_dict(const std::string& prefix) const {
     std::unordered_map<std::string, Tensor> out;
-    for (const auto& kv : parameters_) out[prefix + kv.first] = kv.second->clone();
+    for (const auto& kv : parameters_)
+        if (kv.second && kv.second->is_defined()) out[qualified(prefix, kv.first)] = kv.second->clone();
     for (const auto& kv : submodules_) {
-        for (auto& e : kv.second->state_dict(prefix + kv.first + ".")) out[e.first] = e.second;
+        if (!kv.second) continue;
+        for (auto& e : kv.second->state_dict(qualified(prefix, kv.first))) out[e.first] = e.second;
     }
     return out;
 }
 
 void Module::load_state_dict(const std::unordered_map<std::string, Tensor>& sd, bool strict) {
-    // Walk this module's own parameters, then the submodules with their prefix.
+    // Every defined parameter under its qualified name (src/module.cpp:114-134):
+    // missing entries are an error when strict, shapes must match, and the
+    // registered tensor is written in place (copy_from bumps its version, so a
+    // quantized module repacks its device weight on the next forward).
     std::function<void(Module&, const std::string&)> load = [&](Module& m, const std::string& prefix) {
         for (auto& kv : m.parameters_) {
-            const std::string name = prefix + kv.first;
+            if (!kv.second || !kv.second->is_defined()) continue;
+            const std::string name = qualified(prefix, kv.first);
             auto it = sd.find(name);
             if (it == sd.end()) {
                 if (strict) throw std::runtime_error("Missing parameter in state_dict: '" + name + "'");
@@ -60,10 +74,12 @@ void Module::load_state_dict(const std::unordered_map<std::string, Tensor>& sd, 
             }
             Tensor& dst = *kv.second;
             if (dst.shape() != it->second.shape())
-                throw std::runtime_error("Shape mismatch for parameter '" + name + "' in load_state_dict");
-            dst.copy_from(it->second);  // in place; bumps the version, so packed weights rebuild
+                throw std::runtime_error("Shape mismatch for parameter '" + name + "': expected [" + dst.summary() +
+                                         "] but got [" + it->second.summary() + "]");
+            dst.copy_from(it->second);
         }
-        for (auto& kv : m.submodules_) load(*kv.second, prefix + kv.first + ".");
+        for (auto& kv : m.submodules_)
+            if (kv.second) load(*kv.second, qualified(prefix, kv.first));
     };
     load(*this, "");
 }

@@ -271,16 +271,27 @@ void save_file(const std::unordered_map<std::string, Tensor>& sd, const std::str
 }
 
 std::unordered_map<std::string, Tensor> load_file(const std::string& filepath, Device device) {
-    std::ifstream in(filepath, std::ios::binary);
+    std::ifstream in(filepath, std::ios::binary | std::ios::ate);
     if (!in.is_open()) throw std::runtime_error("Failed to open SafeTensors file: " + filepath);
+    const uint64_t file_size = (uint64_t)in.tellg();
+    in.seekg(0);
     auto [metas, header_len] = read_header(in, filepath);
     const uint64_t base = sizeof(uint64_t) + header_len;
     std::unordered_map<std::string, Tensor> sd;
     for (const auto& kv : metas) {
         const TensorMeta& m = kv.second;
         const size_t es = dtype_size(m.dtype);
-        const int64_t numel = compute_numel(m.shape);
-        if (m.data_offset_end - m.data_offset_start != (size_t)numel * es)
+        // Offsets inside the file and a payload of exactly numel elements,
+        // checked before anything is allocated for the entry.
+        if (m.data_offset_end > file_size - base)
+            throw std::runtime_error("SafeTensors entry '" + kv.first + "' lies past the end of " + filepath);
+        int64_t numel = -1;
+        try {
+            numel = compute_numel(m.shape);
+        } catch (const std::exception&) {
+        }
+        if (numel < 0 || (uint64_t)numel > (file_size - base) / es ||
+            m.data_offset_end - m.data_offset_start != (size_t)numel * es)
             throw std::runtime_error("SafeTensors entry '" + kv.first + "' has a payload size that does not match");
         std::vector<char> raw((size_t)numel * es);
         in.seekg((std::streamoff)(base + m.data_offset_start));

@@ -51,8 +51,14 @@ void save_checkpoint(const std::unordered_map<std::string, Tensor>& sd, const st
 }
 
 std::unordered_map<std::string, Tensor> load_checkpoint(const std::string& filepath, Device device) {
-    std::ifstream in(filepath, std::ios::binary);
+    std::ifstream in(filepath, std::ios::binary | std::ios::ate);
     if (!in.is_open()) throw std::runtime_error("Failed to open file for reading checkpoint: " + filepath);
+    // Every length read from the file is checked against the bytes that are
+    // left before anything is allocated for it: a corrupted or truncated file
+    // is an error, never a huge allocation or a read past the end.
+    const int64_t file_size = (int64_t)in.tellg();
+    in.seekg(0);
+    auto left = [&]() { return file_size - (int64_t)in.tellg(); };
     char magic[4] = {0, 0, 0, 0};
     in.read(magic, 4);
     if (!in || std::memcmp(magic, kMagic, 4) != 0)
@@ -64,14 +70,23 @@ std::unordered_map<std::string, Tensor> load_checkpoint(const std::string& filep
     std::unordered_map<std::string, Tensor> sd;
     for (uint32_t i = 0; i < count; ++i) {
         const uint32_t name_len = get<uint32_t>(in, filepath);
+        if ((int64_t)name_len > left()) throw std::runtime_error("Unexpected end of checkpoint file: " + filepath);
         std::string name(name_len, '\0');
         in.read(&name[0], name_len);
         const uint32_t rank = get<uint32_t>(in, filepath);
+        if ((int64_t)rank * 8 + 8 > left()) throw std::runtime_error("Unexpected end of checkpoint file: " + filepath);
         std::vector<int64_t> shape(rank);
         for (auto& d : shape) d = get<int64_t>(in, filepath);
         const int64_t numel = get<int64_t>(in, filepath);
-        if (numel != compute_numel(shape))
+        int64_t expect = -1;
+        try {
+            expect = compute_numel(shape);
+        } catch (const std::exception&) {
+        }
+        if (numel < 0 || numel != expect)
             throw std::runtime_error("Corrupted checkpoint entry '" + name + "': numel does not match shape");
+        if (numel > left() / (int64_t)sizeof(float))
+            throw std::runtime_error("Unexpected end of checkpoint file: " + filepath);
         Tensor t = Tensor::empty(shape, Device::CPU);
         in.read(reinterpret_cast<char*>(t.data()), (std::streamsize)(numel * sizeof(float)));
         if (!in) throw std::runtime_error("Unexpected end of checkpoint file: " + filepath);

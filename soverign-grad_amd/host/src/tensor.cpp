@@ -2,6 +2,7 @@
 // reference's Tensor used by the quantized path; see tensor.hpp).
 #include "sovereigngrad/tensor.hpp"
 
+#include <cstdint>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -27,6 +28,7 @@ int64_t compute_numel(const std::vector<int64_t>& shape) {
     int64_t n = 1;
     for (int64_t d : shape) {
         if (d < 0) throw std::runtime_error("negative dimension in tensor shape");
+        if (d != 0 && n > INT64_MAX / d) throw std::runtime_error("tensor shape overflows int64 element count");
         n *= d;
     }
     return n;

@@ -6,10 +6,12 @@
 //   test_host gpu    tests that run the gfx950 kernels through libsgq.so
 //
 // Exit status 0 when every check passes.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
 #include <fstream>
 #include <functional>
 #include <iostream>
@@ -67,6 +69,69 @@ static double rel_err(const std::vector<float>& y, const std::vector<float>& ref
 }
 
 static std::string tmp_path(const std::string& name) { return "/tmp/sgq_test_" + name; }
+
+// ------------------------------------------------- checkpoints of the reference
+//
+// tests/golden/persist/ holds modules saved by the reference itself
+// (tests/golden/make_persist.py): <name>.sgrd and <name>.safetensors, and
+// <name>.io.sgrd with W, b, x, the reference module's forward y and
+// meta = [bits, K, N, group_size, M, nested] (nested: the layer is submodule
+// "proj" of a parent module).
+struct RefWeight {
+    std::string name, dir;
+    int bits = 0;
+    int64_t K = 0, N = 0, G = 0, M = 0;
+    bool nested = false;
+    std::unordered_map<std::string, Tensor> io;
+    std::string file(const std::string& ext) const { return dir + "/" + name + ext; }
+    std::string key(const std::string& p) const { return nested ? "proj." + p : p; }
+};
+
+static std::vector<RefWeight> reference_weights(const std::string& dir) {
+    std::vector<RefWeight> out;
+    std::vector<std::string> names;
+    for (const auto& e : std::filesystem::directory_iterator(dir)) {
+        const std::string f = e.path().filename().string();
+        const std::string suffix = ".io.sgrd";
+        if (f.size() > suffix.size() && f.compare(f.size() - suffix.size(), suffix.size(), suffix) == 0)
+            names.push_back(f.substr(0, f.size() - suffix.size()));
+    }
+    std::sort(names.begin(), names.end());
+    for (const auto& n : names) {
+        RefWeight w;
+        w.name = n;
+        w.dir = dir;
+        w.io = serialization::load_checkpoint(w.file(".io.sgrd"));
+        const std::vector<float> m = host(w.io.at("meta"));
+        w.bits = (int)m[0];
+        w.K = (int64_t)m[1];
+        w.N = (int64_t)m[2];
+        w.G = (int64_t)m[3];
+        w.M = (int64_t)m[4];
+        w.nested = m[5] != 0.0f;
+        out.push_back(std::move(w));
+    }
+    return out;
+}
+
+// The tree the reference saved: the layer itself, or a parent holding it as "proj".
+static std::shared_ptr<nn::Module> tree_of(std::shared_ptr<nn::Module> layer, bool nested) {
+    if (!nested) return layer;
+    auto parent = std::make_shared<nn::Module>();
+    parent->register_module("proj", layer);
+    return parent;
+}
+
+// A parameter holder with a quantized layer's names and no quantization work,
+// so that host-only tests can re-save what they loaded through Module::state_dict.
+struct CodesHolder : nn::Module {
+    Tensor qdata, scales, bias;
+    CodesHolder(const Tensor& q, const Tensor& s, const Tensor& b) : qdata(q), scales(s), bias(b) {
+        register_parameter("qdata", qdata);
+        register_parameter("scales", scales);
+        register_parameter("bias", bias);
+    }
+};
 
 // ---------------------------------------------------------------- host-only
 
@@ -149,7 +214,46 @@ static void test_module_state_dict() {
     missing.erase("bias");
     CHECK(throws([&] { other.load_state_dict(missing, true); }));
     other.load_state_dict(missing, false);
-    std::cout << "  * names, clones, strict shape check, missing keys: PASSED\n";
+
+    // Qualified names (src/module.cpp:60-75,94-112): "prefix.name", nested
+    // submodules joined with '.', no separator for an empty prefix, and
+    // undefined parameters skipped.
+    struct Leaf : nn::Module {
+        Tensor a = Tensor::zeros({2}), unset;
+        Leaf() {
+            register_parameter("a", a);
+            register_parameter("unset", unset);
+        }
+    };
+    auto inner = std::make_shared<Leaf>();
+    auto mid = std::make_shared<nn::Module>();
+    mid->register_module("inner", inner);
+    nn::Module top;
+    top.register_module("mid", mid);
+    auto leaf_top = std::make_shared<Leaf>();
+    top.register_module("head", leaf_top);
+    auto keys = [](const std::unordered_map<std::string, Tensor>& m) {
+        std::vector<std::string> k;
+        for (const auto& kv : m) k.push_back(kv.first);
+        std::sort(k.begin(), k.end());
+        return k;
+    };
+    CHECK(keys(top.state_dict()) == std::vector<std::string>({"head.a", "mid.inner.a"}));
+    CHECK(keys(top.state_dict("model")) == std::vector<std::string>({"model.head.a", "model.mid.inner.a"}));
+    CHECK(keys(inner->state_dict("x.y")) == std::vector<std::string>({"x.y.a"}));
+    std::vector<std::string> np;
+    for (const auto& kv : top.named_parameters("model")) np.push_back(kv.first);
+    std::sort(np.begin(), np.end());
+    CHECK(np == std::vector<std::string>({"model.head.a", "model.mid.inner.a"}));
+    CHECK(top.parameters().size() == 2);
+    // load_state_dict takes the unprefixed names of the tree it is called on.
+    auto tsd = top.state_dict();
+    tsd["mid.inner.a"] = Tensor::full({2}, 4.0f);
+    top.load_state_dict(tsd);
+    CHECK(host(inner->a)[1] == 4.0f);
+    tsd.erase("head.a");
+    CHECK(throws([&] { top.load_state_dict(tsd, true); }));
+    std::cout << "  * names, clones, strict shape check, missing keys, prefixes of nested modules: PASSED\n";
 }
 
 static void test_sgrd_format() {
@@ -220,6 +324,168 @@ static void test_safetensors_format() {
     CHECK(host(sd["a"]) == std::vector<float>({1.0f, -2.5f}));
     CHECK(host(sd["b"]) == std::vector<float>({-7.0f, 9.0f}));
     std::cout << "  * round trip, inspect, F16/I32 payloads, metadata: PASSED\n";
+}
+
+
+// The host layer's two loaders read the reference's own files: both formats
+// give the same tensors, under the reference's keys, with integral codes in
+// range and the reference's scale count.  Then the host writers save the same
+// state under the same tree into out_dir, for the reference to load back
+// (tests/test_persist_cpu.py).
+static void test_reference_checkpoints_read(const std::string& dir, const std::string& out_dir) {
+    std::cout << "--- checkpoints written by the reference\n";
+    int n = 0;
+    for (const RefWeight& w : reference_weights(dir)) {
+        auto a = serialization::load_checkpoint(w.file(".sgrd"));
+        auto b = safetensors::load_file(w.file(".safetensors"));
+        CHECK(a.size() == 3 && b.size() == 3);
+        for (const char* p : {"qdata", "scales", "bias"}) {
+            CHECK(a.count(w.key(p)) && b.count(w.key(p)));
+            if (!a.count(w.key(p)) || !b.count(w.key(p))) continue;
+            CHECK(a[w.key(p)].shape() == b[w.key(p)].shape());
+            CHECK(same_bits(host(a[w.key(p)]), host(b[w.key(p)])));
+        }
+        const auto q = host(a[w.key("qdata")]);
+        const int lim = w.bits == 8 ? 127 : 7;
+        bool ok = a[w.key("qdata")].shape() == std::vector<int64_t>({w.K, w.N});
+        for (float c : q) ok = ok && c == std::round(c) && std::fabs(c) <= lim;
+        CHECK(ok);
+        const int64_t ns = w.bits == 8 ? w.K : (w.K * w.N + w.G - 1) / w.G;
+        CHECK(a[w.key("scales")].numel() == ns);
+        CHECK(same_bits(host(a[w.key("bias")]), host(w.io.at("b"))));
+        const auto meta = safetensors::inspect_file(w.file(".safetensors"));
+        CHECK(meta.count(w.key("qdata")) && meta.at(w.key("qdata")).dtype == "F32");
+        if (!out_dir.empty()) {
+            auto layer = std::make_shared<CodesHolder>(a[w.key("qdata")], a[w.key("scales")], a[w.key("bias")]);
+            auto tree = tree_of(layer, w.nested);
+            serialization::save_module(*tree, out_dir + "/" + w.name + ".sgrd");
+            safetensors::save_module(*tree, out_dir + "/" + w.name + ".safetensors");
+        }
+        ++n;
+    }
+    CHECK(n >= 5);
+    std::cout << "  * " << n << " reference-written modules, .sgrd == .safetensors, keys, codes, scales: PASSED\n";
+}
+
+// Damaged files: every truncation of a valid .sgrd and .safetensors file, every
+// single-byte change of their headers, and hand-made malformed headers must
+// either load or throw -- never crash, hang, read past the end or allocate
+// what the file cannot hold.  (Run under the sanitizer build too.)
+static void test_corrupt_files() {
+    std::cout << "--- damaged checkpoint files\n";
+    nn::Linear lin(3, 2);
+    const std::string sp = tmp_path("ok.sgrd"), tp = tmp_path("ok.safetensors");
+    serialization::save_module(lin, sp);
+    safetensors::save_module(lin, tp);
+    auto slurp = [](const std::string& p) {
+        std::ifstream in(p, std::ios::binary);
+        return std::string((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
+    };
+    auto spit = [](const std::string& p, const std::string& bytes) {
+        std::ofstream o(p, std::ios::binary);
+        o.write(bytes.data(), (std::streamsize)bytes.size());
+    };
+    const std::string sgrd = slurp(sp), st = slurp(tp);
+    const std::string bad = tmp_path("damaged");
+    int loaded = 0, thrown = 0;
+    auto attempt = [&](bool safet) {
+        try {
+            if (safet)
+                safetensors::load_file(bad);
+            else
+                serialization::load_checkpoint(bad);
+            ++loaded;
+        } catch (const std::exception&) {
+            ++thrown;
+        }
+    };
+    for (size_t n = 0; n < sgrd.size(); ++n) {  // every proper prefix is an error
+        spit(bad, sgrd.substr(0, n));
+        const int t0 = thrown;
+        attempt(false);
+        CHECK(thrown == t0 + 1);
+    }
+    for (size_t n = 0; n < st.size(); ++n) {
+        spit(bad, st.substr(0, n));
+        const int t0 = thrown;
+        attempt(true);
+        CHECK(thrown == t0 + 1);
+    }
+    // Every byte of the .sgrd structure (everything but the payload floats of
+    // the first entry) and of the safetensors length + JSON header, set to a
+    // few values: 0x00, 0xFF, 0x7F, '{', '"', '-', '9'.
+    const unsigned char vals[] = {0x00, 0xFF, 0x7F, '{', '"', '-', '9'};
+    const size_t st_hdr = 8 + (size_t)*reinterpret_cast<const uint64_t*>(st.data());
+    for (size_t i = 0; i < sgrd.size(); ++i)
+        for (unsigned char v : vals) {
+            std::string b = sgrd;
+            b[i] = (char)v;
+            spit(bad, b);
+            attempt(false);
+        }
+    for (size_t i = 0; i < st_hdr; ++i)
+        for (unsigned char v : vals) {
+            std::string b = st;
+            b[i] = (char)v;
+            spit(bad, b);
+            attempt(true);
+        }
+    // Hand-made headers: wrong offsets, negative or huge dims, unknown dtype,
+    // unterminated JSON, a header longer than the file.
+    auto st_file = [&](const std::string& js, size_t payload) {
+        std::string b(8, '\0');
+        const uint64_t len = js.size();
+        std::memcpy(&b[0], &len, 8);
+        spit(bad, b + js + std::string(payload, '\0'));
+    };
+    const char* headers[] = {
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[0,16]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[-2],\"data_offsets\":[0,8]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[4611686018427387904,4],\"data_offsets\":[0,0]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[8,0]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[0,18446744073709551615]}}",
+        "{\"a\":{\"dtype\":\"Q7\",\"shape\":[2],\"data_offsets\":[0,8]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[0,8]}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2]}}",
+        "{\"a\":{\"dtype\":\"F32\",\"shape\":[2,\"data_offsets\":[0,8]}}",
+        "{\"__metadata__\":{\"k\":[1,{\"x\":\"y\"}]},\"a\":",
+        "\"a\"",
+        "{\"a\\",
+    };
+    for (const char* h : headers) {
+        st_file(h, 8);
+        const int t0 = thrown;
+        attempt(true);
+        CHECK(thrown == t0 + 1);
+    }
+    {  // a header length beyond the file
+        std::string b(8, '\0');
+        const uint64_t len = 1000;
+        std::memcpy(&b[0], &len, 8);
+        spit(bad, b + "{}");
+        const int t0 = thrown;
+        attempt(true);
+        CHECK(thrown == t0 + 1);
+    }
+    {  // an .sgrd entry claiming 2^32-1 dims, or a name longer than the file
+        std::string b = sgrd.substr(0, 12);
+        const uint32_t nl = 1, rank = 0xFFFFFFFFu;
+        b.append(reinterpret_cast<const char*>(&nl), 4);
+        b += "w";
+        b.append(reinterpret_cast<const char*>(&rank), 4);
+        spit(bad, b);
+        int t0 = thrown;
+        attempt(false);
+        CHECK(thrown == t0 + 1);
+        b = sgrd.substr(0, 12);
+        const uint32_t big = 0x7FFFFFFFu;
+        b.append(reinterpret_cast<const char*>(&big), 4);
+        spit(bad, b);
+        t0 = thrown;
+        attempt(false);
+        CHECK(thrown == t0 + 1);
+    }
+    std::cout << "  * " << thrown << " rejected, " << loaded << " loaded, no crash: PASSED\n";
 }
 
 // --------------------------------------------------------------------- GPU
@@ -340,6 +606,67 @@ static void test_persistence_bridge() {
         CHECK(throws([&] { e8.forward(x); }));
     }
     std::cout << "  * .sgrd, .safetensors and load_state_dict repack (CPU and CUDA modules): PASSED\n";
+}
+
+
+// Reference-written checkpoints into the host layer's quantized modules on the
+// GPU: the loaded codes and scales are the ones this library's quantizer
+// produces from the same float weight (bit for bit), and the forward matches
+// the reference module's own forward within 1e-5.  With out_dir set, modules
+// quantized here (from_float on the GPU) are saved by the host writers there,
+// for the reference to load (tests/test_persist_cpu.py).
+static void test_reference_checkpoints_forward(const std::string& dir, const std::string& out_dir) {
+    std::cout << "--- reference checkpoints -> host modules on CUDA\n";
+    double worst = 0.0;
+    int n = 0;
+    for (const RefWeight& w : reference_weights(dir)) {
+        const Tensor Wd = w.io.at("W").to(Device::CUDA);
+        quantization::QuantizedTensor mine =
+            w.bits == 8 ? quantization::quantize_int8(Wd, QuantizationScheme::PerChannelSymmetric)
+                        : quantization::quantize_int4(Wd, w.G);
+        for (const char* ext : {".sgrd", ".safetensors"}) {
+            std::shared_ptr<nn::Module> layer;
+            std::shared_ptr<nn::QuantizedLinear> q8;
+            std::shared_ptr<nn::QuantizedLinear4Bit> q4;
+            if (w.bits == 8)
+                layer = q8 = std::make_shared<nn::QuantizedLinear>(w.K, w.N, Device::CUDA);
+            else
+                layer = q4 = std::make_shared<nn::QuantizedLinear4Bit>(w.K, w.N, w.G, Device::CUDA);
+            auto tree = tree_of(layer, w.nested);
+            if (std::string(ext) == ".sgrd")
+                serialization::load_module(*tree, w.file(ext));
+            else
+                safetensors::load_module(*tree, w.file(ext));
+            const auto& qw = w.bits == 8 ? q8->q_weight : q4->q_weight;
+            CHECK(same_bits(host(qw.qdata), host(mine.qdata)));
+            CHECK(same_bits(host(qw.scales), host(mine.scales)));
+            auto sd = tree->state_dict();
+            CHECK(sd.count(w.key("qdata")) && sd.count(w.key("scales")) && sd.count(w.key("bias")));
+            const Tensor x = w.io.at("x").to(Device::CUDA);
+            const Tensor y = w.bits == 8 ? q8->forward(x) : q4->forward(x);
+            CHECK(y.device() == Device::CUDA);
+            const double e = rel_err(host(y), host(w.io.at("y")));
+            worst = std::max(worst, e);
+            CHECK(e <= 1e-5);
+            ++n;
+        }
+        if (!out_dir.empty()) {  // the same weight through from_float on the GPU, saved by the host layer
+            nn::Linear fl(w.K, w.N, Device::CUDA);
+            fl.W.copy_from(w.io.at("W"));
+            fl.b.copy_from(w.io.at("b"));
+            std::shared_ptr<nn::Module> layer;
+            if (w.bits == 8)
+                layer = nn::QuantizedLinear::from_float(fl);
+            else
+                layer = nn::QuantizedLinear4Bit::from_float(fl, w.G);
+            auto tree = tree_of(layer, w.nested);
+            serialization::save_module(*tree, out_dir + "/" + w.name + ".sgrd");
+            safetensors::save_module(*tree, out_dir + "/" + w.name + ".safetensors");
+        }
+    }
+    CHECK(n >= 10);
+    std::cout << "  * " << n << " loads, codes/scales bit-exact with this quantizer, worst forward rel err " << worst
+              << ": " << (worst <= 1e-5 ? "PASSED" : "FAILED") << "\n";
 }
 
 static void test_module_to_device() {
@@ -504,14 +831,21 @@ static void test_llama_block_decode() {
 }
 
 int main(int argc, char** argv) {
+    // test_host cpu|gpu [golden_persist_dir [out_dir]]
     const std::string mode = argc > 1 ? argv[1] : "cpu";
+    const std::string golden = argc > 2 ? argv[2] : "";
+    const std::string out_dir = argc > 3 ? argv[3] : "";
+    if (!out_dir.empty()) std::filesystem::create_directories(out_dir);
     std::vector<std::pair<std::string, std::function<void()>>> tests;
     if (mode == "cpu") {
         tests = {{"allocator_cpu", test_allocator_cpu},
                  {"tensor_basics", test_tensor_basics},
                  {"module_state_dict", test_module_state_dict},
                  {"sgrd_format", test_sgrd_format},
-                 {"safetensors_format", test_safetensors_format}};
+                 {"safetensors_format", test_safetensors_format},
+                 {"corrupt_files", test_corrupt_files}};
+        if (!golden.empty())
+            tests.push_back({"reference_checkpoints_read", [&] { test_reference_checkpoints_read(golden, out_dir); }});
     } else if (mode == "gpu") {
         tests = {{"allocator_gpu", test_allocator_gpu},
                  {"quantization_cpu", [] { test_quantization(Device::CPU); }},
@@ -521,8 +855,11 @@ int main(int argc, char** argv) {
                  {"module_to_device", test_module_to_device},
                  {"concurrent_forward", test_concurrent_forward},
                  {"llama_block_decode", test_llama_block_decode}};
+        if (!golden.empty())
+            tests.push_back(
+                {"reference_checkpoints_forward", [&] { test_reference_checkpoints_forward(golden, out_dir); }});
     } else {
-        std::cerr << "usage: test_host cpu|gpu\n";
+        std::cerr << "usage: test_host cpu|gpu [golden_persist_dir [out_dir]]\n";
         return 2;
     }
     for (auto& t : tests) {

@@ -12,7 +12,8 @@ BIN = helpers.PKG_DIR / "host" / "test_host"
 def test_host_layer_cpu():
     if not BIN.exists():
         pytest.fail(f"{BIN} is not built (run __graft_entry__.build())")
-    r = subprocess.run([str(BIN), "cpu"], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([str(BIN), "cpu", str(helpers.GOLDEN_DIR / "persist")], capture_output=True, text=True,
+                       timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "ALL PASSED" in r.stdout
