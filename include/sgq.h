@@ -98,6 +98,18 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
  * time must not share one workspace.  16-byte alignment required. */
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
 
+/* The kernel a forward of this shape runs and its K splits, on a device
+ * with `compute_units` CUs (0: the calling thread's current device; a full
+ * MI355X has 256, a partition fewer).  *path: 0 the GEMV, 1 the three-term
+ * bf16 MFMA GEMM, 2 the fp32 MFMA GEMM (INT4 groups that are not a multiple
+ * of 128), 3 the generic kernel of the flat INT4 layout.  *k_splits: 1, or
+ * the number of workgroups sharing each output tile's K range (the GEMM on
+ * grids smaller than the device).  sgq_linear_workspace_bytes sizes for the
+ * largest device, so it covers every plan.  Host-only; this library's own
+ * extension (the reference has no launch planning). */
+int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int* path,
+                    int* k_splits);
+
 /* Zero-fills a workspace with a kernel (no hipMemset), on `stream`. */
 int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 

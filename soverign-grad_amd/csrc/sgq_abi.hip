@@ -127,6 +127,23 @@ DecodeWs decode_ws(int64_t B, int64_t D, int64_t H, int64_t max_len) {
 
 bool bad_dims(int64_t a, int64_t b) { return a < 0 || b < 0 || a > kMaxDim || b > kMaxDim || a * b > ((int64_t)1 << 40); }
 
+// The forward kernels address a strip of codes, a scale column and a row of x
+// (GEMV: Kpad * 4 bytes each) or a 128-row tile of x (GEMM: 128 * K * 4 bytes)
+// through 32-bit buffer offsets.  Shapes past those limits are refused with
+// SGQ_ERR_UNSUPPORTED instead of wrapping into wrong outputs.
+constexpr int64_t kGemvMaxKpad = ((int64_t)1 << 29) - kPadK;  // Kpad * 4 < 2^31
+constexpr int64_t kGemmMaxK = (int64_t)1 << 22;               // 128 * K * 4 <= 2^31
+bool forward_fits(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size) {
+    if (round_up(K, kPadK) > kGemvMaxKpad) return false;
+    if (linear_uses_gemv(M, K, N)) return true;
+    if (K > kGemmMaxK) return false;
+    if (bits == 4) {  // the fp32-MFMA kernel (groups not a multiple of 128) maps all devscales at once
+        const I4Geom g(K, N, group_size);
+        if (g.tiled && g.spc % 16 != 0 && g.devscale_count() * 4 >= ((int64_t)1 << 32)) return false;
+    }
+    return true;
+}
+
 int check_codes_flag(const int* dflag, hipStream_t s) {
     int host_flag = 0;
     SGQ_HIP(hipMemcpyAsync(&host_flag, dflag, sizeof(int), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flag)");
@@ -181,6 +198,15 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N) {
     if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4)) return -1;
     return linear_ws_bytes(bits, M, K, N);
+}
+
+int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int* path,
+                    int* k_splits) {
+    if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4) || compute_units < 0 || !path || !k_splits)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_plan: bad argument");
+    const int64_t cus = compute_units > 0 ? compute_units : device_cus(nullptr);
+    linear_plan(bits, M, K, N, group_size, cus, path, k_splits);
+    return ok();
 }
 
 int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size) {
@@ -326,6 +352,8 @@ int sgq_dequantize_int8(const void* packed, const float* scales, int scheme, int
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: bad scheme");
     if (K * N > 0 && (!packed || !scales || !out))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: null pointer");
+    if (K * N > 0 && !aligned16(packed))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int8: packed must be 16-byte aligned");
     SGQ_HIP(launch_unpack_i8_tiled(packed, K, N, scales, scheme == SGQ_PER_TENSOR_SYMMETRIC, out,
                                    (hipStream_t)stream),
             "unpack_i8");
@@ -338,6 +366,8 @@ int sgq_dequantize_int4(const void* packed, const float* scales, int64_t K, int6
     if (K * N > 0 && (!packed || !scales || !out))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int4: null pointer");
     const I4Geom g(K, N, group_size);
+    if (K * N > 0 && g.tiled && !aligned16(packed))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_dequantize_int4: packed must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     if (g.tiled)
         SGQ_HIP(launch_unpack_i4_tiled(packed, K, N, g.G, scales, out, s), "unpack_i4_tiled");
@@ -385,6 +415,8 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     const bool per_tensor = scheme == SGQ_PER_TENSOR_SYMMETRIC;
     if (!aligned16(packed) || (!per_tensor && !aligned16(scales)))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: packed and per-channel scales must be 16-byte aligned");
+    if (!forward_fits(8, M, K, N, 0))
+        return fail(SGQ_ERR_UNSUPPORTED, "sgq_linear_int8: K = %lld is too long for this batch", (long long)K);
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
@@ -417,6 +449,8 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
     if (!aligned16(packed) || !aligned16(devscales))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: packed and devscales must be 16-byte aligned");
+    if (!forward_fits(4, M, K, N, g.G))
+        return fail(SGQ_ERR_UNSUPPORTED, "sgq_linear_int4: K = %lld is too long for this batch", (long long)K);
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
@@ -454,6 +488,8 @@ int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (!aligned16(packed_gate) || !aligned16(packed_up) ||
         (!per_tensor && (!aligned16(scales_gate) || !aligned16(scales_up))))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and per-channel scales must be 16-byte aligned", fn);
+    if (!forward_fits(8, M, K, N, 0))
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i8(x, M, K, N, packed_gate, scales_gate, bias_gate, packed_up, scales_up, bias_up,
                                       per_tensor, h, s),
@@ -499,6 +535,8 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: tiled layout needs devscales", fn);
     if (!aligned16(packed_gate) || !aligned16(packed_up) || !aligned16(devscales_gate) || !aligned16(devscales_up))
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
+    if (!forward_fits(4, M, K, N, g.G))
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i4(x, M, K, N, packed_gate, devscales_gate, bias_gate, packed_up, devscales_up,
                                       bias_up, g, h, s),
@@ -554,6 +592,8 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
     const I4Geom gdd(D, D, G), gdh(D, H, G), ghd(H, D, G);
     if (!gdd.tiled || !gdh.tiled || !ghd.tiled)
         return fail(SGQ_ERR_UNSUPPORTED, "%s: D, H and group_size must be multiples of 8 (tiled INT4 layout)", fn);
+    if (H > kGemmMaxK)  // the down projection's K, within both forward kernels' 32-bit offsets
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: H > %lld", fn, (long long)kGemmMaxK);
     const sgq_int4_linear* lin[7] = {&blk->q, &blk->k, &blk->v, &blk->o, &blk->gate, &blk->up, &blk->down};
     for (int i = 0; i < 7; ++i) {
         if (!lin[i]->packed || !lin[i]->devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null weight", fn);

@@ -148,10 +148,20 @@ struct GemmPlan {
 struct GemmTile {
     int64_t bm, bn, per_cu;  // tile rows and columns, workgroups resident per CU
 };
-constexpr int64_t kCus = 256;  // MI355X compute units
-GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t);
+// Compute units the launch heuristics plan for: the count of the device a
+// stream runs on (a partition of an MI355X reports its own share), at most
+// kMaxCus, the full MI355X.  Split-K workspaces are sized for kMaxCus, an upper
+// bound for every smaller count: the number of K splits never grows as the CU
+// count shrinks.
+constexpr int64_t kMaxCus = 256;
+int device_cus(hipStream_t s);
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus);
 GemmTile gemm_tile(int bits);
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+// The plan a forward of this shape runs on `cus` compute units: path 0 the
+// GEMV, 1 the three-term bf16 GEMM, 2 the fp32 GEMM, 3 the flat INT4 kernel;
+// ks the K splits (1: none).
+void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int64_t cus, int* path, int* ks);
 hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, void* ws, hipStream_t s);
 hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,

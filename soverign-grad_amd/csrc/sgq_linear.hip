@@ -167,6 +167,7 @@ struct GemvArgs {
     FastDiv spc;             // INT4: division by mode (strips per scale column)
     int nblk;                // grid x (passed here: reading the hidden gridDim argument cost a second
                              // dependent round of kernel-argument loads ahead of the first data load)
+    int cus;                 // compute units of the launch's device (host-side heuristics only)
 };
 
 // ---------------------------------------------------------------------------
@@ -1097,7 +1098,7 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
         // wavefronts to keep all of K in one batch of loads.  Measured on
         // MI355X at M=1: 4096->4096 4.30 -> 4.21 us, 4096->11008 7.67 -> 6.93,
         // 11008->4096 7.39 -> 7.22 (16 wavefronts); M=2 4096->11008 9.11 -> 8.52.
-        if (nw == 1 && a.mode % 2 == 0 && a.NS >= 2 * kCus) {
+        if (nw == 1 && a.mode % 2 == 0 && a.NS >= 2 * a.cus) {
             constexpr int um = gemv_umax(2 * MT);
             if (a.RQ <= um * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, kGemvWaves>(a, nw, s);
             if (a.RQ <= um * 2 * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, 2 * kGemvWaves>(a, nw, s);
@@ -1109,7 +1110,7 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
     // each SIMD holds more than one wavefront to hide load latency.  Measured
     // on MI355X: 5632 -> 2048 at M=8 9.1 -> 7.7 us, M=1 4.8 -> 4.6 us;
     // 2048 -> 2048 at M=4 3.9 -> 3.7 us.
-    if (((int64_t)nw * a.NS << a.Plog) < 2 * kCus && a.RQ >= 8 * 64)
+    if (((int64_t)nw * a.NS << a.Plog) < 2 * a.cus && a.RQ >= 8 * 64)
         return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
     // A K too long for one batch of four wavefronts but within one batch of
     // eight: eight wavefronts, so that every load is in flight at once instead
@@ -1126,6 +1127,7 @@ hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
 template <int BITS, int NG>
 hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.M = (int)M;
+    a.cus = device_cus(s);
     constexpr int kRowsMax = 8;  // rows per workgroup beyond four
     // All rows in one launch: M <= 4 as one row group, larger M in row groups
     // of kRowsMax (each a workgroup of its own over the same strip), their
@@ -1229,12 +1231,31 @@ hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t) {
+int device_cus(hipStream_t s) {
+    int dev = 0;
+    if (hipStreamGetDevice(s, &dev) != hipSuccess) {
+        (void)hipGetLastError();  // leave no error behind for the launch check
+        if (hipGetDevice(&dev) != hipSuccess) {
+            (void)hipGetLastError();
+            return (int)kMaxCus;
+        }
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) {
+        (void)hipGetLastError();
+        return (int)kMaxCus;
+    }
+    return cus < kMaxCus ? cus : (int)kMaxCus;
+}
+
+GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus) {
     const int64_t tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
     const int64_t KT = ceil_div(round_up(K, kPadK), kBK);
     GemmPlan p{1, (int)KT};
-    if (tiles < t.per_cu * kCus && KT >= 4) {
-        int64_t ks = ceil_div(t.per_cu * kCus, tiles);  // about per_cu workgroups per CU
+    if (cus < 1) cus = 1;
+    if (cus > kMaxCus) cus = kMaxCus;
+    if (tiles < t.per_cu * cus && KT >= 4) {
+        int64_t ks = ceil_div(t.per_cu * cus, tiles);  // about per_cu workgroups per CU
         if (ks > KT / 2) ks = KT / 2;                     // at least two stages per split
         if (ks > kMaxSplits) ks = kMaxSplits;
         if (ks > 1) {
@@ -1251,26 +1272,46 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t) {
 GemmTile gemm_tile(int bits) { return bits == 8 ? GemmTile{kBM, 2 * kBN, 1} : GemmTile{kBM, kBN, 2}; }
 
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    // Either code width (and the fp32 kernel's 128 x 128 tile): room for the largest plan.
-    int64_t ks = gemm_plan(M, K, N, GemmTile{kBM, kBN, 2}).KS;
+    // Either code width (and the fp32 kernel's 128 x 128 tile) on the largest
+    // device: room for the largest plan on any device.
+    int64_t ks = gemm_plan(M, K, N, GemmTile{kBM, kBN, 2}, kMaxCus).KS;
     for (int bits : {4, 8}) {
-        const int64_t k = gemm_plan(M, K, N, gemm_tile(bits)).KS;
+        const int64_t k = gemm_plan(M, K, N, gemm_tile(bits), kMaxCus).KS;
         if (k > ks) ks = k;
     }
     return ks > 1 ? ks * M * N * 4 : 0;
+}
+
+// Which GEMM kernel a shape takes and its tile: the three-term bf16 kernel
+// folds the scale into A, so a tile's columns must share their scale (always
+// for INT8's 256-column tiles; for INT4 when a scale column spans a multiple
+// of 16 strips, i.e. a group that is a multiple of 128).
+static bool gemm_three_term(int bits, int mode) { return bits == 8 || mode % 16 == 0; }
+
+void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int64_t cus, int* path, int* ks) {
+    *ks = 1;
+    if (bits == 4 && !I4Geom(K, N, group_size).tiled) {
+        *path = 3;
+        return;
+    }
+    if (linear_uses_gemv(M, K, N)) {
+        *path = 0;
+        return;
+    }
+    const int mode = bits == 4 ? (int)I4Geom(K, N, group_size).spc : 0;
+    const bool three = gemm_three_term(bits, mode);
+    *path = three ? 1 : 2;
+    *ks = gemm_plan(M, K, N, three ? gemm_tile(bits) : GemmTile{kBM, kBN, 2}, cus).KS;
 }
 
 namespace {
 template <int BITS>
 hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc, int mode,
                        int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, void* ws, hipStream_t s) {
-    // The three-term bf16 kernel folds the scale into A, so a tile's columns
-    // must share their scale: always for INT8 (256-column tiles), for INT4
-    // when a scale column spans a multiple of 16 strips (group a multiple of
-    // 128; 128-column tiles).  Other INT4 groups take the fp32-MFMA kernel.
-    const bool three = BITS == 8 || mode % 16 == 0;
+    // INT4 groups that are not a multiple of 128 take the fp32-MFMA kernel.
+    const bool three = gemm_three_term(BITS, mode);
     const GemmTile t = three ? gemm_tile(BITS) : GemmTile{kBM, kBN, 2};
-    const GemmPlan p = gemm_plan(M, K, N, t);
+    const GemmPlan p = gemm_plan(M, K, N, t, device_cus(s));
     float* part = p.KS > 1 ? (float*)ws : nullptr;
     const dim3 grid((unsigned)(ceil_div(M, t.bm) * ceil_div(N, t.bn) * p.KS));
     const bool k4 = x_aligned4(x, K);

@@ -11,6 +11,14 @@
 //     driver and retries, then throws std::runtime_error -- it never calls
 //     back into a locked accessor (the reference's OOM path deadlocks on its
 //     own mutex, src/allocator.cpp:37,95,184).
+//
+// Stream order: a freed device block is cached at once and may be handed to
+// the next allocate() while kernels that use it are still queued.  That is
+// safe because every launch of the host layer goes to the default stream, in
+// order, like the reference's CUDA path: work queued on the freed block runs
+// before any work queued later on its new owner.  A caller that launches on
+// other streams must synchronise them before freeing memory they use (the
+// same contract as the reference's pool, which also reuses without events).
 #pragma once
 
 #include <cstddef>

@@ -27,8 +27,7 @@ struct PackedWeight {
     std::shared_ptr<Storage> codes;  // GPU
     Tensor devscales;                // GPU (INT4 strip-major layout)
     Tensor scales_dev;               // GPU copy of the reference-layout scales
-    const void* qdata_key = nullptr;
-    const void* scales_key = nullptr;
+    uint64_t qdata_id = 0, scales_id = 0;  // TensorImpl ids of the qdata / scales it was built from
     uint64_t qdata_version = 0, scales_version = 0;
     bool valid = false;
 };

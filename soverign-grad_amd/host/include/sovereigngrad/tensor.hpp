@@ -7,6 +7,7 @@
 
 #include "sovereigngrad/allocator.hpp"
 
+#include <atomic>
 #include <cstdint>
 #include <initializer_list>
 #include <memory>
@@ -37,13 +38,19 @@ struct TensorImpl {
     Device device = Device::CPU;
     DType dtype = DType::Float32;
     bool requires_grad = false;
-    uint64_t version = 0;  // bumped by every in-place write (load_state_dict, copy_from)
+    // Bumped by every in-place write: copy_from (load_state_dict) and every
+    // mutable data() access through Tensor.  Atomic: forwards on several host
+    // threads read it while packing weights.
+    std::atomic<uint64_t> version{0};
+    // Unique for the life of the process (a new impl never reuses an old id,
+    // even at the same address), so caches can key on it.
+    const uint64_t id;
 
     TensorImpl(const std::vector<int64_t>& shape, Device device, bool requires_grad = false, bool zero_fill = true);
     float* data() { return storage ? static_cast<float*>(storage->ptr) : nullptr; }
     const float* data() const { return storage ? static_cast<const float*>(storage->ptr) : nullptr; }
     int64_t numel() const;
-    void bump_version() { ++version; }
+    void bump_version() { version.fetch_add(1, std::memory_order_acq_rel); }
 };
 
 class Tensor {
@@ -77,9 +84,17 @@ public:
     bool is_contiguous() const { return true; }
     bool is_defined() const { return impl != nullptr; }
     bool defined() const { return impl != nullptr; }
-    uint64_t version() const { return impl ? impl->version : 0; }
+    uint64_t version() const { return impl ? impl->version.load(std::memory_order_acquire) : 0; }
+    uint64_t id() const { return impl ? impl->id : 0; }
     bool requires_grad() const { return impl && impl->requires_grad; }
-    float* data() { return impl ? impl->data() : nullptr; }
+    // Mutable access counts as a write: it bumps the version, so a quantized
+    // layer whose qdata or scales are changed through it repacks its device
+    // weight on the next forward (the reference re-reads qdata every call).
+    float* data() {
+        if (!impl) return nullptr;
+        impl->bump_version();
+        return impl->data();
+    }
     const float* data() const { return impl ? impl->data() : nullptr; }
 
     Tensor to(Device device) const;

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <utility>
 #include <stdexcept>
 
 #include "hip_check.hpp"
@@ -20,8 +21,8 @@ RMSNorm::RMSNorm(int64_t d, float e, Device device) : eps(e) {
 Tensor RMSNorm::forward(const Tensor& x) {
     if (x.shape().size() < 2) throw std::runtime_error("RMSNorm requires at least 2D tensor!");  // ops.cpp:1533
     const int64_t D = x.shape().back();
-    Tensor xg = x.device() == Device::CUDA ? x : x.to(Device::CUDA);
-    Tensor wg = weight.device() == Device::CUDA ? weight : weight.to(Device::CUDA);
+    const Tensor xg = x.device() == Device::CUDA ? x : x.to(Device::CUDA);
+    const Tensor wg = weight.device() == Device::CUDA ? weight : weight.to(Device::CUDA);
     Tensor out = Tensor::empty(x.shape(), Device::CUDA);
     SG_SGQ_CHECK(sgq_rms_norm(xg.data(), xg.numel() / D, D, wg.data(), eps, out.data(), nullptr));
     return x.device() == Device::CUDA ? out : out.to(x.device());
@@ -122,7 +123,7 @@ Tensor QuantizedLLaMABlock::decode(const Tensor& x, KVCache& cache, const Decode
     if ((int64_t)pos.host().size() != B) throw std::runtime_error("decode: one position per sequence");
     const int64_t max_len = std::min(pos.max_len(), cache.max_tokens);
     auto gpu = [](const Tensor& t) { return t.device() == Device::CUDA ? t : t.to(Device::CUDA); };
-    Tensor xg = gpu(x);
+    const Tensor xg = gpu(x);
     const std::shared_ptr<nn::QuantizedLinear4Bit> lin[7] = {attn->q_proj, attn->k_proj, attn->v_proj, attn->out_proj,
                                                             mlp->w_gate, mlp->w_up, mlp->w_down};
     quantization::PackedHandle ph[7];
@@ -137,10 +138,10 @@ Tensor QuantizedLLaMABlock::decode(const Tensor& x, KVCache& cache, const Decode
         ph[i] = quantization::packed_weight(lin[i]->q_weight);
         if (!ph[i].devscales.defined()) throw std::runtime_error("decode: projection not in the tiled INT4 layout");
         if (lin[i]->bias.defined()) bias[i] = gpu(lin[i]->bias);
-        *fields[i] = sgq_int4_linear{ph[i].codes->ptr, ph[i].devscales.data(),
-                                     bias[i].defined() ? bias[i].data() : nullptr};
+        *fields[i] = sgq_int4_linear{ph[i].codes->ptr, std::as_const(ph[i].devscales).data(),
+                                     bias[i].defined() ? std::as_const(bias[i]).data() : nullptr};
     }
-    Tensor g1 = gpu(norm1->weight), g2 = gpu(norm2->weight);
+    const Tensor g1 = gpu(norm1->weight), g2 = gpu(norm2->weight);
     blk.D = embed_dim;
     blk.H = hidden_dim;
     blk.group_size = group_size;

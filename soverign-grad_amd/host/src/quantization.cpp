@@ -43,8 +43,8 @@ int int8_branch(const QuantizedTensor& q) {
 }
 
 void record(PackedWeight& p, const QuantizedTensor& q) {
-    p.qdata_key = q.qdata.impl.get();
-    p.scales_key = q.scales.impl.get();
+    p.qdata_id = q.qdata.id();
+    p.scales_id = q.scales.id();
     p.qdata_version = q.qdata.version();
     p.scales_version = q.scales.version();
     p.valid = true;
@@ -66,12 +66,12 @@ PackedView packed_of(const QuantizedTensor& q) {
     if (!q.packed) throw std::runtime_error("QuantizedTensor has no packed state");
     PackedWeight& p = *q.packed;
     std::lock_guard<std::mutex> lock(p.mu);
-    if (p.valid && p.qdata_key == q.qdata.impl.get() && p.scales_key == q.scales.impl.get() &&
+    if (p.valid && p.qdata_id == q.qdata.id() && p.scales_id == q.scales.id() &&
         p.qdata_version == q.qdata.version() && p.scales_version == q.scales.version())
         return view_of(p);
     if (!q.qdata.defined() || !q.scales.defined()) throw std::runtime_error("QuantizedTensor is empty");
     const View2D v = view2d(q.original_shape);
-    Tensor qg = on_gpu(q.qdata);
+    const Tensor qg = on_gpu(q.qdata);
     Tensor sg = on_gpu(q.scales).clone();
     std::shared_ptr<Storage> ws;
     if (q.bits == 8) {
@@ -122,7 +122,7 @@ QuantizedTensor quantize_int8(const Tensor& x, QuantizationScheme scheme) {
                         : SGQ_PER_CHANNEL_SYMMETRIC;
     if (eff == SGQ_PER_CHANNEL_SYMMETRIC && v.rows == 0)
         throw std::runtime_error("quantize_int8: per-channel quantization of a tensor with no rows");
-    Tensor xg = on_gpu(x);
+    const Tensor xg = on_gpu(x);
     QuantizedTensor r;
     r.original_shape = x.shape();
     r.scheme = scheme;
@@ -147,7 +147,7 @@ QuantizedTensor quantize_int8(const Tensor& x, QuantizationScheme scheme) {
 QuantizedTensor quantize_int4(const Tensor& x, int64_t group_size) {
     if (group_size <= 0) group_size = 32;  // src/quantization.cpp:118
     const View2D v = view2d(x.shape());
-    Tensor xg = on_gpu(x);
+    const Tensor xg = on_gpu(x);
     QuantizedTensor r;
     r.original_shape = x.shape();
     r.scheme = QuantizationScheme::GroupedAsymmetric;
@@ -176,8 +176,8 @@ QuantizedTensor quantize_int4(const Tensor& x, int64_t group_size) {
 namespace {
 Tensor dequantize_codes(const QuantizedTensor& qx, int bits, int branch) {
     const View2D v = view2d(qx.original_shape);
-    Tensor qg = on_gpu(qx.qdata);
-    Tensor sg = on_gpu(qx.scales);
+    const Tensor qg = on_gpu(qx.qdata);
+    const Tensor sg = on_gpu(qx.scales);
     Tensor out = Tensor::empty(qx.original_shape, Device::CUDA);
     SG_SGQ_CHECK(sgq_dequantize_codes(qg.data(), sg.data(), bits, branch, v.rows, v.cols, qx.group_size, out.data(),
                                       nullptr));
@@ -193,15 +193,16 @@ Tensor quantized_matmul_int8(const Tensor& x, const QuantizedTensor& q_weight, c
     View2D v{};
     check_linear_args(x, q_weight, bias, v);
     const PackedView p = packed_of(q_weight);
-    Tensor xg = on_gpu(x);
-    Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
+    const Tensor xg = on_gpu(x);
+    const Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
     const int64_t M = x.shape()[0];
     Tensor y = Tensor::empty({M, v.cols}, Device::CUDA);
     // The workspace the library asks for (none for the current kernels), from
     // the device pool; stream order keeps a later reuse behind this launch.
     const int64_t wsb = sgq_linear_workspace_bytes(8, M, v.rows, v.cols);
     const std::shared_ptr<Storage> ws = wsb > 0 ? gpu_bytes(wsb) : nullptr;
-    SG_SGQ_CHECK(sgq_linear_int8(xg.data(), M, v.rows, v.cols, p.codes->ptr, p.scales_dev.data(), int8_branch(q_weight),
+    SG_SGQ_CHECK(sgq_linear_int8(xg.data(), M, v.rows, v.cols, p.codes->ptr, std::as_const(p.scales_dev).data(),
+                                 int8_branch(q_weight),
                                  bg.defined() ? bg.data() : nullptr, y.data(), ws ? ws->ptr : nullptr, wsb, nullptr));
     return to_device(y, x.device());
 }
@@ -210,14 +211,15 @@ Tensor quantized_matmul_int4(const Tensor& x, const QuantizedTensor& q_weight, c
     View2D v{};
     check_linear_args(x, q_weight, bias, v);
     const PackedView p = packed_of(q_weight);
-    Tensor xg = on_gpu(x);
-    Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
+    const Tensor xg = on_gpu(x);
+    const Tensor bg = bias.defined() ? on_gpu(bias) : Tensor();
     const int64_t M = x.shape()[0];
     Tensor y = Tensor::empty({M, v.cols}, Device::CUDA);
     const int64_t wsb = sgq_linear_workspace_bytes(4, M, v.rows, v.cols);
     const std::shared_ptr<Storage> ws = wsb > 0 ? gpu_bytes(wsb) : nullptr;
-    SG_SGQ_CHECK(sgq_linear_int4(xg.data(), M, v.rows, v.cols, p.codes->ptr, p.scales_dev.data(),
-                                 p.devscales.defined() ? p.devscales.data() : nullptr, q_weight.group_size,
+    SG_SGQ_CHECK(sgq_linear_int4(xg.data(), M, v.rows, v.cols, p.codes->ptr, std::as_const(p.scales_dev).data(),
+                                 p.devscales.defined() ? std::as_const(p.devscales).data() : nullptr,
+                                 q_weight.group_size,
                                  bg.defined() ? bg.data() : nullptr, y.data(), ws ? ws->ptr : nullptr, wsb, nullptr));
     return to_device(y, x.device());
 }

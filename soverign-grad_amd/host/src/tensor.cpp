@@ -46,8 +46,12 @@ Storage::Storage(size_t bytes, Device dev, bool zero_fill) : size(bytes), device
 
 Storage::~Storage() { MemoryAllocator::instance().free(ptr, device); }
 
+namespace {
+std::atomic<uint64_t> g_next_impl_id{1};
+}  // namespace
+
 TensorImpl::TensorImpl(const std::vector<int64_t>& shp, Device dev, bool req, bool zero_fill)
-    : shape(shp), device(dev), requires_grad(req) {
+    : shape(shp), device(dev), requires_grad(req), id(g_next_impl_id.fetch_add(1, std::memory_order_relaxed)) {
     storage = std::make_shared<Storage>(static_cast<size_t>(compute_numel(shp)) * sizeof(float), dev, zero_fill);
 }
 
@@ -141,8 +145,8 @@ Tensor Tensor::clone() const {
 void Tensor::copy_from(const Tensor& src) {
     if (!impl || !src.impl) throw std::runtime_error("copy_from on an undefined tensor");
     if (src.numel() != numel()) throw std::runtime_error("copy_from: element counts differ");
-    copy_bytes(data(), impl->device, src.data(), src.device(), (size_t)numel() * sizeof(float));
-    impl->bump_version();
+    copy_bytes(impl->data(), impl->device, src.data(), src.device(), (size_t)numel() * sizeof(float));
+    impl->bump_version();  // one write, one version
 }
 
 Tensor Tensor::matmul(const Tensor& other) const {

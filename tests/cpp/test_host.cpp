@@ -17,6 +17,9 @@
 #include <iostream>
 #include <string>
 #include <thread>
+#include <utility>
+
+#include <hip/hip_runtime_api.h>
 #include <vector>
 
 #include "sovereigngrad/allocator.hpp"
@@ -31,6 +34,11 @@ using namespace sovereigngrad;
 using quantization::QuantizationScheme;
 
 static int g_failures = 0;
+
+#define SG_TEST_HIP(call)                                                               \
+    do {                                                                                \
+        if ((call) != hipSuccess) throw std::runtime_error("HIP call failed: " #call);  \
+    } while (0)
 
 #define CHECK(cond)                                                                          \
     do {                                                                                     \
@@ -669,6 +677,64 @@ static void test_reference_checkpoints_forward(const std::string& dir, const std
               << ": " << (worst <= 1e-5 ? "PASSED" : "FAILED") << "\n";
 }
 
+// Writes through Tensor::data() reach the next forward: mutable access counts
+// as a write, so the packed device weight is rebuilt (the reference re-reads
+// qdata and scales on every call, src/quantization.cpp:189-206).  Replacing a
+// tensor by a new one is seen by its impl id even if the address is reused.
+static void test_packed_cache_invalidation() {
+    std::cout << "--- packed weight follows qdata/scales writes\n";
+    Tensor::manual_seed(31);
+    for (Device dev : {Device::CPU, Device::CUDA}) {
+        nn::QuantizedLinear4Bit m(64, 48, 16, dev);
+        Tensor x = Tensor::randn({3, 64}, 0.0f, 1.0f, dev);
+        const auto y0 = host(m.forward(x));
+        // Double every scale through data(): every output doubles (exactly: a
+        // power-of-two factor on each product and sum).
+        {
+            Tensor s = m.q_weight.scales.cpu();
+            float* p = s.data();
+            for (int64_t i = 0; i < s.numel(); ++i) p[i] *= 2.0f;
+            if (dev == Device::CPU) {
+                float* d = m.q_weight.scales.data();
+                std::memcpy(d, p, sizeof(float) * (size_t)s.numel());
+            } else {
+                SG_TEST_HIP(hipMemcpy(m.q_weight.scales.data(), p, sizeof(float) * (size_t)s.numel(),
+                                      hipMemcpyHostToDevice));
+            }
+        }
+        const auto y1 = host(m.forward(x));
+        bool doubled = true;
+        for (size_t i = 0; i < y0.size(); ++i) doubled = doubled && y1[i] == 2.0f * y0[i];
+        CHECK(doubled);
+        // Negate the codes through data(): every output flips sign.
+        {
+            Tensor q = m.q_weight.qdata.cpu();
+            float* p = q.data();
+            for (int64_t i = 0; i < q.numel(); ++i) p[i] = -p[i];
+            if (dev == Device::CPU)
+                std::memcpy(m.q_weight.qdata.data(), p, sizeof(float) * (size_t)q.numel());
+            else
+                SG_TEST_HIP(hipMemcpy(m.q_weight.qdata.data(), p, sizeof(float) * (size_t)q.numel(),
+                                      hipMemcpyHostToDevice));
+        }
+        const auto y2 = host(m.forward(x));
+        bool flipped = true;
+        for (size_t i = 0; i < y0.size(); ++i) flipped = flipped && y2[i] == -y1[i];
+        CHECK(flipped);
+        // A replaced scales tensor (new impl, maybe at a recycled address) is seen.
+        m.q_weight.scales = m.q_weight.scales.clone();
+        m.q_weight.scales.copy_from(Tensor::ones({m.q_weight.scales.numel()}));
+        const auto y3 = host(m.forward(x));
+        CHECK(!same_bits(y3, y2));
+        // Reads do not invalidate: a const read leaves the version alone.
+        const uint64_t v = m.q_weight.qdata.version();
+        (void)std::as_const(m.q_weight.qdata).data();
+        (void)host(m.forward(x));
+        CHECK(m.q_weight.qdata.version() == v);
+    }
+    std::cout << "  * writes through data() and replaced tensors reach the forward (CPU and CUDA modules): PASSED\n";
+}
+
 static void test_module_to_device() {
     std::cout << "--- Module::to\n";
     Tensor::manual_seed(5);
@@ -852,6 +918,7 @@ int main(int argc, char** argv) {
                  {"quantization_cuda", [] { test_quantization(Device::CUDA); }},
                  {"forward_composition", test_forward_matches_composition},
                  {"persistence_bridge", test_persistence_bridge},
+                 {"packed_cache_invalidation", test_packed_cache_invalidation},
                  {"module_to_device", test_module_to_device},
                  {"concurrent_forward", test_concurrent_forward},
                  {"llama_block_decode", test_llama_block_decode}};

@@ -181,6 +181,30 @@ def test_argument_errors_before_gpu(lib, sgq):
     assert lib.sgq_linear_int8(None, 0, 4, 4, None, None, 0, None, None, None, 0, None) == 0
 
 
+def test_dequantize_alignment_checked_before_gpu(lib):
+    # The unpack kernels read packed codes 16 bytes at a time (tiled layouts).
+    assert lib.sgq_dequantize_int8(24, 16, 0, 64, 64, 16, None) == 1
+    assert b"aligned" in lib.sgq_last_error()
+    assert lib.sgq_dequantize_int4(24, 16, 64, 64, 32, 16, None) == 1  # tiled: N % 8 == 0, G % 8 == 0
+    assert b"aligned" in lib.sgq_last_error()
+
+
+def test_forward_refuses_k_past_32bit_offsets(lib):
+    """K long enough that the kernels' 32-bit buffer offsets would wrap is
+    refused (SGQ_ERR_UNSUPPORTED) before any launch: past 2^22 rows for the
+    MFMA GEMM (128-row tiles of x), past 2^29 rows for the GEMV."""
+    big_gemm = (1 << 22) + 16  # GEMM path at M=32 (M * K * N > 2^29)
+    assert lib.sgq_linear_int8(16, 32, big_gemm, 64, 16, 16, 0, None, 16, 16, 1 << 40, None) == 2
+    assert b"too long" in lib.sgq_last_error()
+    assert lib.sgq_linear_int4(16, 32, big_gemm, 64, 16, 16, 16, 128, None, 16, 16, 1 << 40, None) == 2
+    big_gemv = (1 << 29)  # GEMV path at M=1
+    assert lib.sgq_linear_int8(16, 1, big_gemv, 8, 16, 16, 0, None, 16, None, 0, None) == 2
+    assert lib.sgq_linear_int4(16, 1, big_gemv, 8, 16, 16, 16, 128, None, 16, None, 0, None) == 2
+    assert lib.sgq_swiglu_int8(16, 1, big_gemv, 8, 16, 16, None, 16, 16, None, 0, 16, 16, 1 << 40, None) == 2
+    assert lib.sgq_swiglu_int4(16, 1, big_gemv, 8, 16, 16, 16, None, 16, 16, 16, None, 128, 16, 16, 1 << 40,
+                               None) == 2
+
+
 # ---- numpy layout models -------------------------------------------------
 
 def _unpack_model_i8(buf, K, N):
@@ -224,3 +248,37 @@ def test_model_devscales():
     assert g["spc"] == 1
     # strip 1 of row 2 covers elements 2*24+8 .. +7 -> group (56)//8 = 7
     assert ds[1, 2] == s[7]
+
+
+def _plan(lib, bits, M, K, N, G, cus):
+    path, ks = ctypes.c_int(-1), ctypes.c_int(-1)
+    assert lib.sgq_linear_plan(bits, M, K, N, G, cus, ctypes.byref(path), ctypes.byref(ks)) == 0
+    return path.value, ks.value
+
+
+def test_plan_follows_the_device_cu_count(lib):
+    """The launch plan takes the CU count of the device (a partitioned MI355X
+    reports fewer than 256): fewer CUs never mean more K splits, so the
+    workspace sized for 256 CUs covers every device."""
+    shapes = [(8, 128, 1024, 1024, 0), (8, 512, 4096, 4096, 0), (8, 256, 4096, 1024, 0), (4, 256, 4096, 1024, 128),
+              (4, 300, 2048, 640, 32), (8, 2048, 4096, 4096, 0), (4, 64, 11008, 4096, 128), (8, 17, 8192, 512, 0)]
+    for bits, M, K, N, G in shapes:
+        ws = lib.sgq_linear_workspace_bytes(bits, M, K, N)
+        prev = None
+        for cus in (256, 128, 80, 64, 32, 8, 1):
+            path, ks = _plan(lib, bits, M, K, N, G, cus)
+            assert ks >= 1
+            if path in (1, 2) and ks > 1:
+                assert ws >= ks * M * N * 4, (bits, M, K, N, cus)
+            if prev is not None:
+                assert ks <= prev, (bits, M, K, N, cus, ks, prev)
+            prev = ks
+    # C4 fills any device without splitting K; a small GEMM splits less on a partition.
+    assert _plan(lib, 8, 2048, 4096, 4096, 0, 256) == (1, 1)
+    assert _plan(lib, 8, 256, 4096, 1024, 0, 256)[1] > _plan(lib, 8, 256, 4096, 1024, 0, 32)[1]
+    assert _plan(lib, 4, 1, 4096, 4096, 128, 256) == (0, 1)  # decode: the GEMV
+    assert _plan(lib, 4, 300, 2048, 640, 32, 256)[0] == 2  # group 32: the fp32 MFMA kernel
+    assert _plan(lib, 4, 300, 2048, 644, 32, 256)[0] == 3  # N % 8 != 0: flat layout
+    # A CU count above the full chip is planned as the full chip.
+    assert _plan(lib, 8, 256, 4096, 1024, 0, 1024) == _plan(lib, 8, 256, 4096, 1024, 0, 256)
+    assert lib.sgq_linear_plan(8, 1, 4, 4, 0, -1, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == 1

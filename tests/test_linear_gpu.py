@@ -84,6 +84,8 @@ def _case(sgq, dev, oracle, synth, bits_, M, K, N, G=128, scheme=0, bias=False, 
         ("C3_gate_M8", 4, 8, 4096, 11008, 128, 0, False, 2),
         ("C3_gate_M16", 4, 16, 4096, 11008, 128, 0, False, 2),
         ("C3_down_M1", 4, 1, 11008, 4096, 128, 0, False, 2),
+        ("C3_down_M4", 4, 4, 11008, 4096, 128, 0, False, 2),
+        ("C3_down_M8", 4, 8, 11008, 4096, 128, 0, False, 2),
         ("C3_down_M16", 4, 16, 11008, 4096, 128, 0, False, 2),
         ("C5_qkv_M8", 4, 8, 2048, 6144, 128, 0, False, 4),
         ("C5_o_M8", 4, 8, 2048, 2048, 128, 0, False, 4),
@@ -104,6 +106,50 @@ def test_config4_gemm_rows(sgq, dev, oracle, synth):
     rows = np.r_[0:16, 1000:1016, 2032:2048]
     print("  case C4_int8_pt_M2048 (48 rows vs oracle)", flush=True)
     y, yref = _case(sgq, dev, oracle, synth, 8, M, 4096, 4096, 0, 0, False, 3, rows=rows)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
+def test_config4_gemm_all_rows_vs_fp64(sgq, dev, oracle, synth):
+    """C4 in full: all 2048 rows of the M=2048 INT8 per-tensor GEMM within 1e-5
+    of an fp64 product of x with the reference's fp32 weights q * s (beside the
+    48-row oracle check above)."""
+    M, K, N = 2048, 4096, 4096
+    W = synth.normal((K, N), synth.config_seed(3), synth.STREAM_W, 0.0, 0.02)
+    x = synth.normal((M, K), synth.config_seed(3), synth.STREAM_X, 0.0, 1.0)
+    print("  case C4_int8_pt_M2048 (all rows vs fp64)", flush=True)
+    qw = sgq.quantize_int8(_to_dev(W, dev), 0)
+    y = _np(sgq.quantized_matmul_int8(_to_dev(x, dev), qw))
+    q, s = oracle.quantize_int8(W, 0)
+    w32 = oracle.dequantize_int8(q, s, 0)
+    y64 = x.astype(np.float64) @ np.asarray(w32, np.float64)
+    e = rel_err(y, y64)
+    print(f"    rel_err vs fp64 over {M} rows: {e:.3e}", flush=True)
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (11008, 4096), (4096, 11008)])
+@pytest.mark.parametrize("kind", ["abs", "silu"])
+def test_same_sign_activations(sgq, dev, oracle, synth, M, K, N, kind):
+    """The one- and two-row INT4 GEMV accumulates offset-binary codes u = q + 8
+    and subtracts 8 * sum(x * s) per lane.  With activations of one sign (|x|,
+    or silu outputs, as the down projection sees them) at long K, that
+    correction is as large as it gets; the result must still be within 1e-5 of
+    the reference's dequantize-then-matmul."""
+    W = synth.normal((K, N), synth.config_seed(40), synth.STREAM_W, 0.0, 0.02)
+    z = synth.normal((M, K), synth.config_seed(40), synth.STREAM_X, 0.0, 1.0)
+    if kind == "abs":
+        x = np.abs(z).astype(np.float32)
+    else:
+        zz = (2.0 * z).astype(np.float32)
+        x = (zz / (np.float32(1.0) + np.exp(-zz))).astype(np.float32)
+    print(f"  case M={M} K={K} N={N} x={kind}", flush=True)
+    qw = sgq.quantize_int4(_to_dev(W, dev), 128)
+    y = _np(sgq.quantized_matmul_int4(_to_dev(x, dev), qw))
+    q, s = oracle.quantize_int4(W, 128)
+    yref = oracle.quantized_matmul_int4(x, q, s, 128)
     e = rel_err(y, yref)
     print(f"    rel_err={e:.3e}", flush=True)
     assert e <= TOL
