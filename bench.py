@@ -166,20 +166,30 @@ class Case:
         return s.elapsed_time(e) / steps  # ms per step
 
     def time_graph(self, steps: int, warmup: int, extra_replays: int = 0) -> float:
-        """K launches captured into one hipGraph, replayed once in the timed region.
-        extra_replays > 0 replays it that many more times afterwards (untimed by
-        the contract) and keeps their per-call times in self.replay_ms."""
+        """K launches captured into one hipGraph (call i on weight copy i % C),
+        replayed once in the timed region.  Before every timed replay an
+        untimed sweep graph runs one call on each of the C copies in order, so
+        that whatever K is, each timed call's weights were last touched at
+        least C calls (more than the 256 MB Infinity Cache) earlier and stream
+        from HBM.  extra_replays > 0 replays it that many more times afterwards
+        (untimed by the contract) and keeps their per-call times in
+        self.replay_ms."""
         import torch
 
         for i in range(warmup):
             self.launch(i)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
         cap = torch.cuda.Stream(self.dev)
+        g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=cap):
             for i in range(steps):
                 self.launch(i)
-        g.replay()  # untimed: first replay uploads the graph
+        sweep = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(sweep, stream=cap):
+            for i in range(len(self.packed)):
+                self.launch(i)
+        g.replay()  # untimed: first replays upload the graphs
+        sweep.replay()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
@@ -189,11 +199,13 @@ class Case:
         ms = s.elapsed_time(e) / steps
         self.replay_ms = []
         for _ in range(extra_replays):
+            sweep.replay()
             s.record()
             g.replay()
             e.record()
             torch.cuda.synchronize()
             self.replay_ms.append(s.elapsed_time(e) / steps)
+        del sweep
         return ms
 
     def check(self, oracle, rows=None) -> float:
@@ -234,6 +246,78 @@ def measured_traffic(config: str):
     if not path.exists():
         return None
     return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline lines."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _ref_forward_ms(ref, c, x, q, s, b, budget_s: float, max_reps: int = 50):
+    """Median ms of the reference forward on this host: one untimed warm-up
+    call, then as many calls as fit in budget_s (at least 3, at most
+    max_reps).  Returns (median ms, calls timed)."""
+    first, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, 1)
+    reps = int(max(3, min(max_reps, budget_s / max(first[0], 1e-6))))
+    secs, _ = ref.time_quantized_matmul(c["bits"], x, q, s, c["scheme"], c["G"], b, reps)
+    return statistics.median(secs) * 1e3, reps
+
+
+CPU_OTHER = ["c1", "c3_gate_m1", "c3_gate_m16", "c3_down_m1", "c3_down_m16", "c4"]
+
+
+def cpu_baseline_others(budget_s: float):
+    """The reference's CPU forward on the other BASELINE configs (C1, C3 at M=1
+    and 16, C4) and one C5 decode step, each on a bounded sample: the median
+    of the calls that fit in budget_s per config (at least 3).  C5's 110 calls
+    are 22 layers of the same five shapes, so one layer's five calls are timed
+    and the step is 22 times their sum.  None when oracle/_ref is absent."""
+    from oracle.oracle import Oracle, Reference, reference_available
+    from soverign_grad_amd import synth
+
+    if not reference_available():
+        return None
+    ref, orc = Reference(), Oracle()
+    threads, model = ref.omp_max_threads(), cpu_model()
+    out = {}
+    for key in CPU_OTHER:
+        c = CONFIGS[key]
+        seed = synth.config_seed(c["seed"])
+        W = synth_normal((c["K"], c["N"]), seed, synth.STREAM_W, 0.0, 0.02)
+        x = synth_normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
+        b = synth_normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
+        q, sc = orc.quantize_int4(W, c["G"]) if c["bits"] == 4 else orc.quantize_int8(W, c["scheme"])
+        ms, reps = _ref_forward_ms(ref, c, x, q, sc, b, budget_s)
+        out[key] = {"workload": c["name"], "ms_per_call": round(ms, 3), "calls_timed": reps,
+                    "GB_s": round(alg_bytes(c) / ms / 1e6, 3), "TFLOP_s": round(alg_flops(c) / ms / 1e9, 4),
+                    "threads": threads, "cpu": model, "kind": "reference"}
+        log(f"[bench] cpu {key}: {ms:.2f} ms/call over {reps} calls")
+    seed = synth.config_seed(4)
+    layer_ms, calls = 0.0, 0
+    for i, (name, K, N) in enumerate(C5_MATS):
+        c = dict(bits=4, M=C5_M, K=K, N=N, G=C5_G, scheme=2, bias=False)
+        W = synth.normal((K, N), seed, 3 * i + synth.STREAM_W, 0.0, 0.02)
+        x = synth.normal((C5_M, K), seed, 3 * i + synth.STREAM_X, 0.0, 1.0)
+        q, sc = orc.quantize_int4(W, C5_G)
+        ms, reps = _ref_forward_ms(ref, c, x, q, sc, None, budget_s / len(C5_MATS))
+        layer_ms += ms
+        calls += reps
+    step_ms = C5_LAYERS * layer_ms
+    nbytes = C5_LAYERS * sum(K * N // 2 + 4 * (K * N // C5_G) + 4 * C5_M * (K + N) for _, K, N in C5_MATS)
+    flops = C5_LAYERS * sum(2 * C5_M * K * N for _, K, N in C5_MATS)
+    out["c5"] = {"workload": "C5: one NanoLLaMA decode step (110 INT4 g128 QuantizedLinear calls, M=8)",
+                 "ms_per_step": round(step_ms, 3),
+                 "sample": f"one layer's 5 calls timed ({calls} calls in all, median per shape), step = 22 x layer",
+                 "GB_s": round(nbytes / step_ms / 1e6, 3), "TFLOP_s": round(flops / step_ms / 1e9, 4),
+                 "threads": threads, "cpu": model, "kind": "reference"}
+    log(f"[bench] cpu c5: {step_ms:.1f} ms/step")
+    return out
 
 
 def cpu_baseline(c, budget_s: float):
@@ -290,13 +374,19 @@ def cpu_baseline(c, budget_s: float):
         "cores": cores,
         "kind": kind,
         "sample": f"{c['name']}: {len(secs)} forward calls, median {med * 1e3:.2f} ms "
-                  f"(dequantize + blocked AVX2 matmul + bias), host {platform.processor() or platform.machine()}, "
+                  f"(dequantize + blocked AVX2 matmul + bias), {cores} OpenMP threads on {cpu_model()}, "
                   f"nproc={os.cpu_count()}",
+        "cpu": cpu_model(),
         "tflops": round(alg_flops(c) / med / 1e12, 4),
         "phases_ms": phases,
         "one_thread": one_thread,
     }
 
+
+# Graph sizes of the secondary legs, fixed whatever --steps is (the timed
+# region of the headline line is exactly --steps calls).
+OTHER_STEPS = 200  # forward calls per C1/C3 graph
+DECODE_STEPS = 10  # decode steps per C5 graph (110 or 88 calls each)
 
 OTHER_CONFIGS = ["c1", "c3_gate_m1", "c3_gate_m4", "c3_gate_m8", "c3_gate_m16", "c3_down_m1", "c3_down_m4",
                  "c3_down_m8", "c3_down_m16"]
@@ -640,7 +730,7 @@ def main() -> int:
         # A graph of back-to-back calls after a warm-up, replayed five times:
         # the median per-call time (single short eager bursts ran before the
         # clocks had settled and read up to 25% slow).
-        n4 = max(5, min(50, args.steps // 40))
+        n4 = 50  # a fixed graph whatever --steps is (the leg is compute-bound: its weights fit the caches)
         first4 = case4.time_graph(n4, 10, extra_replays=4)
         reps4 = sorted([first4] + case4.replay_ms)
         ms4 = statistics.median(reps4)
@@ -670,7 +760,7 @@ def main() -> int:
         oracle = Oracle()
         others = {}
         for key in OTHER_CONFIGS:
-            others[key] = other_config(pkg, key, dev, oracle, max(20, min(400, args.steps // 5)))
+            others[key] = other_config(pkg, key, dev, oracle, OTHER_STEPS)
             log(f"[bench] {key}: {others[key]['us_per_call']} us/call, {others[key]['GB_s']} GB/s, "
                 f"{others[key]['TFLOP_s']} TFLOP/s, rel_err {others[key]['rel_err_vs_oracle']:.2e}")
             if others[key]["rel_err_vs_oracle"] > 1e-5:
@@ -678,7 +768,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         for M in (1, 8):
             key = f"c3_swiglu_m{M}"
-            others[key] = swiglu_pair(pkg, dev, oracle, max(20, min(400, args.steps // 5)), M)
+            others[key] = swiglu_pair(pkg, dev, oracle, OTHER_STEPS, M)
             log(f"[bench] {key}: {others[key]['us_per_call']} us/call, {others[key]['GB_s']} GB/s, "
                 f"rel_err {others[key]['rel_err_vs_oracle']:.2e}")
             if others[key]["rel_err_vs_oracle"] > 1e-5:
@@ -686,14 +776,14 @@ def main() -> int:
             torch.cuda.empty_cache()
         for ctx_len in (128, 1024):
             key = f"c5_block_decode_ctx{ctx_len}"
-            others[key] = block_decode_step(pkg, dev, oracle, max(2, min(10, args.steps // 200)), ctx_len)
+            others[key] = block_decode_step(pkg, dev, oracle, DECODE_STEPS, ctx_len)
             log(f"[bench] {key}: {others[key]['us_per_step']} us/step, {others[key]['tokens_per_s']} tok/s, "
                 f"rel_err {others[key]['rel_err_vs_oracle']:.2e}")
             if others[key]["rel_err_vs_oracle"] > 1e-5:
                 raise SystemExit(f"parity failure in bench ({key})")
             torch.cuda.empty_cache()
         for key, fused in (("c5", False), ("c5_fused_swiglu", True)):
-            others[key] = decode_step(pkg, dev, oracle, max(2, min(20, args.steps // 100)), fused)
+            others[key] = decode_step(pkg, dev, oracle, DECODE_STEPS, fused)
             log(f"[bench] {key}: {others[key]['us_per_step']} us/step, rel_err {others[key]['rel_err_vs_oracle']:.2e}")
             if others[key]["rel_err_vs_oracle"] > 1e-5:
                 raise SystemExit(f"parity failure in bench ({key})")
@@ -704,6 +794,10 @@ def main() -> int:
         t0 = time.time()
         out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget)
         log(f"[bench] cpu baseline {out['cpu_baseline']['value']} GB/s in {time.time() - t0:.1f}s")
+        if not args.no_others and args.config == "c2":
+            t0 = time.time()
+            out["cpu_baseline"]["other_configs"] = cpu_baseline_others(args.cpu_budget / 4)
+            log(f"[bench] cpu baselines of the other configs in {time.time() - t0:.1f}s")
     print(json.dumps(out), flush=True)
     return 0
 
