@@ -203,6 +203,21 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
                     const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* sgq_linear_int4 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * allocates nothing: the split-K partials of the GEMM go to a static device
+ * array of 32 MiB per GPU (created when the library is loaded on that GPU
+ * and held until the process ends).  Shapes whose sgq_linear_workspace_bytes
+ * exceeds 32 MiB are refused with SGQ_ERR_UNSUPPORTED.  The stream must
+ * belong to the calling thread's current device.  Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (two
+ * streams, two threads) race and must be serialised by the caller; calls in
+ * order on one stream are safe.  Same results as sgq_linear_int4 (the same
+ * kernels and plan). */
+int sgq_linear_int4_noalloc(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                            const float* devscales, int64_t group_size, const float* bias, float* y, void* stream);
+
 /* ---- gated MLP (caller-side fusion) ----------------------------------- */
 
 /* Replaces the first three lines of nn::SwiGLU::forward

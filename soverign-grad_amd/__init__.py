@@ -64,6 +64,7 @@ SIGNATURES = {
     "sgq_dequantize_codes": (_int, [_vp, _vp, _int, _int, _i64, _i64, _i64, _vp, _vp]),
     "sgq_linear_int8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _int, _vp, _vp, _vp, _i64, _vp]),
     "sgq_linear_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "sgq_linear_int4_noalloc": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp]),
     "sgq_swiglu_workspace_bytes": (_i64, [_int, _i64, _i64, _i64, _i64]),
     "sgq_swiglu_int8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp, _vp, _i64, _vp]),
     "sgq_swiglu_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64,

@@ -1,14 +1,17 @@
 // sgq_abi.hip -- the extern "C" entry points of libsgq.so (declared in include/sgq.h).
 //
 // Every function validates its arguments on the host, then enqueues kernels
-// on the caller's stream.  No allocation, no global mutable state; the only
-// per-thread state is the last error message.
+// on the caller's stream.  No allocation; the only per-thread state is the
+// last error message.  The one piece of process state is the per-device
+// address of the static scratch array used by sgq_linear_int4_noalloc
+// (written once per device).
 #include "sgq.h"
 #include "sgq_internal.h"
 
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 
 #define SGQ_ABI_VERSION 1
 
@@ -149,6 +152,86 @@ int check_codes_flag(const int* dflag, hipStream_t s) {
     SGQ_HIP(hipMemcpyAsync(&host_flag, dflag, sizeof(int), hipMemcpyDeviceToHost, s), "hipMemcpyAsync(flag)");
     SGQ_HIP(hipStreamSynchronize(s), "hipStreamSynchronize");
     if (host_flag) return fail(SGQ_ERR_CODES, "qdata holds a value that is not an integer code in range");
+    return ok();
+}
+
+
+// ---- static scratch of sgq_linear_int4_noalloc ------------------------------
+// The split-K partials of the no-allocation forward live in this array: one
+// copy per GPU, created when the library's code object is loaded on that GPU
+// and held until the process ends.  Host code never uses the array's name as
+// an address (on the host it is a stand-in symbol); the device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+constexpr int64_t kScratchBytes = (int64_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_status[kScratchDevices];
+
+// The scratch address on the device `stream` runs on, which must be the
+// calling thread's current device (the symbol is resolved with it current).
+int scratch_for_stream(const char* fn, hipStream_t stream, void** out) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(SGQ_ERR_HIP, "%s: no current device", fn);
+    }
+    if (stream) {
+        int sdev = cur;
+        if (hipStreamGetDevice(stream, &sdev) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: cannot query the stream's device", fn);
+        }
+        if (sdev != cur)
+            return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: the stream's device (%d) is not the current device (%d)", fn,
+                        sdev, cur);
+    }
+    if (cur < 0 || cur >= kScratchDevices) return fail(SGQ_ERR_UNSUPPORTED, "%s: device %d out of range", fn, cur);
+    std::call_once(g_scratch_once[cur], [cur] {
+        void* p = nullptr;
+        g_scratch_status[cur] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (g_scratch_status[cur] != hipSuccess) (void)hipGetLastError();
+        g_scratch_ptr[cur] = p;
+    });
+    if (g_scratch_status[cur] != hipSuccess || !g_scratch_ptr[cur])
+        return fail(SGQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(g_scratch_status[cur]));
+    *out = g_scratch_ptr[cur];
+    return SGQ_OK;
+}
+
+int linear_int4(const char* fn, const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad shape", fn);
+    if (M == 0 || N == 0) return ok();
+    if (!y) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null output", fn);
+    if (K == 0) {
+        SGQ_HIP(launch_fill_bias(y, M, N, bias, s), "fill_bias");
+        return ok();
+    }
+    const I4Geom g(K, N, group_size);
+    if (!x || !packed) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null pointer", fn);
+    if (!g.tiled) {
+        if (!scales) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: flat layout needs scales", fn);
+        SGQ_HIP(launch_linear_i4_flat(x, M, K, N, packed, scales, g.G, bias, y, s), "linear_i4_flat");
+        return ok();
+    }
+    if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: tiled layout needs devscales", fn);
+    if (!aligned16(packed) || !aligned16(devscales))
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
+    if (!forward_fits(4, M, K, N, g.G))
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
+    if (linear_uses_gemv(M, K, N)) {
+        SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
+    } else {
+        const int st = check_linear_ws(fn, M, K, N, workspace, workspace_bytes);
+        if (st != SGQ_OK) return st;
+        SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
+    }
     return ok();
 }
 
@@ -430,35 +513,25 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
 int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
                     int64_t workspace_bytes, void* stream) {
-    hipStream_t s = (hipStream_t)stream;
-    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N))
-        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: bad shape");
-    if (M == 0 || N == 0) return ok();
-    if (!y) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: null output");
-    if (K == 0) {
-        SGQ_HIP(launch_fill_bias(y, M, N, bias, s), "fill_bias");
-        return ok();
-    }
-    const I4Geom g(K, N, group_size);
-    if (!x || !packed) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: null pointer");
-    if (!g.tiled) {
-        if (!scales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: flat layout needs scales");
-        SGQ_HIP(launch_linear_i4_flat(x, M, K, N, packed, scales, g.G, bias, y, s), "linear_i4_flat");
-        return ok();
-    }
-    if (!devscales) return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: tiled layout needs devscales");
-    if (!aligned16(packed) || !aligned16(devscales))
-        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int4: packed and devscales must be 16-byte aligned");
-    if (!forward_fits(4, M, K, N, g.G))
-        return fail(SGQ_ERR_UNSUPPORTED, "sgq_linear_int4: K = %lld is too long for this batch", (long long)K);
-    if (linear_uses_gemv(M, K, N)) {
-        SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
-    } else {
-        const int st = check_linear_ws("sgq_linear_int4", M, K, N, workspace, workspace_bytes);
+    return linear_int4("sgq_linear_int4", x, M, K, N, packed, scales, devscales, group_size, bias, y, workspace,
+                       workspace_bytes, stream);
+}
+
+int sgq_linear_int4_noalloc(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                            const float* devscales, int64_t group_size, const float* bias, float* y, void* stream) {
+    const char* fn = "sgq_linear_int4_noalloc";
+    if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N)) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad shape", fn);
+    const int64_t need = linear_ws_bytes(4, M, K, N);
+    if (need > kScratchBytes)
+        return fail(SGQ_ERR_UNSUPPORTED, "%s: this shape needs %lld bytes of scratch, more than the %lld of the static "
+                    "array (use sgq_linear_int4 with a workspace)", fn, (long long)need, (long long)kScratchBytes);
+    void* ws = nullptr;
+    if (need > 0) {
+        const int st = scratch_for_stream(fn, (hipStream_t)stream, &ws);
         if (st != SGQ_OK) return st;
-        SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
     }
-    return ok();
+    return linear_int4(fn, x, M, K, N, packed, scales, devscales, group_size, bias, y, ws, need > 0 ? kScratchBytes : 0,
+                       stream);
 }
 
 int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_gate,
