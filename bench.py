@@ -409,6 +409,40 @@ def other_config(pkg, key, dev, oracle, steps):
             "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "weight_copies": copies, "rel_err_vs_oracle": err}
 
 
+XOVER_M = (16, 17, 24, 32, 48, 64, 128)
+
+
+def c3_crossover(pkg, dev, oracle, steps):
+    """C3's gate (4096->11008) and down (11008->4096) projections through
+    sgq_linear_int4 at batches around the GEMV -> GEMM switch, as the library
+    dispatches them (sgq_linear_plan names the path), graph-timed over rotating
+    weight copies; rows 0..7 of each output checked against the oracle."""
+    import ctypes
+
+    out = {}
+    lib = pkg.load_library()
+    for name, K, N in (("gate", 4096, 11008), ("down", 11008, 4096)):
+        rows = []
+        for M in XOVER_M:
+            c = dict(name=f"C3 {name} {K}->{N}, M={M}", bits=4, M=M, K=K, N=N, G=128, scheme=2, bias=False, seed=2)
+            copies = max(1, min(64, -(-300_000_000 // alg_bytes(c))))
+            case = Case(pkg, c, dev, copies)
+            ms = case.time_graph(steps, 10)
+            err = case.check(oracle, rows=np.r_[0:8])
+            path, ks = ctypes.c_int(), ctypes.c_int()
+            lib.sgq_linear_plan(4, M, K, N, 128, 0, ctypes.byref(path), ctypes.byref(ks))
+            rows.append({"M": M, "us_per_call": round(ms * 1e3, 3), "us_per_row": round(ms * 1e3 / M, 3),
+                         "path": ["gemv", "gemm_bf16x3", "gemm_fp32", "flat"][path.value], "k_splits": ks.value,
+                         "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "rel_err_vs_oracle_rows0_7": err})
+            if err > 1e-5:
+                raise SystemExit(f"parity failure in bench (c3 crossover {name} M={M}): {err}")
+            del case
+        first_gemm = next((r["M"] for r in rows if r["path"] != "gemv"), None)
+        out[name] = {"shape": f"{K}->{N}", "calls": rows, "gemm_from_M": first_gemm}
+        log(f"[bench] c3 crossover {name}: " + ", ".join(f"M={r['M']} {r['us_per_call']}us {r['path']}" for r in rows))
+    return out
+
+
 def _graph_ms(dev, body, steps):
     """`steps` calls of body(i) captured into one hipGraph; ms per call of one timed replay."""
     import torch
@@ -649,6 +683,8 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--block-decode", type=int, default=0, metavar="CTX",
                     help="only time the 22-layer block decode step at CTX cached positions (for profiling)")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="only time the 110-call C5 decode step (for profiling)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -664,6 +700,12 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.c5_only:
+        r = decode_step(pkg, dev, Oracle(), DECODE_STEPS, False)
+        if r["rel_err_vs_oracle"] > 1e-5:
+            raise SystemExit("parity failure in bench (c5)")
+        print(json.dumps(r), flush=True)
+        return 0
     if args.block_decode:
         r = block_decode_step(pkg, dev, Oracle(), max(2, min(10, args.steps)), args.block_decode)
         if r["rel_err_vs_oracle"] > 1e-5:
@@ -766,6 +808,8 @@ def main() -> int:
             if others[key]["rel_err_vs_oracle"] > 1e-5:
                 raise SystemExit(f"parity failure in bench ({key})")
             torch.cuda.empty_cache()
+        others["c3_crossover"] = c3_crossover(pkg, dev, oracle, OTHER_STEPS)
+        torch.cuda.empty_cache()
         for M in (1, 8):
             key = f"c3_swiglu_m{M}"
             others[key] = swiglu_pair(pkg, dev, oracle, OTHER_STEPS, M)

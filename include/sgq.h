@@ -88,9 +88,10 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
 
 /* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
  * Nonzero only for the GEMM (M > 16, except batches of up to 128 rows with
- * M * K * N <= 2^29, which run the GEMV) when its grid of output tiles (128
- * rows by 256 columns for INT8, 128 for INT4) is smaller than the GPU: K is
- * then split over workgroups, whose partial
+ * M * K * N <= 2^28, which run the GEMV) when its grid of output tiles (32 or
+ * 64 rows by 128 columns for batches of up to 32 or 64 rows; else 128 rows by
+ * 256 columns for INT8, 128 for INT4) is smaller than the GPU: K is then
+ * split over workgroups, whose partial
  * tiles (KS * M * N floats) are summed by a second kernel in fixed order.
  * 0 otherwise (the GEMV and large GEMMs own whole outputs per workgroup), and
  * the workspace arguments may then be NULL/0.  The contents need no
@@ -186,7 +187,7 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
  * Dispatch: M <= 16 runs the wavefront GEMV (row groups of 8), as do up to
- * 128 rows when M * K * N <= 2^29; larger batches the LDS-staged MFMA
+ * 128 rows when M * K * N <= 2^28; larger batches the LDS-staged MFMA
  * GEMM, whose fp32 products run on the bf16 matrix cores as three exact bf16
  * products each (fp32 accumulation; as accurate as an fp32 product).
  * workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes, else
@@ -296,7 +297,7 @@ int64_t sgq_llama_decode_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_
  *   workspace: sgq_llama_decode_workspace_bytes(B, D, H, max_len) bytes,
  *              16-byte aligned.
  * Batches the forward runs on the GEMV (B <= 16, or up to 128 when every
- * projection's B * K * N <= 2^29) run every projection on it (q, k, v in one
+ * projection's B * K * N <= 2^28) run every projection on it (q, k, v in one
  * launch; the RMSNorms folded in; the residual adds in the epilogues);
  * larger B on the MFMA GEMM.  fp32 results throughout;
  * outputs match the reference's full-sequence forward within 1e-5 relative. */

@@ -84,10 +84,14 @@ constexpr int kGemvMaxM = 16;  // M <= this runs the GEMV, larger M the MFMA GEM
 // The plain forward also runs the GEMV for batches of up to this many rows
 // (row groups of 8, one workgroup each) when the work is small: the GEMV's
 // time grows with M * K * N at the VALU rate from a fixed ~3 us, the GEMM's
-// from ~15 us of pipeline fill, split-K partials and reduce (measured on
-// MI355X: 128 x 1024 x 1024 INT8 took 20 us on the GEMM).
+// from ~10-15 us of pipeline fill, split-K partials and reduce.  Measured on
+// MI355X with each path forced (INT4 g128): at 16 rows the GEMV wins on every
+// shape tried (4096->11008 31 vs 35 us, 2048->2048 5.6 vs 11.8 us); from 17
+// rows the GEMM's 32- and 64-row tiles win once M * K * N passes about 2^28
+// (4096x4096 at 17..32 rows 19-23 vs 23 us, 4096->11008 at 17 rows 35 vs
+// 54 us) and lose below it (2048x2048 at 64 rows 17 vs 14 us).
 constexpr int64_t kGemvRowsMax = 128;
-constexpr int64_t kGemvSmallWork = (int64_t)1 << 29;  // M * K * N
+constexpr int64_t kGemvSmallWork = (int64_t)1 << 28;  // M * K * N
 inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
     return M <= kGemvMaxM || (M <= kGemvRowsMax && M * K * N <= kGemvSmallWork);
 }
@@ -156,7 +160,10 @@ struct GemmTile {
 constexpr int64_t kMaxCus = 256;
 int device_cus(hipStream_t s);
 GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus);
-GemmTile gemm_tile(int bits);
+// Tile of the three-term GEMM for a code width and batch: 32 or 64 rows by
+// 128 columns for batches of up to 32 or 64 rows, else 128 x 256 (INT8) or
+// 128 x 128 (INT4).
+GemmTile gemm_tile(int bits, int64_t M);
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 // The plan a forward of this shape runs on `cus` compute units: path 0 the
 // GEMV, 1 the three-term bf16 GEMM, 2 the fp32 GEMM, 3 the flat INT4 kernel;

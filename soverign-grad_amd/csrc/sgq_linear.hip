@@ -778,6 +778,10 @@ struct G3Shape {
 };
 using G3Wide = G3Shape<2, 4, 4, 4>;  // 128 x 256, 8 wavefronts: INT8
 using G3Tile = G3Shape<2, 4, 2, 4>;  // 128 x 128, 4 wavefronts: INT4
+// Skinny batches (17..64 rows) waste most of a 128-row tile's MFMA work and
+// split work: they take 32- or 64-row tiles (either code width, 128 columns).
+using G3Rows32 = G3Shape<1, 2, 2, 4>;  // 32 x 128, 2 wavefronts
+using G3Rows64 = G3Shape<2, 2, 2, 4>;  // 64 x 128, 4 wavefronts
 
 template <int BITS, bool KALIGN4, bool PT, class SH>
 __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(
@@ -1266,17 +1270,22 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t c
     return p;
 }
 
-// Tile of the three-term GEMM for a code width (the fp32 kernel uses the
-// 128 x 128 tile), with the workgroups a CU holds at once: two of the
-// 128-wide tiles, one of the 256-wide (its LDS and registers fill the CU).
-GemmTile gemm_tile(int bits) { return bits == 8 ? GemmTile{kBM, 2 * kBN, 1} : GemmTile{kBM, kBN, 2}; }
+// Tile of the three-term GEMM for a code width and batch (the fp32 kernel
+// uses the 128 x 128 tile), with the workgroups a CU holds at once: two of
+// the 128 x 128 tiles, one of the 128 x 256 (its LDS and registers fill the
+// CU); of the small-batch tiles (28 and 40 KB of LDS) four and three.
+GemmTile gemm_tile(int bits, int64_t M) {
+    if (M <= 32) return GemmTile{32, kBN, 4};
+    if (M <= 64) return GemmTile{64, kBN, 3};
+    return bits == 8 ? GemmTile{kBM, 2 * kBN, 1} : GemmTile{kBM, kBN, 2};
+}
 
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     // Either code width (and the fp32 kernel's 128 x 128 tile) on the largest
     // device: room for the largest plan on any device.
     int64_t ks = gemm_plan(M, K, N, GemmTile{kBM, kBN, 2}, kMaxCus).KS;
     for (int bits : {4, 8}) {
-        const int64_t k = gemm_plan(M, K, N, gemm_tile(bits), kMaxCus).KS;
+        const int64_t k = gemm_plan(M, K, N, gemm_tile(bits, M), kMaxCus).KS;
         if (k > ks) ks = k;
     }
     return ks > 1 ? ks * M * N * 4 : 0;
@@ -1301,7 +1310,7 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
     const int mode = bits == 4 ? (int)I4Geom(K, N, group_size).spc : 0;
     const bool three = gemm_three_term(bits, mode);
     *path = three ? 1 : 2;
-    *ks = gemm_plan(M, K, N, three ? gemm_tile(bits) : GemmTile{kBM, kBN, 2}, cus).KS;
+    *ks = gemm_plan(M, K, N, three ? gemm_tile(bits, M) : GemmTile{kBM, kBN, 2}, cus).KS;
 }
 
 namespace {
@@ -1310,7 +1319,7 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
                        int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, void* ws, hipStream_t s) {
     // INT4 groups that are not a multiple of 128 take the fp32-MFMA kernel.
     const bool three = gemm_three_term(BITS, mode);
-    const GemmTile t = three ? gemm_tile(BITS) : GemmTile{kBM, kBN, 2};
+    const GemmTile t = three ? gemm_tile(BITS, M) : GemmTile{kBM, kBN, 2};
     const GemmPlan p = gemm_plan(M, K, N, t, device_cus(s));
     float* part = p.KS > 1 ? (float*)ws : nullptr;
     const dim3 grid((unsigned)(ceil_div(M, t.bm) * ceil_div(N, t.bn) * p.KS));
@@ -1330,7 +1339,11 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
         SGQ_GEMM3(SH, false, true);       \
     else                                  \
         SGQ_GEMM3(SH, false, false);
-    if (three) {
+    if (three && t.bm == 32) {
+        SGQ_GEMM3_SHAPE(G3Rows32)
+    } else if (three && t.bm == 64) {
+        SGQ_GEMM3_SHAPE(G3Rows64)
+    } else if (three) {
         SGQ_GEMM3_SHAPE(Big)
     } else if (k4)
         k_gemm<BITS, true><<<grid, kThreads, 0, s>>>(x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode,

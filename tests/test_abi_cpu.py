@@ -193,7 +193,7 @@ def test_forward_refuses_k_past_32bit_offsets(lib):
     """K long enough that the kernels' 32-bit buffer offsets would wrap is
     refused (SGQ_ERR_UNSUPPORTED) before any launch: past 2^22 rows for the
     MFMA GEMM (128-row tiles of x), past 2^29 rows for the GEMV."""
-    big_gemm = (1 << 22) + 16  # GEMM path at M=32 (M * K * N > 2^29)
+    big_gemm = (1 << 22) + 16  # GEMM path at M=32 (M * K * N > 2^28)
     assert lib.sgq_linear_int8(16, 32, big_gemm, 64, 16, 16, 0, None, 16, 16, 1 << 40, None) == 2
     assert b"too long" in lib.sgq_last_error()
     assert lib.sgq_linear_int4(16, 32, big_gemm, 64, 16, 16, 16, 128, None, 16, 16, 1 << 40, None) == 2

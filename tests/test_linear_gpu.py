@@ -5,6 +5,8 @@ dequantize-then-matmul (fp32 accumulate; the kernels accumulate in a different
 order, so bits are not expected to match).  y_ref comes from the golden
 fixtures (compiled reference) or the oracle on the same quantized weights.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -150,6 +152,23 @@ def test_same_sign_activations(sgq, dev, oracle, synth, M, K, N, kind):
     y = _np(sgq.quantized_matmul_int4(_to_dev(x, dev), qw))
     q, s = oracle.quantize_int4(W, 128)
     yref = oracle.quantized_matmul_int4(x, q, s, 128)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
+# Batches of 17..64 rows with too much work for the GEMV take the GEMM's 32-
+# and 64-row tiles (split K); every row against the oracle.
+@pytest.mark.parametrize("M", [17, 24, 32, 33, 48, 64])
+@pytest.mark.parametrize("bits_,K,N,G,scheme", [(4, 4096, 11008, 128, 0), (4, 11008, 4096, 128, 0),
+                                                (8, 4096, 8192, 0, 0), (8, 4096, 8192, 0, 1)])
+def test_skinny_gemm_tiles(sgq, dev, oracle, synth, M, bits_, K, N, G, scheme):
+    lib = sgq.load_library()
+    path, ks = ctypes.c_int(), ctypes.c_int()
+    assert lib.sgq_linear_plan(bits_, M, K, N, G, 256, ctypes.byref(path), ctypes.byref(ks)) == 0
+    print(f"  case M={M} K={K} N={N} bits={bits_} path={path.value} k_splits={ks.value}", flush=True)
+    assert path.value == 1  # the three-term GEMM
+    y, yref = _case(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme, True, 17)
     e = rel_err(y, yref)
     print(f"    rel_err={e:.3e}", flush=True)
     assert e <= TOL
