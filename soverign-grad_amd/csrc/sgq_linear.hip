@@ -787,11 +787,12 @@ template <int BITS, bool KALIGN4, bool PT, class SH>
 __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(
     const float* __restrict__ x, int M, int K, int N, const uint4* __restrict__ W, const float* __restrict__ S,
     int mode, int Kpad, int RQ, int NS, int KS, int sps, const float* __restrict__ bias, float* __restrict__ y,
-    float* __restrict__ part) {
+    float* __restrict__ part, int xr) {
     // mode: INT8 -> per-tensor flag (also the template flag PT, so that no
     // stage holds a branch); INT4 -> strips per scale column (a multiple of
     // 16: one scale column per 128-column tile).  Workgroup b computes split
-    // b % KS (stages [kt0, kt1) of sps each) of tile b / KS.
+    // b % KS (stages [kt0, kt1) of sps each) of tile b / KS.  xr > 0 (no K
+    // split): each XCD takes a rectangle of xr tile rows (see below).
     constexpr int SW = (BITS == 4) ? 8 : 4;
     constexpr int NT = SH::NT, BM = SH::BM, BN = SH::BN, RB = SH::RB, CB = SH::CB;
     constexpr int EA = BM * kB3KG / NT;  // A entries (row, k group) per thread
@@ -809,7 +810,17 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
     // shapes; with a split (small grids) the plain order measured better.
     const int bsw = KS == 1 ? xcd_swizzle(blockIdx.x, gridDim.x) : (int)blockIdx.x;
     const int tile = bsw / KS, split = bsw - tile * KS;
-    const int tm = tile / ntn, tn = tile - tm * ntn;
+    int tm = tile / ntn, tn = tile - tm * ntn;
+    if (xr > 0) {
+        // The grid's tiles fall into 8 rectangles of xr tile rows by per / xr
+        // tile columns, one per XCD (its share of the swizzled ids), so an
+        // XCD's L2 fetches xr row blocks of x and per / xr column blocks of
+        // codes instead of every column block (C4: 16 MiB per XCD, not 20).
+        const int per = gridDim.x / kXcds, x = tile / per, l = tile - x * per;
+        const int bw = per / xr, rects_m = (gridDim.x / ntn) / xr;
+        tm = (x % rects_m) * xr + l % xr;
+        tn = (x / rects_m) * bw + l / xr;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
     const int KT = (Kpad + kB3BK - 1) / kB3BK;
     const int kt0 = split * sps, kt1 = (kt0 + sps) < KT ? (kt0 + sps) : KT;
@@ -1314,6 +1325,25 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
 }
 
 namespace {
+// Tile rows per XCD rectangle for a grid of tm x tn tiles without a K split:
+// the divisor a of both tm and per = tm * tn / 8 (per / a dividing tn) that
+// minimises what one XCD's L2 fetches, a row blocks of x (xb bytes each) and
+// per / a column blocks of codes (wb bytes each); 0 when the grid does not
+// tile into 8 such rectangles (the plain XCD order then).
+int xcd_rect_rows(int64_t tm, int64_t tn, int64_t xb, int64_t wb) {
+    const int64_t T = tm * tn;
+    if (T % kXcds != 0) return 0;
+    const int64_t per = T / kXcds;
+    int best = 0;
+    int64_t cost = 0;
+    for (int64_t a = 1; a <= per && a <= tm; ++a) {
+        if (per % a || tm % a || tn % (per / a) || (tm / a) * (tn / (per / a)) != kXcds) continue;
+        const int64_t c = a * xb + (per / a) * wb;
+        if (best == 0 || c < cost) best = (int)a, cost = c;
+    }
+    return best;
+}
+
 template <int BITS>
 hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc, int mode,
                        int64_t Kpad, int64_t RQ, int64_t NS, const float* bias, float* y, void* ws, hipStream_t s) {
@@ -1323,13 +1353,16 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
     const GemmPlan p = gemm_plan(M, K, N, t, device_cus(s));
     float* part = p.KS > 1 ? (float*)ws : nullptr;
     const dim3 grid((unsigned)(ceil_div(M, t.bm) * ceil_div(N, t.bn) * p.KS));
+    const int xr = p.KS == 1 ? xcd_rect_rows(ceil_div(M, t.bm), ceil_div(N, t.bn), t.bm * K * 4,
+                                             t.bn * K * BITS / 8)
+                             : 0;
     const bool k4 = x_aligned4(x, K);
     const bool pt = BITS == 8 && mode;
     using Big = typename std::conditional<BITS == 8, G3Wide, G3Tile>::type;
 #define SGQ_GEMM3(SH, A4, PT_)                                                                                 \
     k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(x, (int)M, (int)K, (int)N,              \
                                                                     (const uint4*)packed, sc, mode, (int)Kpad, \
-                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part)
+                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part, xr)
 #define SGQ_GEMM3_SHAPE(SH)               \
     if (k4 && pt)                         \
         SGQ_GEMM3(SH, true, true);        \
