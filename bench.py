@@ -248,6 +248,15 @@ def measured_traffic(config: str):
     return json.loads(path.read_text()).get("hbm_bytes_per_launch")
 
 
+def profiled_kernel(config: str):
+    """The dominant kernel's duration per launch from the committed rocprofv3
+    kernel-trace summary for this workload (None if there is none)."""
+    path = ROOT / "profiles" / f"kernel_{config}.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text())
+
+
 def cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo), for the CPU baseline lines."""
     try:
@@ -742,6 +751,14 @@ def main() -> int:
          "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
          "frac_of_fp32_mfma_peak": round(tfl / FP32_MFMA_PEAK_TFLOPS, 4)}
     )
+    prof = profiled_kernel(args.config)
+    if prof and hbm_bound:
+        # The same fraction with the kernel's own duration from the committed
+        # rocprofv3 trace (no launch gaps), beside the event-timed one above.
+        kns = prof.get("avg_ns_graph_replays") or prof.get("avg_ns")
+        roofline["kernel_ns_rocprof"] = kns
+        roofline["frac_kernel_rocprof"] = round(nbytes / (kns * 1e-9) / 1e9 / HBM_PEAK_GBS, 4)
+        roofline["kernel_summary"] = prof.get("summary")
     out = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -793,8 +810,15 @@ def main() -> int:
                          "unit": "TFLOP/s", "frac": round(tfl4 / GEMM3_PEAK_TFLOPS, 4),
                          "traffic": measured_traffic("c4"),
                          "peak_basis": "bf16 dense MFMA 2500 TFLOP/s / 3 exact bf16 products per fp32 product",
+                         "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS,
                          "frac_of_fp32_mfma_peak": round(tfl4 / FP32_MFMA_PEAK_TFLOPS, 4)},
         }
+        p4 = profiled_kernel("c4")
+        if p4:
+            kns = p4.get("median_ns") or p4.get("avg_ns")
+            out["secondary"]["roofline"]["kernel_ns_rocprof"] = kns
+            out["secondary"]["roofline"]["frac_kernel_rocprof"] = round(
+                alg_flops(c4) / (kns * 1e-9) / 1e12 / GEMM3_PEAK_TFLOPS, 4)
         del case4
         torch.cuda.empty_cache()
 
