@@ -103,7 +103,9 @@ int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
  * with `compute_units` CUs (0: the calling thread's current device; a full
  * MI355X has 256, a partition fewer).  *path: 0 the GEMV, 1 the three-term
  * bf16 MFMA GEMM, 2 the fp32 MFMA GEMM (INT4 groups that are not a multiple
- * of 128), 3 the generic kernel of the flat INT4 layout.  *k_splits: 1, or
+ * of 128), 3 the generic kernel of the flat INT4 layout, 4 the skinny bf16
+ * MFMA kernel (INT4, 5..16 rows over a weight wide enough to fill the
+ * device with workgroups of 32 or 64 columns).  *k_splits: 1, or
  * the number of workgroups sharing each output tile's K range (the GEMM on
  * grids smaller than the device).  sgq_linear_workspace_bytes sizes for the
  * largest device, so it covers every plan.  Host-only; this library's own

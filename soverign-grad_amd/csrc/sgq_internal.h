@@ -96,6 +96,31 @@ inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
     return M <= kGemvMaxM || (M <= kGemvRowsMax && M * K * N <= kGemvSmallWork);
 }
 
+// Batches of kSkinnyMinRows..kGemvMaxM rows over wide INT4 weights run on the
+// bf16 matrix cores (k_skinny3) instead of the GEMV: column blocks of 16 per
+// workgroup (at most cmax; 2*C strips must share a scale column), or 0 where
+// the GEMV is the faster path.  The GEMV's cost grows with the rows (one FMA
+// per code and row), the MFMA form's hardly at all, but its workgroups own
+// 16*C columns each, so it needs a wide weight to fill the GPU (at least 5/8
+// of a workgroup per CU with C = 4 or 2) and a K long enough to amortise its
+// split and LDS reduction.  Measured on MI355X (INT4 g128, graphs of 100
+// calls, GEMV -> MFMA): 4096->11008 at 5 / 8 / 16 rows 19.0 / 19.9 / 31.0 ->
+// 15.4 / 15.9 / 17.0 us; 2048->6144 at 8 / 16 rows 8.4 / 12.9 -> 7.4 / 8.4;
+// 4096->14336 at 16 rows 37.9 -> 17.4; 8192->28672 at 16 rows 130 -> 59.
+// Kept on the GEMV: 4 rows (4096->11008 12.8 vs 15.3 us), narrow weights
+// (N <= 4096: 128-256 workgroups of 16 columns, no gain), K = 1024
+// (1024->5120 at 8 rows 5.9 vs 7.0 us).
+constexpr int64_t kSkinnyMinRows = 5;
+constexpr int64_t kSkinnyMinK = 2048;
+constexpr int64_t kSkinnyMaxK = (int64_t)1 << 24;  // 16 rows of x addressed with 32-bit offsets
+inline int skinny_blocks(int64_t M, int64_t K, const I4Geom& g, int64_t cus, int cmax) {
+    if (M < kSkinnyMinRows || M > kGemvMaxM || K < kSkinnyMinK || K > kSkinnyMaxK || !g.tiled || g.spc % 2 != 0)
+        return 0;
+    for (int c = cmax; c >= 2; c /= 2)
+        if (g.spc % (2 * c) == 0 && g.NS / (2 * c) * 8 >= 5 * cus) return c;
+    return 0;
+}
+
 // ---- launchers (return hipError_t of the launch) ----------------------
 hipError_t launch_fill_zero(void* p, int64_t bytes, hipStream_t s);
 hipError_t launch_fill_bias(float* y, int64_t M, int64_t N, const float* bias, hipStream_t s);
@@ -166,8 +191,8 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t c
 GemmTile gemm_tile(int bits, int64_t M);
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 // The plan a forward of this shape runs on `cus` compute units: path 0 the
-// GEMV, 1 the three-term bf16 GEMM, 2 the fp32 GEMM, 3 the flat INT4 kernel;
-// ks the K splits (1: none).
+// GEMV, 1 the three-term bf16 GEMM, 2 the fp32 GEMM, 3 the flat INT4 kernel,
+// 4 the skinny MFMA kernel; ks the K splits (1: none).
 void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int64_t cus, int* path, int* ks);
 hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                           bool per_tensor, const float* bias, float* y, void* ws, hipStream_t s);

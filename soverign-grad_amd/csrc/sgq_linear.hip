@@ -1001,6 +1001,219 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny INT4 forward on the bf16 matrix cores: batches of 5..16 rows over
+// wide weights (src/quantization.cpp:199-206 for those shapes).
+//
+// The batch is the 16 rows of one v_mfma_f32_16x16x32_bf16 (rows past M are
+// zeros), with the three-term split of k_gemm3: A = x * s as three bf16
+// planes, B = codes (exact in bf16), fp32 accumulation.  A workgroup owns C
+// column blocks of 16 (2C strips of one scale column, so one x * s split
+// serves all of them) over all of K; its NW wavefronts take 32-row k blocks
+// in turn and are summed through LDS at the end.  No workgroup needs another's
+// result, as in the GEMV.
+//
+// B operand straight from the strip layout, without LDS: a 32-row k block of
+// a strip is 128 bytes, dword r = row r's eight nibbles.  Lane l of a 16-lane
+// row takes column e = (l & 3) | (l & 8) >> 1 of strip j = (l >> 2) & 1 and,
+// in lane group g = l >> 4, rows 8g .. 8g+7.  Each lane loads one dword (row
+// 8g + e of its strip, all eight columns); an 8x8 nibble transpose across the
+// eight lanes of (g, j) leaves it with rows 8g .. 8g+7 of column e, which is
+// its B operand.  The codes are read once, in 256-byte runs per wavefront.
+// ---------------------------------------------------------------------------
+
+// Exchanges within the eight lanes of a transpose group: lane bits 0 and 1
+// are group bits 0 and 1 (DPP quad_perm), lane bit 3 is group bit 2 (DPP
+// row_ror:8 within a 16-lane row).
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); }
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true); }
+__device__ __forceinline__ uint32_t dpp_xor8(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); }
+__device__ __forceinline__ uint32_t rotr32(uint32_t v, uint32_t s) { return __builtin_amdgcn_alignbit(v, v, s); }
+
+// Per-lane constants of the transpose for group lane e.  Step d (4, 2, 1
+// nibbles): the lane keeps its nibbles whose index has bit d equal to its own
+// bit d and takes the other half from its partner (e ^ d), rotated by 4d bits
+// so that partner nibble c lands on c ^ d.
+struct NibbleT {
+    uint32_t keep4, keep2, keep1, rot2, rot1;
+};
+__device__ __forceinline__ NibbleT nibble_t(int e) {
+    NibbleT t;
+    t.keep4 = (e & 4) ? 0xFFFF0000u : 0x0000FFFFu;
+    t.keep2 = (e & 2) ? 0xFF00FF00u : 0x00FF00FFu;
+    t.keep1 = (e & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    t.rot2 = (e & 2) ? 8u : 24u;  // right by 8, or left by 8
+    t.rot1 = (e & 1) ? 4u : 28u;
+    return t;
+}
+// On entry nibble c of lane e is T[e][c]; on return nibble r is T[r][e].
+__device__ __forceinline__ uint32_t nibble_transpose8(uint32_t w, const NibbleT& t) {
+    uint32_t p = dpp_xor8(w);
+    w = (w & t.keep4) | (rotr32(p, 16u) & ~t.keep4);
+    p = dpp_xor2(w);
+    w = (w & t.keep2) | (rotr32(p, t.rot2) & ~t.keep2);
+    p = dpp_xor1(w);
+    w = (w & t.keep1) | (rotr32(p, t.rot1) & ~t.keep1);
+    return w;
+}
+
+// Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
+// operand: high nibbles masked in place and low nibbles shifted up read as
+// signed bytes 16q, converted exactly.
+__device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
+    const uint32_t hi = t & 0xF0F0F0F0u, lo = (t << 4) & 0xF0F0F0F0u;
+    const uint4 b = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<0>(hi)), pack_hi16(cvt_sbyte<1>(lo), cvt_sbyte<1>(hi)),
+                               pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<2>(hi)), pack_hi16(cvt_sbyte<3>(lo), cvt_sbyte<3>(hi)));
+    return __builtin_bit_cast(bf16x8, b);
+}
+
+struct SkinnyArgs {
+    const float* x;  // [M, K]
+    int M, K, N;
+    const uint4* W[2];  // NG weights of equal shape (gate, up)
+    const float* SC[2];
+    const float* bias[2];
+    int spc, Kpad, RQ;
+    FastDiv wpc;  // workgroups per scale column
+    float* y;     // [M, N]
+    int nblk;     // grid size
+};
+
+// NG == 2: the gated MLP, gate and up blocks of the same columns in one
+// workgroup, h = silu(gate + bias) * (up + bias2).  XA: x rows are 16-byte
+// aligned and K % 4 == 0 (float4 loads); otherwise one float per load.
+template <int NW, int U, int C, int NG, bool XA>
+__global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
+    const int K = a.K;
+    const int v = xcd_swizzle(blockIdx.x, a.nblk);
+    const int blk0 = v * C;  // first column block
+    const int sc = a.wpc.div(v);
+    __amdgpu_buffer_rsrc_t rW[NG], rS[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        rW[q] = make_rsrc(a.W[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
+        rS[q] = make_rsrc(a.SC[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
+    }
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
+    int wv[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + 32 * g + 4 * e;
+    const bool row_live = n < a.M;
+    const int xrow = n * K * 4;
+    const NibbleT tp = nibble_t(e);
+    floatx4 acc[NG][C];
+#pragma unroll
+    for (int q = 0; q < NG; ++q)
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[q][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int nkb = (a.Kpad + 31) >> 5;
+    // K blocks kb0, kb0 + NW, ..., U of them per batch.  A block past the end
+    // reads x and the scales as zeros (its code dwords are whatever follows
+    // and are multiplied by zero), so partial batches need no branch.
+    for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
+        uint32_t w[U][NG][C];
+        float xv[U][8], sv[U][NG][8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kb = kb0 + u * NW;
+#pragma unroll
+            for (int q = 0; q < NG; ++q)
+#pragma unroll
+                for (int c = 0; c < C; ++c)
+                    w[u][q][c] = __builtin_amdgcn_raw_buffer_load_b32(rW[q], wv[c], kb * 128, 0);
+            const int k0 = kb * 32 + 8 * g;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kk = k0 + 4 * h;
+                if constexpr (XA) {
+                    const float4 xq = buf_load4f<true>(rX, row_live && kk < K ? xrow + kk * 4 : kOobOff, 0);
+                    xv[u][4 * h] = xq.x, xv[u][4 * h + 1] = xq.y, xv[u][4 * h + 2] = xq.z, xv[u][4 * h + 3] = xq.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        xv[u][4 * h + i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rX, row_live && kk + i < K ? xrow + (kk + i) * 4 : kOobOff, 0, 0));
+                }
+#pragma unroll
+                for (int q = 0; q < NG; ++q) {
+                    const float4 sq = buf_load4f<true>(rS[q], kk * 4, 0);
+                    sv[u][q][4 * h] = sq.x, sv[u][q][4 * h + 1] = sq.y, sv[u][q][4 * h + 2] = sq.z,
+                                 sv[u][q][4 * h + 3] = sq.w;
+                }
+            }
+        }
+        // Every load of the batch is issued before the first is used.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int q = 0; q < NG; ++q) {
+                float xs[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xs[i] = xv[u][i] * sv[u][q][i];
+                uint4 ah, am, al;
+                split3(xs, ah, am, al);
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    const bf16x8 b = nibbles_bf16x16(nibble_transpose8(w[u][q][c], tp));
+                    acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), b, acc[q][c], 0, 0, 0);
+                    acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), b, acc[q][c], 0, 0, 0);
+                    acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), b, acc[q][c], 0, 0, 0);
+                }
+            }
+    }
+    // Accumulator element r of lane l is output row 4 * (l >> 4) + r of
+    // column lane l & 15 of its block.  The wavefronts' partial tiles are
+    // summed in wavefront order (deterministic), one weight at a time through
+    // the same LDS; thread t keeps output t (t + NW * 64, ...) of each.
+    constexpr int OPT = (256 * C + NW * 64 - 1) / (NW * 64);
+    __shared__ float red[NW][C][4][64];
+    float o[NG][OPT];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        if (q > 0) __syncthreads();  // every thread has read the previous weight's partials
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][c][r][lane] = acc[q][c][r];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < OPT; ++i) {
+            const int t = threadIdx.x + i * NW * 64;
+            const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
+            const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
+            const int col = 8 * strip + el;
+            float s = 0.0f;
+            if (t < 256 * C && m < a.M && col < a.N) {
+#pragma unroll
+                for (int w2 = 0; w2 < NW; ++w2) s += red[w2][c][m & 3][16 * (m >> 2) + sl];
+                s *= 0.0625f;  // the codes entered as 16q
+                // h + m + l turns an infinite x * s into inf - inf: recompute
+                // a non-finite total as the reference's k-order sum.
+                if (!isfinite(s))
+                    s = i4_column_exact<false>(a.W[q], a.SC[q], strip, el, a.spc, a.Kpad, a.RQ, a.x + (int64_t)m * K,
+                                               nullptr, K);
+                if (a.bias[q]) s = s + a.bias[q][col];
+            }
+            o[q][i] = s;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+        const int t = threadIdx.x + i * NW * 64;
+        const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
+        const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
+        if (t < 256 * C && m < a.M && col < a.N) {
+            float r0 = o[0][i];
+            if constexpr (NG == 2) r0 = silu_f32(o[0][i]) * o[1][i];
+            a.y[(int64_t)m * a.N + col] = r0;
+        }
+    }
+}
+
 // h[i] = silu(h[i]) * u[i]: the gated MLP's elementwise tail after two
 // separate projections (mul of equal shapes is one multiply, ops.cpp:239-253).
 __global__ __launch_bounds__(kThreads) void k_silu_mul(float* __restrict__ h, const float* __restrict__ u, int64_t n) {
@@ -1175,10 +1388,55 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
     return a;
 }
 
+// Wavefronts per workgroup of k_skinny3 (each takes every 16th k block) and
+// k blocks a wavefront keeps in flight (U per batch of loads).
+constexpr int kSkinnyWaves = 16;
+
+// One k_skinny3 launch with C column blocks per workgroup (C from
+// skinny_blocks); NG weights of equal shape with their devscales and biases.
+template <int C, int NG>
+hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* const* packed,
+                         const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
+                         hipStream_t s) {
+    constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
+    SkinnyArgs a{};
+    a.x = x;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.N = (int)N;
+    for (int q = 0; q < NG; ++q) {
+        a.W[q] = (const uint4*)packed[q];
+        a.SC[q] = devscales[q];
+        a.bias[q] = bias[q];
+    }
+    a.spc = (int)g.spc;
+    a.Kpad = (int)g.Kpad;
+    a.RQ = (int)g.RQ;
+    a.wpc = FastDiv((uint32_t)(g.spc / (2 * C)));
+    a.y = y;
+    a.nblk = (int)(g.NS / (2 * C));  // skinny_blocks: 2C divides spc, which divides NS
+    if (x_aligned4(x, K))
+        k_skinny3<kSkinnyWaves, U, C, NG, true><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    else
+        k_skinny3<kSkinnyWaves, U, C, NG, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int NG>
+hipError_t skinny_dispatch(int c, const float* x, int64_t M, int64_t K, int64_t N, const void* const* packed,
+                           const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
+                           hipStream_t s) {
+    if (c == 4) return skinny_launch<4, NG>(x, M, K, N, packed, devscales, bias, g, y, s);
+    if (c == 2) return skinny_launch<2, NG>(x, M, K, N, packed, devscales, bias, g, y, s);
+    return hipErrorInvalidValue;
+}
+
 }  // namespace
 
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
+    const int c = skinny_blocks(M, K, g, device_cus(s), 4);
+    if (c > 0) return skinny_dispatch<1>(c, x, M, K, N, &packed, &devscales, &bias, g, y, s);
     return launch_gemv_i4_multi(x, M, K, N, 1, &packed, &devscales, &bias, g, y, N, nullptr, nullptr, 0.0f, s);
 }
 
@@ -1211,6 +1469,16 @@ hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
                                  hipStream_t s, const float* gamma, float eps) {
+    // The same path as two forward calls of these shapes, so the gate and up
+    // sums are the plain forward's (k_skinny3 sums k blocks in the same order
+    // whatever its column blocks per workgroup).
+    const int c = gamma ? 0 : skinny_blocks(M, K, g, device_cus(s), 4);
+    if (c > 0) {
+        const void* packed[2] = {packed_g, packed_u};
+        const float* ds[2] = {devscales_g, devscales_u};
+        const float* bs[2] = {bias_g, bias_u};
+        return skinny_dispatch<2>(c, x, M, K, N, packed, ds, bs, g, h, s);
+    }
     GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, h, N, nullptr);
     a.gamma = gamma;
     a.eps = eps;
@@ -1315,7 +1583,8 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
         return;
     }
     if (linear_uses_gemv(M, K, N)) {
-        *path = 0;
+        const int64_t c = cus < kMaxCus ? cus : kMaxCus;  // as device_cus reports it
+        *path = bits == 4 && skinny_blocks(M, K, I4Geom(K, N, group_size), c, 4) > 0 ? 4 : 0;
         return;
     }
     const int mode = bits == 4 ? (int)I4Geom(K, N, group_size).spc : 0;

@@ -281,4 +281,32 @@ def test_plan_follows_the_device_cu_count(lib):
     assert _plan(lib, 4, 300, 2048, 644, 32, 256)[0] == 3  # N % 8 != 0: flat layout
     # A CU count above the full chip is planned as the full chip.
     assert _plan(lib, 8, 256, 4096, 1024, 0, 1024) == _plan(lib, 8, 256, 4096, 1024, 0, 256)
+    assert _plan(lib, 4, 8, 4096, 11008, 128, 1024) == _plan(lib, 4, 8, 4096, 11008, 128, 256)
     assert lib.sgq_linear_plan(8, 1, 4, 4, 0, -1, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == 1
+
+
+def test_plan_skinny_mfma(lib):
+    """Batches of 5..16 rows over a wide INT4 weight take the skinny bf16 MFMA
+    kernel (path 4) when its 32- or 64-column workgroups fill at least 5/8 of
+    the CUs, and need 2C strips per scale column; everything else at those
+    batch sizes stays on the GEMV (path 0)."""
+    for M in range(5, 17):
+        assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (4, 1)  # 172 workgroups of 64 columns
+        assert _plan(lib, 4, M, 2048, 6144, 128, 256) == (4, 1)  # 192 of 32
+        assert _plan(lib, 4, M, 5632, 2048, 128, 256) == (0, 1)  # 128 of 16: too narrow
+    for M in (1, 2, 3, 4):
+        assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (0, 1)
+    assert _plan(lib, 4, 17, 4096, 11008, 128, 256)[0] == 1  # the GEMM from 17 rows
+    assert _plan(lib, 8, 8, 4096, 11008, 0, 256) == (0, 1)  # INT8 stays on the GEMV
+    assert _plan(lib, 4, 8, 2048, 6144, 8, 256) == (0, 1)  # one strip per scale column
+    assert _plan(lib, 4, 8, 2048, 6144, 16, 256) == (0, 1)  # two strips: 16 columns, too narrow
+    assert _plan(lib, 4, 8, 2048, 5120, 32, 256) == (4, 1)  # four strips: 160 workgroups of 32
+    assert _plan(lib, 4, 8, 1024, 5120, 32, 256) == (0, 1)  # K too short
+    assert _plan(lib, 4, 8, 2048, 5112, 24, 256) == (0, 1)  # three strips per scale column
+    assert _plan(lib, 4, 8, 4096, 8192, 64, 256) == (4, 1)  # C = 2: 256 workgroups
+    assert _plan(lib, 4, 8, 4096, 11004, 128, 256)[0] == 3  # flat layout
+    # The threshold follows the device: a quarter of the CUs needs a quarter
+    # of the workgroups (64 of 32 columns for N = 2048).
+    assert _plan(lib, 4, 8, 5632, 2048, 128, 64) == (4, 1)
+    assert _plan(lib, 4, 8, 5632, 2048, 128, 128) == (0, 1)
+    assert _plan(lib, 4, 8, (1 << 24) + 16, 6144, 128, 256) == (0, 1)  # K beyond 32-bit x offsets
