@@ -418,14 +418,17 @@ def other_config(pkg, key, dev, oracle, steps):
             "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "weight_copies": copies, "rel_err_vs_oracle": err}
 
 
-XOVER_M = (16, 17, 24, 32, 48, 64, 128)
+XOVER_M = (4, 5, 8, 16, 17, 24, 32, 48, 64, 128)
+# sgq_linear_plan's path codes (include/sgq.h)
+PATH_NAMES = ("gemv", "gemm_bf16x3", "gemm_fp32", "flat", "skinny_bf16x3")
 
 
 def c3_crossover(pkg, dev, oracle, steps):
     """C3's gate (4096->11008) and down (11008->4096) projections through
-    sgq_linear_int4 at batches around the GEMV -> GEMM switch, as the library
-    dispatches them (sgq_linear_plan names the path), graph-timed over rotating
-    weight copies; rows 0..7 of each output checked against the oracle."""
+    sgq_linear_int4 at batches around the switches from the GEMV to the skinny
+    MFMA kernel and to the GEMM, as the library dispatches them
+    (sgq_linear_plan names the path), graph-timed over rotating weight copies;
+    the first (up to 8) rows of each output checked against the oracle."""
     import ctypes
 
     out = {}
@@ -437,17 +440,18 @@ def c3_crossover(pkg, dev, oracle, steps):
             copies = max(1, min(64, -(-300_000_000 // alg_bytes(c))))
             case = Case(pkg, c, dev, copies)
             ms = case.time_graph(steps, 10)
-            err = case.check(oracle, rows=np.r_[0:8])
+            err = case.check(oracle, rows=np.r_[0:min(M, 8)])
             path, ks = ctypes.c_int(), ctypes.c_int()
             lib.sgq_linear_plan(4, M, K, N, 128, 0, ctypes.byref(path), ctypes.byref(ks))
             rows.append({"M": M, "us_per_call": round(ms * 1e3, 3), "us_per_row": round(ms * 1e3 / M, 3),
-                         "path": ["gemv", "gemm_bf16x3", "gemm_fp32", "flat"][path.value], "k_splits": ks.value,
-                         "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "rel_err_vs_oracle_rows0_7": err})
+                         "path": PATH_NAMES[path.value], "k_splits": ks.value,
+                         "TFLOP_s": round(alg_flops(c) / ms / 1e9, 3), "rel_err_vs_oracle_first_rows": err})
             if err > 1e-5:
                 raise SystemExit(f"parity failure in bench (c3 crossover {name} M={M}): {err}")
             del case
-        first_gemm = next((r["M"] for r in rows if r["path"] != "gemv"), None)
-        out[name] = {"shape": f"{K}->{N}", "calls": rows, "gemm_from_M": first_gemm}
+        first_mfma = next((r["M"] for r in rows if r["path"] != "gemv"), None)
+        first_gemm = next((r["M"] for r in rows if r["path"] == "gemm_bf16x3"), None)
+        out[name] = {"shape": f"{K}->{N}", "calls": rows, "mfma_from_M": first_mfma, "gemm_from_M": first_gemm}
         log(f"[bench] c3 crossover {name}: " + ", ".join(f"M={r['M']} {r['us_per_call']}us {r['path']}" for r in rows))
     return out
 
