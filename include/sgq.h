@@ -87,16 +87,19 @@ int64_t sgq_int4_scale_count(int64_t rows, int64_t cols, int64_t group_size);
 int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64_t group_size);
 
 /* Workspace bytes needed by sgq_linear_int8 / sgq_linear_int4 for batch M.
- * Nonzero only for the GEMM (M > 16, except batches of up to 128 rows with
- * M * K * N <= 2^28, which run the GEMV) when its grid of output tiles (32 or
- * 64 rows by 128 columns for batches of up to 32 or 64 rows; else 128 rows by
- * 256 columns for INT8, 128 for INT4) is smaller than the GPU: K is then
- * split over workgroups, whose partial
- * tiles (KS * M * N floats) are summed by a second kernel in fixed order.
- * 0 otherwise (the GEMV and large GEMMs own whole outputs per workgroup), and
- * the workspace arguments may then be NULL/0.  The contents need no
- * initialisation and are overwritten by each call; calls that overlap in
- * time must not share one workspace.  16-byte alignment required. */
+ * Nonzero when a kernel splits K over workgroups, whose partial outputs (KS *
+ * M * N floats) are summed by a second kernel in fixed order: the GEMM (M >
+ * 16, except batches of up to 128 rows with M * K * N <= 2^28, which run the
+ * GEMV) when its grid of output tiles (32 or 64 rows by 128 columns for
+ * batches of up to 32 or 64 rows; else 128 rows by 256 columns for INT8, 128
+ * for INT4) is smaller than the GPU, and for INT4 the skinny MFMA kernel over
+ * weights too narrow to fill the GPU (M >= 4 with M * K * N >= 2^29) or, with
+ * 17..32 rows, over a K longer than 8192 rows.  The size is the largest any
+ * group size and device could need.  0 otherwise (the GEMV and the other
+ * kernels own whole outputs per workgroup), and the workspace arguments may
+ * then be NULL/0.  The contents need no initialisation and are overwritten by
+ * each call; calls that overlap in time must not share one workspace.
+ * 16-byte alignment required. */
 int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
 
 /* The kernel a forward of this shape runs and its K splits, on a device
@@ -104,10 +107,11 @@ int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
  * MI355X has 256, a partition fewer).  *path: 0 the GEMV, 1 the three-term
  * bf16 MFMA GEMM, 2 the fp32 MFMA GEMM (INT4 groups that are not a multiple
  * of 128), 3 the generic kernel of the flat INT4 layout, 4 the skinny bf16
- * MFMA kernel (INT4, 5..16 rows over a weight wide enough to fill the
- * device with workgroups of 32 or 64 columns).  *k_splits: 1, or
- * the number of workgroups sharing each output tile's K range (the GEMM on
- * grids smaller than the device).  sgq_linear_workspace_bytes sizes for the
+ * MFMA kernel (INT4, 5..32 rows over a weight wide enough to fill the
+ * device with workgroups of 32 or 64 columns; 4..32 rows over narrower
+ * weights with M * K * N >= 2^29, K split).  *k_splits: 1, or the number of
+ * workgroups sharing each output tile's K range (the GEMM on grids smaller
+ * than the device, the skinny kernel's K ranges).  sgq_linear_workspace_bytes sizes for the
  * largest device, so it covers every plan.  Host-only; this library's own
  * extension (the reference has no launch planning). */
 int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int* path,
@@ -201,7 +205,10 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
 /* Replaces quantization::quantized_matmul_int4 (src/quantization.cpp:199-206)
  * and nn::QuantizedLinear4Bit::forward (include/sovereigngrad/nn.hpp:994-996).
  * scales: the reference-layout scales (used by the FLAT layout); devscales:
- * the device scales written by sgq_quantize_int4/sgq_pack_int4 (TILED layout). */
+ * the device scales written by sgq_quantize_int4/sgq_pack_int4 (TILED layout).
+ * Dispatch (sgq_linear_plan): the skinny bf16 MFMA kernel for the batches of
+ * 4..32 rows it takes, else as sgq_linear_int8.  workspace:
+ * sgq_linear_workspace_bytes(4, M, K, N) bytes, else SGQ_ERR_WORKSPACE. */
 int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
                     int64_t workspace_bytes, void* stream);
@@ -209,7 +216,7 @@ int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
 /* sgq_linear_int4 without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
- * allocates nothing: the split-K partials of the GEMM go to a static device
+ * allocates nothing: the split-K partials (of the GEMM or the skinny kernel) go to a static device
  * array of 32 MiB per GPU (created when the library is loaded on that GPU
  * and held until the process ends).  Shapes whose sgq_linear_workspace_bytes
  * exceeds 32 MiB are refused with SGQ_ERR_UNSUPPORTED.  The stream must
@@ -230,9 +237,9 @@ int sgq_linear_int4_noalloc(const float* x, int64_t M, int64_t K, int64_t N, con
  * silu(v) = v / (1 + exp(-v)) as Tensor::silu (src/ops.cpp:561-575,
  * include/sovereigngrad/simd.hpp:103-108), * as mul (src/ops.cpp:239-253).
  * The two weights share K, N, scheme / group_size.  The batches the forward
- * runs on the GEMV (above), with the tiled layout, run both GEMVs in one launch (x read once per strip pair, no
- * intermediate in HBM); otherwise two projections (GEMM or flat INT4) and an
- * elementwise kernel.  Biases may be NULL.  workspace:
+ * runs on the GEMV or on the skinny MFMA kernel (above), with the tiled layout, run both weights in one launch (x read
+ * once per strip pair, no intermediate in HBM; a split K adds its reduce kernel); otherwise two projections (GEMM or
+ * flat INT4) and an elementwise kernel.  Biases may be NULL.  workspace:
  * sgq_swiglu_workspace_bytes(bits, M, K, N, group_size) bytes (group_size is
  * ignored for bits 8), else SGQ_ERR_WORKSPACE. */
 int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size);

@@ -61,14 +61,20 @@ QuantWs quant_ws(int64_t ngroups) {
 
 int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 32 : G); }
 
-// Only the GEMM uses a workspace, for split-K partial tiles when its tile
-// grid is smaller than the GPU (see gemm_plan); the GEMV owns whole columns.
-int64_t linear_ws_bytes(int, int64_t M, int64_t K, int64_t N) {
-    return linear_uses_gemv(M, K, N) ? 0 : gemm_workspace_bytes(M, K, N);
+// A workspace holds split-K partials: of the GEMM when its tile grid is
+// smaller than the GPU (see gemm_plan), of the skinny INT4 kernel over weights
+// too narrow to fill it (see skinny_plan); the GEMV owns whole columns.  The
+// size is the largest either could need on any device and for any group
+// size (neither is an argument here).
+int64_t linear_ws_bytes(int bits, int64_t M, int64_t K, int64_t N) {
+    const int64_t gemm = linear_uses_gemv(M, K, N) ? 0 : gemm_workspace_bytes(M, K, N);
+    const int64_t skinny = bits == 4 ? skinny_ws_bound(M, K, N, 1) : 0;
+    return gemm > skinny ? gemm : skinny;
 }
 
-int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void* workspace, int64_t workspace_bytes) {
-    const int64_t need = linear_ws_bytes(0, M, K, N);
+int check_linear_ws(const char* fn, int bits, int64_t M, int64_t K, int64_t N, const void* workspace,
+                    int64_t workspace_bytes) {
+    const int64_t need = linear_ws_bytes(bits, M, K, N);
     if (need == 0) return ok();
     if (!workspace || workspace_bytes < need)
         return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes", fn, (long long)need);
@@ -78,12 +84,21 @@ int check_linear_ws(const char* fn, int64_t M, int64_t K, int64_t N, const void*
 
 // Gated MLP workspace: nothing for the one-launch GEMV; otherwise
 // [up projection: M*N floats, 256-byte aligned][split-K partials of either GEMM].
-// The flat INT4 layout always takes the two-projection form.
-int64_t swiglu_ws_bytes(bool flat, int64_t M, int64_t K, int64_t N) {
+// The flat INT4 layout always takes the two-projection form.  Tiled INT4
+// batches the skinny kernel takes (one launch for both weights) need its
+// split-K partials of both weights; the size covers every device (a device
+// with fewer CUs may run the GEMV or GEMM form instead).
+int64_t swiglu_ws_bytes(int bits, bool flat, int64_t M, int64_t K, int64_t N, int64_t group_size) {
+    int64_t skinny = 0;
+    if (bits == 4 && !flat && K > 0)
+        skinny = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, group_size), kMaxCus), M, N, 2);
+    int64_t other = 0;
     // The one-launch GEMV form takes the batches the plain forward runs on the GEMV.
-    if (!flat && linear_uses_gemv(M, K, N) && K > 0) return 0;
-    const int64_t split = (!flat && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
-    return align_up(M * N * 4) + split;
+    if (flat || !linear_uses_gemv(M, K, N) || K == 0) {
+        const int64_t split = (!flat && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
+        other = align_up(M * N * 4) + split;
+    }
+    return skinny > other ? skinny : other;
 }
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
@@ -225,11 +240,14 @@ int linear_int4(const char* fn, const float* x, int64_t M, int64_t K, int64_t N,
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
     if (!forward_fits(4, M, K, N, g.G))
         return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
-    if (linear_uses_gemv(M, K, N)) {
+    const int st = check_linear_ws(fn, 4, M, K, N, workspace, workspace_bytes);
+    if (st != SGQ_OK) return st;
+    const SkinnyPlan sp = skinny_plan(M, K, g, device_cus(s));
+    if (sp.C > 0) {
+        SGQ_HIP(launch_skinny_i4(x, M, K, N, 1, &packed, &devscales, &bias, g, sp, y, workspace, s), "skinny_i4");
+    } else if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
-        const int st = check_linear_ws(fn, M, K, N, workspace, workspace_bytes);
-        if (st != SGQ_OK) return st;
         SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
     }
     return ok();
@@ -295,7 +313,7 @@ int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_siz
 int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size) {
     if (bad_dims(M, K) || bad_dims(K, N) || bad_dims(M, N) || (bits != 8 && bits != 4)) return -1;
     if (M == 0 || N == 0) return 0;
-    return swiglu_ws_bytes(bits == 4 && !I4Geom(K, N, group_size).tiled, M, K, N);
+    return swiglu_ws_bytes(bits, bits == 4 && !I4Geom(K, N, group_size).tiled, M, K, N, group_size);
 }
 
 int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream) {
@@ -503,7 +521,7 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
-        const int st = check_linear_ws("sgq_linear_int8", M, K, N, workspace, workspace_bytes);
+        const int st = check_linear_ws("sgq_linear_int8", 8, M, K, N, workspace, workspace_bytes);
         if (st != SGQ_OK) return st;
         SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, workspace, s), "gemm_i8");
     }
@@ -545,7 +563,7 @@ int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: bad scheme", fn);
     if (M == 0 || N == 0) return ok();
     if (!h) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null output", fn);
-    const int64_t need = swiglu_ws_bytes(false, M, K, N);
+    const int64_t need = swiglu_ws_bytes(8, false, M, K, N, 0);
     if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
         return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes, 16-byte aligned", fn, (long long)need);
     float* u = (float*)workspace;
@@ -586,7 +604,7 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
     if (M == 0 || N == 0) return ok();
     if (!h) return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: null output", fn);
     const I4Geom g(K, N, group_size);
-    const int64_t need = swiglu_ws_bytes(!g.tiled, M, K, N);
+    const int64_t need = swiglu_ws_bytes(4, !g.tiled, M, K, N, group_size);
     if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
         return fail(SGQ_ERR_WORKSPACE, "%s: workspace needs %lld bytes, 16-byte aligned", fn, (long long)need);
     float* u = (float*)workspace;
@@ -610,6 +628,16 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and devscales must be 16-byte aligned", fn);
     if (!forward_fits(4, M, K, N, g.G))
         return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
+    // The same path as two forward calls of these shapes, so the gate and up
+    // sums are the plain forward's.
+    const SkinnyPlan sp = skinny_plan(M, K, g, device_cus(s));
+    if (sp.C > 0) {
+        const void* pk[2] = {packed_gate, packed_up};
+        const float* ds[2] = {devscales_gate, devscales_up};
+        const float* bs[2] = {bias_gate, bias_up};
+        SGQ_HIP(launch_skinny_i4(x, M, K, N, 2, pk, ds, bs, g, sp, h, workspace, s), "skinny_i4");
+        return ok();
+    }
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i4(x, M, K, N, packed_gate, devscales_gate, bias_gate, packed_up, devscales_up,
                                       bias_up, g, h, s),

@@ -34,6 +34,13 @@ namespace sgq {
 
 constexpr int64_t kPadK = 16;  // rows are padded to a multiple of this
 
+// Compute units the launch heuristics plan for: the count of the device a
+// stream runs on (a partition of an MI355X reports its own share), at most
+// kMaxCus, the full MI355X.  Split-K workspaces are sized for kMaxCus, an upper
+// bound for every smaller count: the number of K splits never grows as the CU
+// count shrinks.
+constexpr int64_t kMaxCus = 256;
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Division of n in [0, 2^31) by a divisor d >= 1 fixed at launch, as a
@@ -96,29 +103,102 @@ inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
     return M <= kGemvMaxM || (M <= kGemvRowsMax && M * K * N <= kGemvSmallWork);
 }
 
-// Batches of kSkinnyMinRows..kGemvMaxM rows over wide INT4 weights run on the
-// bf16 matrix cores (k_skinny3) instead of the GEMV: column blocks of 16 per
-// workgroup (at most cmax; 2*C strips must share a scale column), or 0 where
-// the GEMV is the faster path.  The GEMV's cost grows with the rows (one FMA
-// per code and row), the MFMA form's hardly at all, but its workgroups own
-// 16*C columns each, so it needs a wide weight to fill the GPU (at least 5/8
-// of a workgroup per CU with C = 4 or 2) and a K long enough to amortise its
-// split and LDS reduction.  Measured on MI355X (INT4 g128, graphs of 100
-// calls, GEMV -> MFMA): 4096->11008 at 5 / 8 / 16 rows 19.0 / 19.9 / 31.0 ->
-// 15.4 / 15.9 / 17.0 us; 2048->6144 at 8 / 16 rows 8.4 / 12.9 -> 7.4 / 8.4;
-// 4096->14336 at 16 rows 37.9 -> 17.4; 8192->28672 at 16 rows 130 -> 59.
-// Kept on the GEMV: 4 rows (4096->11008 12.8 vs 15.3 us), narrow weights
-// (N <= 4096: 128-256 workgroups of 16 columns, no gain), K = 1024
-// (1024->5120 at 8 rows 5.9 vs 7.0 us).
-constexpr int64_t kSkinnyMinRows = 5;
-constexpr int64_t kSkinnyMinK = 2048;
-constexpr int64_t kSkinnyMaxK = (int64_t)1 << 24;  // 16 rows of x addressed with 32-bit offsets
-inline int skinny_blocks(int64_t M, int64_t K, const I4Geom& g, int64_t cus, int cmax) {
-    if (M < kSkinnyMinRows || M > kGemvMaxM || K < kSkinnyMinK || K > kSkinnyMaxK || !g.tiled || g.spc % 2 != 0)
-        return 0;
-    for (int c = cmax; c >= 2; c /= 2)
-        if (g.spc % (2 * c) == 0 && g.NS / (2 * c) * 8 >= 5 * cus) return c;
-    return 0;
+// Batches of a few to 32 rows over INT4 weights run on the bf16 matrix cores
+// (k_skinny3) instead of the GEMV or the GEMM.  The GEMV's cost grows with
+// the rows (one FMA per code and row), the MFMA form's hardly at all.  Its
+// workgroups own C column blocks of 16 (2C strips must share a scale column,
+// so one split of x * s serves them all):
+//  - wide weights (at least 5/8 of a workgroup per CU with C = 4 or 2) give
+//    each workgroup all of K.  Measured on MI355X (INT4 g128, graphs of 100
+//    calls, GEMV -> MFMA): 4096->11008 at 5 / 8 / 16 rows 19.0 / 19.9 / 31.0
+//    -> 15.4 / 15.9 / 17.0 us; 2048->6144 at 8 / 16 rows 8.4 / 12.9 -> 7.4 /
+//    8.4; 4096->14336 at 16 rows 37.9 -> 17.4.  Four rows stay on the GEMV
+//    (4096->11008 12.8 vs 15.3 us), as does K below 2048.
+//  - narrower weights split K into S ranges (a power of two, enough
+//    workgroups to fill the device, at least kSkinnyMinRangeBlocks 32-row k
+//    blocks each).  Every workgroup of the GEMV or of the unsplit kernel
+//    reads all M rows of x, which for M >= 4 is more than its codes; a range
+//    reads its own slice.  The partial sums go to the caller's workspace and
+//    a second kernel adds them in range order.
+constexpr int64_t kSkinnyMinRows = 5;        // wide weights
+constexpr int64_t kSkinnyNarrowMinRows = 4;  // split K
+constexpr int64_t kSkinnyMaxRows = 32;       // two row blocks of 16
+constexpr int64_t kSkinnyMinK = 2048;        // wide weights
+constexpr int64_t kSkinnyNarrowMinK = 1024;  // split K
+constexpr int64_t kSkinnyMaxK = (int64_t)1 << 24;  // strip offsets (2C strips of Kpad rows) in 32 bits
+constexpr int kSkinnyMaxSplits = 16;
+constexpr int64_t kSkinnySB = 128;            // rows per super-block (the kernel's unit of K)
+constexpr int64_t kSkinnyRangeRows = 8192;    // rows of a K range (its scales are kept in LDS)
+constexpr int64_t kSkinnyMinRangeBlocks = 8;  // super-blocks of a split K range, at least
+struct SkinnyPlan {
+    int C = 0;     // column blocks of 16 per workgroup; 0: not the skinny kernel
+    int S = 1;     // K ranges (1: no split, no workspace)
+    int MB = 1;    // row blocks of 16
+    int form = 1;  // 0: k_skinny3 (whole K, one row block), 1: k_skinny_sb (super-blocks)
+};
+// Narrow weights split K only from this much work (M * K * N; measured:
+// 16 x 11008 -> 4096 24 vs 32 us on the GEMV, 32 x 4096 -> 4096 21 vs 23 us on
+// the GEMM; 16 x 4096 -> 4096 15 vs 14 us and 2048 -> 2048 at 4..16 rows
+// 12 vs 4-6 us stay on the GEMV).
+constexpr int64_t kSkinnyNarrowWork = (int64_t)1 << 29;
+// K ranges for ncg column groups of a K of nsb super-blocks on cus CUs:
+// narrow weights split to fill the device (ranges of at least
+// kSkinnyMinRangeBlocks super-blocks); every range holds at most
+// kSkinnyRangeRows rows.  0: K is too long for kSkinnyMaxSplits ranges.
+inline int skinny_splits(int64_t ncg, int64_t nsb, int64_t cus, bool narrow) {
+    int S = 1;
+    if (narrow) {
+        while (ncg * S < cus && S < kSkinnyMaxSplits) S *= 2;
+        while (S > 1 && nsb < kSkinnyMinRangeBlocks * S) S /= 2;
+    }
+    while (ceil_div(nsb, S) * kSkinnySB > kSkinnyRangeRows) {
+        if (S >= kSkinnyMaxSplits) return 0;
+        S *= 2;
+    }
+    return S;
+}
+inline SkinnyPlan skinny_plan(int64_t M, int64_t K, const I4Geom& g, int64_t cus) {
+    SkinnyPlan p;
+    // x is addressed through 32-bit buffer offsets: M * K * 4 bytes <= 2^30.
+    if (M < 1 || M > kSkinnyMaxRows || K < 1 || K > kSkinnyMaxK || M * K > ((int64_t)1 << 28) || !g.tiled ||
+        g.spc % 2 != 0)
+        return p;
+    const int MB = M > 16 ? 2 : 1;
+    const int64_t nsb = ceil_div(g.Kpad, kSkinnySB);
+    for (int c = 4; c >= 2; c /= 2)
+        if (g.spc % (2 * c) == 0 && g.NS / (2 * c) * 8 >= 5 * cus) {
+            if (M < kSkinnyMinRows || K < kSkinnyMinK) return p;
+            // One row block: the whole-K form (any K).  Two: super-blocks,
+            // K split only as far as the scales of a range fit LDS.
+            p.form = MB == 1 ? 0 : 1;
+            p.S = MB == 1 ? 1 : skinny_splits(g.NS / (2 * c), nsb, cus, false);
+            p.C = p.S > 0 ? c : 0;
+            p.MB = MB;
+            if (p.C == 0) p.S = 1;
+            return p;
+        }
+    const int c = g.spc % 8 == 0 ? 4 : (g.spc % 4 == 0 ? 2 : 0);
+    if (c == 0 || M < kSkinnyNarrowMinRows || K < kSkinnyNarrowMinK) return p;
+    if (M * K * g.N < kSkinnyNarrowWork) return p;
+    p.S = skinny_splits(g.NS / (2 * c), nsb, cus, true);
+    p.C = p.S > 1 ? c : 0;  // too short to split (or too long for the ranges): not this kernel
+    p.MB = MB;
+    if (p.C == 0) p.S = 1;
+    return p;
+}
+// Workspace of a skinny launch with NG weights: the K ranges' partial sums.
+inline int64_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t N, int NG) {
+    return p.C > 0 && p.S > 1 ? (int64_t)NG * p.S * M * N * 4 : 0;
+}
+// The largest such workspace over every group size on the largest device
+// (the split count never grows as the CU count falls).
+inline int64_t skinny_ws_bound(int64_t M, int64_t K, int64_t N, int NG) {
+    int64_t ws = 0;
+    for (int64_t G : {16, 32, 64, 128}) {
+        const int64_t w = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, G), kMaxCus), M, N, NG);
+        if (w > ws) ws = w;
+    }
+    return ws;
 }
 
 // ---- launchers (return hipError_t of the launch) ----------------------
@@ -161,6 +241,13 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
                           bool per_tensor, const float* bias, float* y, hipStream_t s);
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
+// Skinny MFMA forward (plan p from skinny_plan, p.C > 0) of ng (1 or 2) tiled
+// INT4 weights of one shape on one input: ng == 1 writes y = x * W + bias,
+// ng == 2 the gated MLP h = silu(x * Wg + bg) * (x * Wu + bu).  With split K,
+// ws holds skinny_ws_bytes(p, M, N, ng) bytes (16-byte aligned).
+hipError_t launch_skinny_i4(const float* x, int64_t M, int64_t K, int64_t N, int ng, const void* const* packed,
+                            const float* const* devscales, const float* const* bias, const I4Geom& g,
+                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s);
 // nw (1..3) tiled INT4 weights of one shape [K, N] side by side on one input:
 // weight w writes y[m * ldy + w * N + n] (+ res at the same index when res is
 // set).  gamma (optional): the input is rms_norm(x, gamma, eps), applied
@@ -177,12 +264,6 @@ struct GemmPlan {
 struct GemmTile {
     int64_t bm, bn, per_cu;  // tile rows and columns, workgroups resident per CU
 };
-// Compute units the launch heuristics plan for: the count of the device a
-// stream runs on (a partition of an MI355X reports its own share), at most
-// kMaxCus, the full MI355X.  Split-K workspaces are sized for kMaxCus, an upper
-// bound for every smaller count: the number of K splits never grows as the CU
-// count shrinks.
-constexpr int64_t kMaxCus = 256;
 int device_cus(hipStream_t s);
 GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus);
 // Tile of the three-term GEMM for a code width and batch: 32 or 64 rows by
@@ -203,8 +284,9 @@ hipError_t launch_linear_i4_flat(const float* x, int64_t M, int64_t K, int64_t N
                                  const float* scales, int64_t G, const float* bias, float* y, hipStream_t s);
 
 // Gated MLP: h = silu(x*Wg + bg) * (x*Wu + bu).  The GEMV form (M <= kGemvMaxM)
-// runs both weights in one launch; larger batches run two projections and
-// launch_silu_mul (h = silu(h) * u, elementwise over n floats).
+// runs both weights in one launch (as does the skinny kernel, launch_skinny_i4
+// with ng == 2); larger batches run two projections and launch_silu_mul
+// (h = silu(h) * u, elementwise over n floats).
 hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
                                  const float* scales_g, const float* bias_g, const void* packed_u,
                                  const float* scales_u, const float* bias_u, bool per_tensor, float* h,

@@ -71,18 +71,19 @@ __device__ __forceinline__ float half_hi(uint32_t p) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(p >> 16));
 }
 
-// One INT4 output summed in k order as code * (x * s) (NORM: x * (gamma * s)),
-// reading strip j of the strip-major layout, whose dword k is row k.  The
-// GEMV falls back to this when its offset-corrected sum is not finite (an
-// infinite or NaN input, or an overflow), so that infinities and NaNs come
-// out as in the reference's x . (q * s) rather than as inf - inf.
+// One INT4 output summed in k order over rows [k0, k1) as code * (x * s)
+// (NORM: x * (gamma * s)), reading strip j of the strip-major layout, whose
+// dword k is row k.  The GEMV falls back to this when its offset-corrected
+// sum is not finite (an infinite or NaN input, or an overflow), so that
+// infinities and NaNs come out as in the reference's x . (q * s) rather than
+// as inf - inf; the skinny MFMA kernel likewise over its K range.
 template <bool NORM>
 __device__ float i4_column_exact(const uint4* W, const float* SC, int j, int e, int spc, int Kpad, int RQ,
-                                 const float* xrow, const float* gamma, int K) {
+                                 const float* xrow, const float* gamma, int k0, int k1) {
     const uint32_t* wd = reinterpret_cast<const uint32_t*>(W + (int64_t)j * RQ);
     const float* sc = SC + (int64_t)(j / spc) * Kpad;
     float acc = 0.0f;
-    for (int k = 0; k < K; ++k) {
+    for (int k = k0; k < k1; ++k) {
         const int q = ((int)(wd[k] << (28 - 4 * e))) >> 28;
         const float s = NORM ? gamma[k] * sc[k] : sc[k];
         acc = fmaf((float)q, xrow[k] * s, acc);
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
             auto i4_total = [&](float t, const uint4* Wg, const float* SCg) {
                 if (!isfinite(t))
                     t = i4_column_exact<NORM>(Wg, SCg, j0 + e / SW, e % SW, mode, Kpad, RQ,
-                                              a.x + (int64_t)(m0 + m) * K, a.gamma, K);
+                                              a.x + (int64_t)(m0 + m) * K, a.gamma, 0, K);
                 return t;
             };
             if constexpr (MIX) r = i4_total(r, NG == 1 ? Wm : a.W[0], NG == 1 ? SCm : a.SC[0]);
@@ -1002,16 +1003,20 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 }
 
 // ---------------------------------------------------------------------------
-// Skinny INT4 forward on the bf16 matrix cores: batches of 5..16 rows over
-// wide weights (src/quantization.cpp:199-206 for those shapes).
+// Skinny INT4 forward on the bf16 matrix cores: batches of a few to 32 rows
+// (src/quantization.cpp:199-206 for those shapes).
 //
-// The batch is the 16 rows of one v_mfma_f32_16x16x32_bf16 (rows past M are
-// zeros), with the three-term split of k_gemm3: A = x * s as three bf16
-// planes, B = codes (exact in bf16), fp32 accumulation.  A workgroup owns C
-// column blocks of 16 (2C strips of one scale column, so one x * s split
-// serves all of them) over all of K; its NW wavefronts take 32-row k blocks
-// in turn and are summed through LDS at the end.  No workgroup needs another's
-// result, as in the GEMV.
+// Each 16 rows of the batch are the rows of one v_mfma_f32_16x16x32_bf16
+// (rows past M are zeros; MB such row blocks share every B operand), with the
+// three-term split of k_gemm3: A = x * s as three bf16 planes, B = codes
+// (exact in bf16), fp32 accumulation.  A workgroup owns C column blocks of 16
+// (2C strips of one scale column, so one x * s split serves all of them) over
+// all of K, or over one of S equal ranges of 32-row k blocks (split K, for
+// weights too narrow to fill the device: the partial sums go to a workspace
+// and k_skinny_reduce adds them in split order).  Its NW wavefronts take the
+// k blocks of its range in turn and are summed through LDS at the end.  The
+// order of every sum depends on the K range and NW only, not on C, MB or the
+// number of weights.
 //
 // B operand straight from the strip layout, without LDS: a 32-row k block of
 // a strip is 128 bytes, dword r = row r's eight nibbles.  Lane l of a 16-lane
@@ -1074,14 +1079,22 @@ struct SkinnyArgs {
     const float* SC[2];
     const float* bias[2];
     int spc, Kpad, RQ;
-    FastDiv wpc;  // workgroups per scale column
+    FastDiv wpc;  // workgroups (column groups) per scale column
     float* y;     // [M, N]
+    float* part;  // split K: [NG][2^slog][M][N] partial sums
     int nblk;     // grid size
+    int slog;     // log2 of the number of K ranges
+    int sbs;      // super-blocks (128 rows) per K range
 };
 
-// NG == 2: the gated MLP, gate and up blocks of the same columns in one
-// workgroup, h = silu(gate + bias) * (up + bias2).  XA: x rows are 16-byte
-// aligned and K % 4 == 0 (float4 loads); otherwise one float per load.
+// The whole-K form for one row block (5..16 rows over wide weights, no K
+// split): NW = 16 wavefronts take 32-row k blocks in turn, U of them per
+// batch of loads, and every load of a batch is issued before the first is
+// used.  Lane (g, e) of strip j loads one dword, row 8g + e of its strip in
+// k block kb, and an 8x8 nibble transpose leaves it with rows 8g .. 8g + 7 of
+// column e (its B operand); x and the scales are loaded per k block.  NG == 2:
+// the gated MLP, h = silu(gate + bias) * (up + bias2).  XA: x rows are
+// 16-byte aligned and K % 4 == 0 (float4 loads); otherwise one float per load.
 template <int NW, int U, int C, int NG, bool XA>
 __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1195,7 +1208,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                 // a non-finite total as the reference's k-order sum.
                 if (!isfinite(s))
                     s = i4_column_exact<false>(a.W[q], a.SC[q], strip, el, a.spc, a.Kpad, a.RQ, a.x + (int64_t)m * K,
-                                               nullptr, K);
+                                               nullptr, 0, K);
                 if (a.bias[q]) s = s + a.bias[q][col];
             }
             o[q][i] = s;
@@ -1211,6 +1224,267 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
             if constexpr (NG == 2) r0 = silu_f32(o[0][i]) * o[1][i];
             a.y[(int64_t)m * a.N + col] = r0;
         }
+    }
+}
+
+
+// The super-block form (any row blocks, optional K split).  NG == 2: the gated MLP, gate and up blocks of the same columns in one
+// workgroup, h = silu(gate + bias) * (up + bias2) (split K: in
+// k_skinny_reduce).  XA: x rows are 16-byte aligned and K % 4 == 0 (float4
+// loads); otherwise one float per load.  MB: row blocks of 16 (M <= 16 MB).
+//
+// The K range is walked in super-blocks of 128 rows, wavefront w taking
+// super-blocks w, w + NW, ...  In a super-block, lane (g, e) of strip j loads
+// rows 32g + 4e .. 32g + 4e + 3 of its strip (16 bytes, all eight columns) and
+// x rows 32g .. 32g + 31 of its batch row; dword i of the codes transposed
+// across the eight lanes e gives column e at rows 32g + 4e' + i (e' = 0..7),
+// the B operand of MFMA i, and component i of the eight x quads the matching
+// A operand.  The scales of the workgroup's K range sit in LDS (read once,
+// coalesced); the next super-block's codes and x are loaded while the current
+// one is computed.
+template <int NW, int C, int NG, bool XA, int MB>
+struct SkinnyRegs {
+    uint4 w[NG][C];      // 4 rows x 8 columns of each strip
+    float4 xq[MB][8];    // 32 consecutive k of each batch row
+};
+
+template <int NW, int C, int NG, bool XA, int MB, bool SPLIT>
+__global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
+    const int K = a.K;
+    // Workgroup v: K range v % S of column group v / S (the ranges of one
+    // column group are neighbours, so they share an XCD's L2 for the scales).
+    const int v = xcd_swizzle(blockIdx.x, a.nblk);
+    const int split = SPLIT ? (v & ((1 << a.slog) - 1)) : 0;
+    const int cgrp = SPLIT ? (v >> a.slog) : v;
+    const int blk0 = cgrp * C;  // first column block
+    const int sc = a.wpc.div(cgrp);
+    const int nsb = (a.Kpad + kSkinnySB - 1) / kSkinnySB;
+    const int sb_lo = SPLIT ? split * a.sbs : 0;
+    const int sb_hi = SPLIT ? min(nsb, sb_lo + a.sbs) : nsb;
+    const int row0 = sb_lo * kSkinnySB;  // first row of the range
+
+    // The range's scales (rows row0 .. row0 + rows - 1 of the scale column,
+    // zeros past Kpad) are loaded ahead of the first super-block's codes and
+    // x, so that storing them into LDS waits for them alone.
+    constexpr int SCI = kSkinnyRangeRows / 4 / (NW * 64);  // float4 per thread and weight
+    static_assert(SCI * NW * 64 * 4 == kSkinnyRangeRows, "the scale rows spread evenly");
+    __shared__ float4 ssc[NG][kSkinnyRangeRows / 4];
+    const int rows4 = (sb_hi - sb_lo) * (kSkinnySB / 4);
+    float4 sreg[NG][SCI];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.SC[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
+#pragma unroll
+        for (int it = 0; it < SCI; ++it) {
+            const int r4 = threadIdx.x + it * NW * 64;
+            sreg[q][it] = buf_load4f<true>(rS, r4 < rows4 ? (row0 + 4 * r4) * 4 : kOobOff, 0);
+        }
+    }
+
+    __amdgpu_buffer_rsrc_t rW[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q)
+        rW[q] = make_rsrc(a.W[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
+    int wv[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (32 * g + 4 * e) * 4;
+    bool row_live[MB];
+    int xrow[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        row_live[b] = n + 16 * b < a.M;
+        xrow[b] = row_live[b] ? (n + 16 * b) * K * 4 : 0;
+    }
+    const NibbleT tp = nibble_t(e);
+
+    // Loads of super-block sb; one past the range reads x as zeros (and codes
+    // that are then multiplied by zero).
+    auto load = [&](SkinnyRegs<NW, C, NG, XA, MB>& r, int sb) {
+        const bool in = sb < sb_hi;
+#pragma unroll
+        for (int q = 0; q < NG; ++q)
+#pragma unroll
+            for (int c = 0; c < C; ++c) r.w[q][c] = buf_load16(rW[q], wv[c], sb * (kSkinnySB * 4));
+        const int k0 = sb * kSkinnySB + 32 * g;
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int kk = k0 + 4 * t;
+                if constexpr (XA) {
+                    r.xq[b][t] = buf_load4f<true>(rX, in && row_live[b] && kk < K ? xrow[b] + kk * 4 : kOobOff, 0);
+                } else {
+                    // One float per load from any 4-byte address; the row's
+                    // tail and the rows past M read as zeros by their offset.
+                    const int base = in && row_live[b] ? xrow[b] + kk * 4 : kOobOff;
+                    float f[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        f[i] = __uint_as_float(
+                            __builtin_amdgcn_raw_buffer_load_b32(rX, kk + i < K ? base + 4 * i : kOobOff, 0, 0));
+                    r.xq[b][t] = make_float4(f[0], f[1], f[2], f[3]);
+                }
+            }
+    };
+
+    floatx4 acc[NG][MB][C];
+#pragma unroll
+    for (int q = 0; q < NG; ++q)
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int c = 0; c < C; ++c) acc[q][b][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB>& r, int sb) {
+        // A super-block past the range has x = 0; its scale reads stay inside
+        // the range's LDS rows.
+        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + 8 * g;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            float4 s4[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) s4[t] = ssc[q][lr + t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint4 ah[MB], am[MB], al[MB];
+#pragma unroll
+                for (int b = 0; b < MB; ++b) {
+                    float xs[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) xs[t] = f4get(r.xq[b][t], i) * f4get(s4[t], i);
+                    split3(xs, ah[b], am[b], al[b]);
+                }
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    const uint32_t wd = i == 0 ? r.w[q][c].x : (i == 1 ? r.w[q][c].y : (i == 2 ? r.w[q][c].z : r.w[q][c].w));
+                    const bf16x8 bq = nibbles_bf16x16(nibble_transpose8(wd, tp));
+#pragma unroll
+                    for (int b = 0; b < MB; ++b) {
+                        acc[q][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[b]), bq,
+                                                                               acc[q][b][c], 0, 0, 0);
+                        acc[q][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am[b]), bq,
+                                                                               acc[q][b][c], 0, 0, 0);
+                        acc[q][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al[b]), bq,
+                                                                               acc[q][b][c], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+
+    // Two register sets: the loads of the next super-block are in flight
+    // while the current one is computed.
+    SkinnyRegs<NW, C, NG, XA, MB> ra, rb;
+    int sb = sb_lo + wave;
+    load(ra, sb);
+#pragma unroll
+    for (int q = 0; q < NG; ++q)
+#pragma unroll
+        for (int it = 0; it < SCI; ++it) {
+            const int r4 = threadIdx.x + it * NW * 64;
+            if (r4 < rows4) ssc[q][r4] = sreg[q][it];
+        }
+    lds_barrier();  // the scales are in LDS (the codes and x loads stay in flight)
+    for (; sb < sb_hi; sb += 2 * NW) {
+        load(rb, sb + NW);
+        compute(ra, sb);
+        load(ra, sb + 2 * NW);
+        compute(rb, sb + NW);
+    }
+
+    // Accumulator element r of lane l is output row 4 * (l >> 4) + r (of its
+    // row block) of column lane l & 15 of its column block.  The wavefronts'
+    // partial tiles are summed in wavefront order (deterministic), one weight
+    // and row block at a time through LDS; thread t keeps output t
+    // (t + NW * 64, ...) of each.
+    constexpr int OPT = (256 * C + NW * 64 - 1) / (NW * 64);
+    __shared__ float red[NW][C][4][64];
+    const int klo = row0, khi = min(K, sb_hi * kSkinnySB);
+    float o[NG][MB][OPT];
+#pragma unroll
+    for (int q = 0; q < NG; ++q)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            if (q > 0 || b > 0) __syncthreads();  // every thread has read the previous tile's partials
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave][c][r][lane] = acc[q][b][c][r];
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < OPT; ++i) {
+                const int t = threadIdx.x + i * NW * 64;
+                const int c = t >> 8, mr = (t >> 4) & 15, sl = t & 15;
+                const int m = mr + 16 * b;
+                const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
+                const int col = 8 * strip + el;
+                float s = 0.0f;
+                if (t < 256 * C && m < a.M && col < a.N) {
+#pragma unroll
+                    for (int w2 = 0; w2 < NW; ++w2) s += red[w2][c][mr & 3][16 * (mr >> 2) + sl];
+                    s *= 0.0625f;  // the codes entered as 16q
+                    // h + m + l turns an infinite x * s into inf - inf: recompute
+                    // a non-finite total as the reference's k-order sum.
+                    if (!isfinite(s))
+                        s = i4_column_exact<false>(a.W[q], a.SC[q], strip, el, a.spc, a.Kpad, a.RQ,
+                                                   a.x + (int64_t)m * K, nullptr, klo, khi);
+                    if (!SPLIT && a.bias[q]) s = s + a.bias[q][col];
+                }
+                o[q][b][i] = s;
+            }
+        }
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < OPT; ++i) {
+            const int t = threadIdx.x + i * NW * 64;
+            const int c = t >> 8, m = ((t >> 4) & 15) + 16 * b, sl = t & 15;
+            const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
+            if (t < 256 * C && m < a.M && col < a.N) {
+                const int64_t at = (int64_t)m * a.N + col;
+                if constexpr (SPLIT) {
+                    const int64_t MN = (int64_t)a.M * a.N;
+#pragma unroll
+                    for (int q = 0; q < NG; ++q) a.part[((int64_t)q << a.slog | split) * MN + at] = o[q][b][i];
+                } else {
+                    float r0 = o[0][b][i];
+                    if constexpr (NG == 2) r0 = silu_f32(o[0][b][i]) * o[1][b][i];
+                    a.y[at] = r0;
+                }
+            }
+        }
+}
+
+// The skinny kernel's K ranges added in range order, plus the bias; NG == 2:
+// h = silu(gate + bias) * (up + bias2).  part is [NG][S][M*N].
+template <int NG>
+__global__ __launch_bounds__(kThreads) void k_skinny_reduce(const float* __restrict__ part, int S, int64_t MN, int N,
+                                                            const float* __restrict__ bias,
+                                                            const float* __restrict__ bias2, float* __restrict__ y) {
+    for (int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; o < MN; o += (int64_t)gridDim.x * blockDim.x) {
+        float r[NG];
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            float t[kSkinnyMaxSplits];
+#pragma unroll
+            for (int sp = 0; sp < kSkinnyMaxSplits; ++sp)  // all loads first
+                t[sp] = sp < S ? part[((int64_t)q * S + sp) * MN + o] : 0.0f;
+            float v = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < kSkinnyMaxSplits; ++sp)
+                if (sp < S) v += t[sp];
+            const float* bq = q == 0 ? bias : bias2;
+            if (bq) v = v + bq[o % N];
+            r[q] = v;
+        }
+        if constexpr (NG == 2)
+            y[o] = silu_f32(r[0]) * r[1];
+        else
+            y[o] = r[0];
     }
 }
 
@@ -1388,17 +1662,19 @@ GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad,
     return a;
 }
 
-// Wavefronts per workgroup of k_skinny3 (each takes every 16th k block) and
-// k blocks a wavefront keeps in flight (U per batch of loads).
-constexpr int kSkinnyWaves = 16;
+// Wavefronts per workgroup of k_skinny_sb (each takes every 8th super-block
+// of its range) and of k_skinny3 (every 16th 32-row k block); the summation
+// order depends on them, so each is the same for every plan of its form.
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyWholeKWaves = 16;
 
-// One k_skinny3 launch with C column blocks per workgroup (C from
-// skinny_blocks); NG weights of equal shape with their devscales and biases.
-template <int C, int NG>
+// One k_skinny3 launch (and, with split K, its reduce) for the plan's C and
+// MB; NG weights of equal shape with their devscales and biases.
+template <int C, int NG, int MB, bool XA>
 hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* const* packed,
-                         const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
-                         hipStream_t s) {
-    constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
+                         const float* const* devscales, const float* const* bias, const I4Geom& g, int form, int S,
+                         float* y, float* part, hipStream_t s) {
+    if (form == 0 && S != 1) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.x = x;
     a.M = (int)M;
@@ -1414,29 +1690,76 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     a.RQ = (int)g.RQ;
     a.wpc = FastDiv((uint32_t)(g.spc / (2 * C)));
     a.y = y;
-    a.nblk = (int)(g.NS / (2 * C));  // skinny_blocks: 2C divides spc, which divides NS
-    if (x_aligned4(x, K))
-        k_skinny3<kSkinnyWaves, U, C, NG, true><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    a.part = part;
+    int slog = 0;
+    while ((1 << slog) < S) ++slog;
+    a.slog = slog;
+    a.sbs = (int)ceil_div(ceil_div(g.Kpad, kSkinnySB), S);
+    a.nblk = (int)(g.NS / (2 * C)) << slog;  // skinny_plan: 2C divides spc, which divides NS
+    if (form == 0) {
+        if constexpr (MB == 1) {
+            constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
+            k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidValue;
+    }
+    if (S > 1)
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
     else
-        k_skinny3<kSkinnyWaves, U, C, NG, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    if (S > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t MN = M * N;
+        int64_t blocks = ceil_div(MN, kThreads);
+        if (blocks > 4096) blocks = 4096;
+        k_skinny_reduce<NG><<<(unsigned)blocks, kThreads, 0, s>>>(part, S, MN, (int)N, bias[0],
+                                                                  NG == 2 ? bias[1] : nullptr, y);
+    }
     return hipGetLastError();
 }
 
 template <int NG>
-hipError_t skinny_dispatch(int c, const float* x, int64_t M, int64_t K, int64_t N, const void* const* packed,
-                           const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
-                           hipStream_t s) {
-    if (c == 4) return skinny_launch<4, NG>(x, M, K, N, packed, devscales, bias, g, y, s);
-    if (c == 2) return skinny_launch<2, NG>(x, M, K, N, packed, devscales, bias, g, y, s);
-    return hipErrorInvalidValue;
+hipError_t skinny_dispatch(const SkinnyPlan& p, const float* x, int64_t M, int64_t K, int64_t N,
+                           const void* const* packed, const float* const* devscales, const float* const* bias,
+                           const I4Geom& g, float* y, float* part, hipStream_t s) {
+    // The super-block form of the gated MLP, and two row blocks of
+    // unaligned x, keep two column blocks per workgroup, within the register
+    // budget (C does not change the order of any sum).
+    if (p.C != 2 && p.C != 4) return hipErrorInvalidValue;
+#define SGQ_SKINNY(C_, MB_, XA_) \
+    return skinny_launch<C_, NG, MB_, XA_>(x, M, K, N, packed, devscales, bias, g, p.form, p.S, y, part, s)
+    const bool xa = x_aligned4(x, K);
+    if (p.C == 4 && p.MB == 1 && (NG == 1 || p.form == 0)) {
+        if (xa) SGQ_SKINNY(4, 1, true);
+        SGQ_SKINNY(4, 1, false);
+    }
+    if constexpr (NG == 1) {
+        if (p.C == 4 && xa) SGQ_SKINNY(4, 2, true);
+    }
+    if (p.MB == 1) {
+        if (xa) SGQ_SKINNY(2, 1, true);
+        SGQ_SKINNY(2, 1, false);
+    }
+    if (xa) SGQ_SKINNY(2, 2, true);
+    SGQ_SKINNY(2, 2, false);
+#undef SGQ_SKINNY
 }
 
 }  // namespace
 
+hipError_t launch_skinny_i4(const float* x, int64_t M, int64_t K, int64_t N, int ng, const void* const* packed,
+                            const float* const* devscales, const float* const* bias, const I4Geom& g,
+                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s) {
+    if (p.C == 0 || (p.S > 1 && !ws)) return hipErrorInvalidValue;
+    if (ng == 1) return skinny_dispatch<1>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, s);
+    if (ng == 2) return skinny_dispatch<2>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, s);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s) {
-    const int c = skinny_blocks(M, K, g, device_cus(s), 4);
-    if (c > 0) return skinny_dispatch<1>(c, x, M, K, N, &packed, &devscales, &bias, g, y, s);
     return launch_gemv_i4_multi(x, M, K, N, 1, &packed, &devscales, &bias, g, y, N, nullptr, nullptr, 0.0f, s);
 }
 
@@ -1469,16 +1792,6 @@ hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
                                  hipStream_t s, const float* gamma, float eps) {
-    // The same path as two forward calls of these shapes, so the gate and up
-    // sums are the plain forward's (k_skinny3 sums k blocks in the same order
-    // whatever its column blocks per workgroup).
-    const int c = gamma ? 0 : skinny_blocks(M, K, g, device_cus(s), 4);
-    if (c > 0) {
-        const void* packed[2] = {packed_g, packed_u};
-        const float* ds[2] = {devscales_g, devscales_u};
-        const float* bs[2] = {bias_g, bias_u};
-        return skinny_dispatch<2>(c, x, M, K, N, packed, ds, bs, g, h, s);
-    }
     GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, h, N, nullptr);
     a.gamma = gamma;
     a.eps = eps;
@@ -1582,9 +1895,16 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
         *path = 3;
         return;
     }
+    if (bits == 4) {
+        const SkinnyPlan sp = skinny_plan(M, K, I4Geom(K, N, group_size), cus < kMaxCus ? cus : kMaxCus);
+        if (sp.C > 0) {
+            *path = 4;
+            *ks = sp.S;
+            return;
+        }
+    }
     if (linear_uses_gemv(M, K, N)) {
-        const int64_t c = cus < kMaxCus ? cus : kMaxCus;  // as device_cus reports it
-        *path = bits == 4 && skinny_blocks(M, K, I4Geom(K, N, group_size), c, 4) > 0 ? 4 : 0;
+        *path = 0;
         return;
     }
     const int mode = bits == 4 ? (int)I4Geom(K, N, group_size).spc : 0;

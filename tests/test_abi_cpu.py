@@ -261,14 +261,16 @@ def test_plan_follows_the_device_cu_count(lib):
     reports fewer than 256): fewer CUs never mean more K splits, so the
     workspace sized for 256 CUs covers every device."""
     shapes = [(8, 128, 1024, 1024, 0), (8, 512, 4096, 4096, 0), (8, 256, 4096, 1024, 0), (4, 256, 4096, 1024, 128),
-              (4, 300, 2048, 640, 32), (8, 2048, 4096, 4096, 0), (4, 64, 11008, 4096, 128), (8, 17, 8192, 512, 0)]
+              (4, 300, 2048, 640, 32), (8, 2048, 4096, 4096, 0), (4, 64, 11008, 4096, 128), (8, 17, 8192, 512, 0),
+              (4, 16, 11008, 4096, 128), (4, 32, 11008, 4096, 64), (4, 24, 16384, 11008, 128),
+              (4, 20, 28672, 8192, 128), (4, 32, 8192, 3072, 32)]
     for bits, M, K, N, G in shapes:
         ws = lib.sgq_linear_workspace_bytes(bits, M, K, N)
         prev = None
         for cus in (256, 128, 80, 64, 32, 8, 1):
             path, ks = _plan(lib, bits, M, K, N, G, cus)
             assert ks >= 1
-            if path in (1, 2) and ks > 1:
+            if path in (1, 2, 4) and ks > 1:
                 assert ws >= ks * M * N * 4, (bits, M, K, N, cus)
             if prev is not None:
                 assert ks <= prev, (bits, M, K, N, cus, ks, prev)
@@ -287,16 +289,27 @@ def test_plan_follows_the_device_cu_count(lib):
 
 def test_plan_skinny_mfma(lib):
     """Batches of 5..16 rows over a wide INT4 weight take the skinny bf16 MFMA
-    kernel (path 4) when its 32- or 64-column workgroups fill at least 5/8 of
-    the CUs, and need 2C strips per scale column; everything else at those
-    batch sizes stays on the GEMV (path 0)."""
-    for M in range(5, 17):
+    kernel (path 4, whole K) when its 32- or 64-column workgroups fill at least
+    5/8 of the CUs, and need 2C strips per scale column; 17..32 rows take its
+    super-block form, and weights too narrow to fill the device split K
+    (k_splits > 1) once M * K * N reaches 2^29.  Everything else stays on the
+    GEMV (path 0) or the GEMM (path 1)."""
+    for M in range(5, 33):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (4, 1)  # 172 workgroups of 64 columns
         assert _plan(lib, 4, M, 2048, 6144, 128, 256) == (4, 1)  # 192 of 32
-        assert _plan(lib, 4, M, 5632, 2048, 128, 256) == (0, 1)  # 128 of 16: too narrow
+    for M in range(1, 33):  # 128 column blocks of 16, too little work to split: GEMV, or GEMM from 2^28
+        assert _plan(lib, 4, M, 5632, 2048, 128, 256)[0] == (0 if M * 5632 * 2048 <= 1 << 28 else 1)
+        assert _plan(lib, 4, M, 2048, 2048, 128, 256)[0] == 0
     for M in (1, 2, 3, 4):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (0, 1)
-    assert _plan(lib, 4, 17, 4096, 11008, 128, 256)[0] == 1  # the GEMM from 17 rows
+    assert _plan(lib, 4, 33, 4096, 11008, 128, 256)[0] == 1  # the GEMM from 33 rows
+    # Narrow weights: K split into 4 ranges of 2752 rows (64 column groups x 4
+    # = 256 workgroups) from M * K * N >= 2^29.
+    assert _plan(lib, 4, 11, 11008, 4096, 128, 256) == (0, 1)
+    for M in (12, 16, 17, 32):
+        assert _plan(lib, 4, M, 11008, 4096, 128, 256) == (4, 4)
+    assert _plan(lib, 4, 16, 4096, 4096, 128, 256) == (0, 1)  # 2^28: the GEMV
+    assert _plan(lib, 4, 32, 4096, 4096, 128, 256) == (4, 4)
     assert _plan(lib, 8, 8, 4096, 11008, 0, 256) == (0, 1)  # INT8 stays on the GEMV
     assert _plan(lib, 4, 8, 2048, 6144, 8, 256) == (0, 1)  # one strip per scale column
     assert _plan(lib, 4, 8, 2048, 6144, 16, 256) == (0, 1)  # two strips: 16 columns, too narrow
@@ -305,6 +318,10 @@ def test_plan_skinny_mfma(lib):
     assert _plan(lib, 4, 8, 2048, 5112, 24, 256) == (0, 1)  # three strips per scale column
     assert _plan(lib, 4, 8, 4096, 8192, 64, 256) == (4, 1)  # C = 2: 256 workgroups
     assert _plan(lib, 4, 8, 4096, 11004, 128, 256)[0] == 3  # flat layout
+    # Two row blocks keep the scales of a K range in LDS: at most 8192 rows a
+    # range, so a long K splits even over a wide weight.
+    assert _plan(lib, 4, 24, 16384, 11008, 128, 256) == (4, 2)
+    assert _plan(lib, 4, 8, 16384, 11008, 128, 256) == (4, 1)  # one row block: whole K
     # The threshold follows the device: a quarter of the CUs needs a quarter
     # of the workgroups (64 of 32 columns for N = 2048).
     assert _plan(lib, 4, 8, 5632, 2048, 128, 64) == (4, 1)

@@ -35,6 +35,9 @@ def _weights(sgq, dev, synth, bits_, K, N, G, scheme, seed):
         ("gemm_int8_pc_M300", 8, 300, 1024, 768, 0, 1, False),
         ("gemm_int4_M256", 4, 256, 1024, 1024, 128, 0, True),
         ("gemm_int4_g32_M40", 4, 40, 512, 256, 32, 0, True),
+        ("skinny_int4_M16", 4, 16, 4096, 11008, 128, 0, True),
+        ("skinny_int4_two_blocks_M24", 4, 24, 2048, 6144, 128, 0, True),
+        ("skinny_int4_split_k_M16", 4, 16, 11008, 4096, 128, 0, True),
     ],
 )
 def test_linear_graph_replays_match_eager(sgq, dev, synth, name, bits_, M, K, N, G, scheme, bias):

@@ -158,7 +158,8 @@ def test_same_sign_activations(sgq, dev, oracle, synth, M, K, N, kind):
 
 
 # Batches of 17..64 rows with too much work for the GEMV take the GEMM's 32-
-# and 64-row tiles (split K); every row against the oracle.
+# and 64-row tiles (split K), or for INT4 up to 32 rows the skinny MFMA
+# kernel's super-block form; every row against the oracle.
 @pytest.mark.parametrize("M", [17, 24, 32, 33, 48, 64])
 @pytest.mark.parametrize("bits_,K,N,G,scheme", [(4, 4096, 11008, 128, 0), (4, 11008, 4096, 128, 0),
                                                 (8, 4096, 8192, 0, 0), (8, 4096, 8192, 0, 1)])
@@ -167,7 +168,7 @@ def test_skinny_gemm_tiles(sgq, dev, oracle, synth, M, bits_, K, N, G, scheme):
     path, ks = ctypes.c_int(), ctypes.c_int()
     assert lib.sgq_linear_plan(bits_, M, K, N, G, 256, ctypes.byref(path), ctypes.byref(ks)) == 0
     print(f"  case M={M} K={K} N={N} bits={bits_} path={path.value} k_splits={ks.value}", flush=True)
-    assert path.value == 1  # the three-term GEMM
+    assert path.value == (4 if bits_ == 4 and M <= 32 else 1)  # skinny MFMA kernel, or the three-term GEMM
     y, yref = _case(sgq, dev, oracle, synth, bits_, M, K, N, G, scheme, True, 17)
     e = rel_err(y, yref)
     print(f"    rel_err={e:.3e}", flush=True)

@@ -79,21 +79,57 @@ def test_skinny_shapes(sgq, dev, oracle, synth, M, K, N, G):
 
 
 def test_skinny_boundaries(sgq, dev):
-    # Four rows, narrow weights and groups whose scale column holds a single
-    # strip stay on the GEMV; the batches above take the MFMA kernel.
+    # Four rows, narrow weights of little work and groups whose scale column
+    # holds a single strip stay on the GEMV; 5..32 rows over wide weights, and
+    # narrow ones from M * K * N = 2^29, take the MFMA kernel; 33 rows the GEMM.
     assert _path(sgq, 4, 4096, 11008, 128) == 0
-    assert _path(sgq, 17, 4096, 11008, 128) == 1
+    assert _path(sgq, 33, 4096, 11008, 128) == 1
     assert _path(sgq, 8, 5632, 2048, 128) == 0
     assert _path(sgq, 8, 2048, 6144, 8) == 0
-    for M in range(5, 17):
+    assert _path(sgq, 8, 11008, 4096, 128) == 0
+    assert _path(sgq, 16, 11008, 4096, 128) == SKINNY
+    for M in range(5, 33):
         assert _path(sgq, M, 4096, 11008, 128) == SKINNY
 
 
+def _splits(sgq, M, K, N, G):
+    lib = sgq.load_library()
+    path, ks = ctypes.c_int(), ctypes.c_int()
+    assert lib.sgq_linear_plan(4, M, K, N, G, 0, ctypes.byref(path), ctypes.byref(ks)) == 0
+    return ks.value
+
+
+# The super-block form: two row blocks over wide weights (17..32 rows; a K
+# longer than 8192 rows splits even there), and narrow weights whose K is
+# split into ranges added by the reduce kernel; K tails inside a super-block
+# and a group of 32 (two column blocks per workgroup).
+@pytest.mark.parametrize("M,K,N,G,ks", [(17, 4096, 11008, 128, 1), (24, 4096, 11008, 128, 1),
+                                        (32, 4096, 11008, 128, 1), (24, 2048, 6144, 128, 1),
+                                        (20, 2048, 5120, 32, 1), (17, 4112, 6144, 128, 1),
+                                        (24, 16384, 11008, 128, 2), (12, 11008, 4096, 128, 4),
+                                        (16, 11008, 4096, 128, 4), (17, 11008, 4096, 128, 4),
+                                        (32, 11008, 4096, 128, 4), (32, 4096, 4096, 128, 4),
+                                        (16, 11024, 4096, 128, 4), (32, 8192, 3072, 32, 4)])
+def test_skinny_superblock_shapes(sgq, dev, oracle, synth, M, K, N, G, ks):
+    path = _path(sgq, M, K, N, G)
+    print(f"  case M={M} K={K} N={N} G={G} path={path} k_splits={_splits(sgq, M, K, N, G)}", flush=True)
+    assert path == SKINNY and _splits(sgq, M, K, N, G) == ks
+    W, b, qw, (q, s) = _quantized(sgq, dev, oracle, synth, K, N, G, 71)
+    x = synth.normal((M, K), synth.config_seed(71), synth.STREAM_X, 0.0, 1.0)
+    y = _np(sgq.quantized_matmul_int4(_to_dev(x, dev), qw, _to_dev(b, dev)))
+    yref = oracle.quantized_matmul_int4(x, q, s, G, b)
+    e = rel_err(y, yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
 # x that is not 16-byte aligned, or whose rows are not a multiple of four
-# floats, takes the kernel's one-float loads.
-@pytest.mark.parametrize("K,offset", [(2048, 1), (2050, 0), (2051, 3)])
-def test_skinny_unaligned_x(sgq, dev, oracle, synth, K, offset):
-    M, N, G = 8, 6144, 128
+# floats, takes the kernel's one-float loads (both forms, split K).
+@pytest.mark.parametrize("M,K,N,offset", [(8, 2048, 6144, 1), (8, 2050, 6144, 0), (8, 2051, 6144, 3),
+                                          (17, 2050, 6144, 0), (24, 2051, 6144, 3), (16, 11008, 4096, 1),
+                                          (20, 11010, 4096, 0)])
+def test_skinny_unaligned_x(sgq, dev, oracle, synth, M, K, N, offset):
+    G = 128
     assert _path(sgq, M, K, N, G) == SKINNY
     W, b = _weights(synth, K, N, 62, G)
     flat = synth.normal((M * K + offset,), synth.config_seed(62), synth.STREAM_X, 0.0, 1.0)
@@ -109,10 +145,12 @@ def test_skinny_unaligned_x(sgq, dev, oracle, synth, K, offset):
 
 
 @pytest.mark.parametrize("kind", ["abs", "silu"])
-def test_skinny_same_sign_activations(sgq, dev, oracle, synth, kind):
+@pytest.mark.parametrize("M,N", [(16, 5632), (16, 4096), (32, 5632)])
+def test_skinny_same_sign_activations(sgq, dev, oracle, synth, kind, M, N):
     # Same-sign inputs at long K: no cancellation between terms to hide an
-    # error in the split of x * s.
-    M, K, N, G = 16, 11008, 5632, 128
+    # error in the split of x * s (whole K, split K, two row blocks).
+    K, G = 11008, 128
+    assert _path(sgq, M, K, N, G) == SKINNY
     W, _ = _weights(synth, K, N, 63, G)
     z = synth.normal((M, K), synth.config_seed(63), synth.STREAM_X, 0.0, 1.0)
     if kind == "abs":
@@ -151,11 +189,13 @@ def test_skinny_split_sums_to_rounded_product(sgq, dev, k0):
     assert helpers.same_bits(y, want), np.count_nonzero(y != want)
 
 
-def test_skinny_infinite_activation(sgq, dev, oracle, synth):
+@pytest.mark.parametrize("M,K,N", [(8, 2048, 6144), (24, 2048, 6144), (16, 11008, 4096)])
+def test_skinny_infinite_activation(sgq, dev, oracle, synth, M, K, N):
     # inf * s split into three bf16 planes is inf - inf; the kernel hands a
-    # non-finite total to the reference's k-order sum, so infinities and NaNs
-    # land where the reference's x . (q * s) puts them.
-    M, K, N, G = 8, 2048, 6144, 128
+    # non-finite total (of its K range) to the reference's k-order sum, so
+    # infinities and NaNs land where the reference's x . (q * s) puts them.
+    G = 128
+    assert _path(sgq, M, K, N, G) == SKINNY
     W, _ = _weights(synth, K, N, 65, G)
     x = synth.normal((M, K), synth.config_seed(65), synth.STREAM_X, 0.0, 1.0)
     x[0, 17] = np.inf
@@ -175,21 +215,25 @@ def test_skinny_infinite_activation(sgq, dev, oracle, synth):
     assert np.max(np.abs(y[fin].astype(np.float64) - yref[fin])) <= TOL * np.max(np.abs(yref[fin]))
 
 
-def test_skinny_rows_independent_and_deterministic(sgq, dev, synth):
+@pytest.mark.parametrize("K,N,Ms", [(4096, 11008, (5, 9, 13, 16)), (4096, 11008, (17, 24, 29, 32)),
+                                     (11008, 4096, (12, 16, 17, 25, 32))])
+def test_skinny_rows_independent_and_deterministic(sgq, dev, synth, K, N, Ms):
     # A row's sums do not depend on the other rows of the batch (each is its
-    # own row of the MFMA tile), and repeated calls give identical bits.
-    K, N, G = 4096, 11008, 128
+    # own row of the MFMA tile; the K ranges and wavefronts of a form do not
+    # depend on M), and repeated calls give identical bits.
+    G = 128
     W, _ = _weights(synth, K, N, 66, G)
-    x = _to_dev(synth.normal((16, K), synth.config_seed(66), synth.STREAM_X, 0.0, 1.0), dev)
+    x = _to_dev(synth.normal((Ms[-1], K), synth.config_seed(66), synth.STREAM_X, 0.0, 1.0), dev)
     qw = sgq.quantize_int4(_to_dev(W, dev), G)
-    y16 = sgq.quantized_matmul_int4(x, qw).clone()
-    for M in (5, 9, 13):
-        assert torch.equal(sgq.quantized_matmul_int4(x[:M].contiguous(), qw), y16[:M])
+    y = sgq.quantized_matmul_int4(x, qw).clone()
+    for M in Ms[:-1]:
+        assert torch.equal(sgq.quantized_matmul_int4(x[:M].contiguous(), qw), y[:M])
     for _ in range(3):
-        assert torch.equal(sgq.quantized_matmul_int4(x, qw), y16)
+        assert torch.equal(sgq.quantized_matmul_int4(x, qw), y)
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 2048, 5632), (16, 4096, 11008)])
+@pytest.mark.parametrize("M,K,N", [(8, 2048, 5632), (16, 4096, 11008), (24, 2048, 5632), (16, 11008, 4096),
+                                   (32, 4096, 4096)])
 def test_skinny_swiglu(sgq, dev, oracle, synth, M, K, N):
     # The gated MLP runs gate and up through the same kernel: its sums equal
     # two forward calls', so the fused output matches the two projections

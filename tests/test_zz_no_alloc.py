@@ -62,6 +62,14 @@ def test_noalloc_matches_workspace_entry_point(sgq, dev, oracle, synth):
     _run(sgq, dev, oracle, synth, 256, 4096, 1024, 128, 63)
 
 
+def test_noalloc_skinny_split_k(sgq, dev, oracle, synth):
+    # The skinny MFMA kernel's K ranges over a narrow weight put their partial
+    # sums in the same scratch: two calls in a row, the second smaller.
+    n1 = _run(sgq, dev, oracle, synth, 32, 11008, 4096, 128, 64)
+    n2 = _run(sgq, dev, oracle, synth, 16, 11008, 4096, 128, 65)
+    assert n1 > n2 > 0
+
+
 def test_noalloc_refuses_oversized_scratch(sgq, dev):
     lib = sgq.load_library()
     M, K, N = 384, 8192, 8192  # split-K partials of 3 x 384 x 8192 floats: 36 MiB
