@@ -547,15 +547,18 @@ def decode_step(pkg, dev, oracle, steps, fused=False):
 
     by = {m["name"]: m for m in mats}
     gate, up = by["gate"], by["up"]
-    nws = lib.sgq_swiglu_workspace_bytes(4, C5_M, gate["K"], gate["N"], C5_G)
-    assert nws == 0  # M=8: the one-launch GEMV
+    # One workspace of the largest size any call asks for (M=8: none at the
+    # NanoLLaMA shapes, whose calls run the GEMV or the unsplit skinny kernel).
+    nws = max([lib.sgq_swiglu_workspace_bytes(4, C5_M, gate["K"], gate["N"], C5_G)] +
+              [lib.sgq_linear_workspace_bytes(4, C5_M, K, N) for _, K, N in C5_MATS])
+    ws = torch.empty(max(nws, 256), dtype=torch.uint8, device=dev)
     h = torch.empty((C5_M, gate["N"]), dtype=torch.float32, device=dev)
 
     def linear(m, layer, stream):
         packed, ds = m["layers"][layer]
         rc = lib.sgq_linear_int4(m["xd"].data_ptr(), C5_M, m["K"], m["N"], packed.data_ptr(),
                                  m["qw"].scales.data_ptr(), ds.data_ptr(), C5_G, None, m["y"].data_ptr(),
-                                 None, 0, stream)
+                                 ws.data_ptr(), ws.numel(), stream)
         if rc != 0:
             raise RuntimeError(lib.sgq_last_error().decode())
 
@@ -570,7 +573,7 @@ def decode_step(pkg, dev, oracle, steps, fused=False):
                     rc = lib.sgq_swiglu_int4(gate["xd"].data_ptr(), C5_M, gate["K"], gate["N"], pg.data_ptr(),
                                              gate["qw"].scales.data_ptr(), dg.data_ptr(), None, pu.data_ptr(),
                                              up["qw"].scales.data_ptr(), du.data_ptr(), None, C5_G, h.data_ptr(),
-                                             None, 0, stream)
+                                             ws.data_ptr(), ws.numel(), stream)
                     if rc != 0:
                         raise RuntimeError(lib.sgq_last_error().decode())
                     continue

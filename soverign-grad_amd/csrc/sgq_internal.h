@@ -121,7 +121,7 @@ inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
 //    reads its own slice.  The partial sums go to the caller's workspace and
 //    a second kernel adds them in range order.
 constexpr int64_t kSkinnyMinRows = 5;        // wide weights
-constexpr int64_t kSkinnyNarrowMinRows = 4;  // split K
+constexpr int64_t kSkinnyNarrowMinRows = 5;  // split K
 constexpr int64_t kSkinnyMaxRows = 32;       // two row blocks of 16
 constexpr int64_t kSkinnyMinK = 2048;        // wide weights
 constexpr int64_t kSkinnyNarrowMinK = 1024;  // split K
@@ -136,11 +136,15 @@ struct SkinnyPlan {
     int MB = 1;    // row blocks of 16
     int form = 1;  // 0: k_skinny3 (whole K, one row block), 1: k_skinny_sb (super-blocks)
 };
-// Narrow weights split K only from this much work (M * K * N; measured:
-// 16 x 11008 -> 4096 24 vs 32 us on the GEMV, 32 x 4096 -> 4096 21 vs 23 us on
-// the GEMM; 16 x 4096 -> 4096 15 vs 14 us and 2048 -> 2048 at 4..16 rows
-// 12 vs 4-6 us stay on the GEMV).
-constexpr int64_t kSkinnyNarrowWork = (int64_t)1 << 29;
+// Narrow weights split K only from this much work, M rounded up to the
+// GEMV's row group of 8 (its time steps up with each group).  Measured (us,
+// GEMV or GEMM -> split): 11008 -> 4096 at 8 / 10 / 16 rows 19.6 / 31.7 /
+// 32.0 -> 18.3 / 18.5 / 20.2; 4096 -> 4096 at 12 / 16 / 24 rows 14.0 / 14.6 /
+// 21.8 -> 10.4 / 10.9 / 14.1; 5632 -> 2048 at 24 rows 20.3 -> 15.6.  Kept:
+// 4096 -> 4096 at 8 rows (9.2 vs 10.3), 5632 -> 2048 at 16 (11.7 vs 12.4),
+// 2048 -> 2048 (5.8 vs 9.0 at 16 rows), four rows (11008 -> 4096 13.7 vs
+// 17.7).
+constexpr int64_t kSkinnyNarrowWork = (int64_t)1 << 28;
 // K ranges for ncg column groups of a K of nsb super-blocks on cus CUs:
 // narrow weights split to fill the device (ranges of at least
 // kSkinnyMinRangeBlocks super-blocks); every range holds at most
@@ -179,7 +183,7 @@ inline SkinnyPlan skinny_plan(int64_t M, int64_t K, const I4Geom& g, int64_t cus
         }
     const int c = g.spc % 8 == 0 ? 4 : (g.spc % 4 == 0 ? 2 : 0);
     if (c == 0 || M < kSkinnyNarrowMinRows || K < kSkinnyNarrowMinK) return p;
-    if (M * K * g.N < kSkinnyNarrowWork) return p;
+    if (round_up(M, 8) * K * g.N < kSkinnyNarrowWork) return p;
     p.S = skinny_splits(g.NS / (2 * c), nsb, cus, true);
     p.C = p.S > 1 ? c : 0;  // too short to split (or too long for the ranges): not this kernel
     p.MB = MB;

@@ -1051,14 +1051,18 @@ __device__ __forceinline__ NibbleT nibble_t(int e) {
     t.rot1 = (e & 1) ? 4u : 28u;
     return t;
 }
+// keep ? a : b, bit by bit, as one v_bitop3_b32: the truth table indexes
+// (a, b, keep) as (0xF0, 0xCC, 0xAA), so (0xF0 & 0xAA) | (0xCC & ~0xAA) =
+// 0xE4.  The compiler writes the and/or form as two or three instructions.
+__device__ __forceinline__ uint32_t bit_select(uint32_t a, uint32_t b, uint32_t keep) {
+    return __builtin_amdgcn_bitop3_b32(a, b, keep, 0xE4);
+}
 // On entry nibble c of lane e is T[e][c]; on return nibble r is T[r][e].
+// Three instructions per step: the DPP exchange, a rotate, a bit select.
 __device__ __forceinline__ uint32_t nibble_transpose8(uint32_t w, const NibbleT& t) {
-    uint32_t p = dpp_xor8(w);
-    w = (w & t.keep4) | (rotr32(p, 16u) & ~t.keep4);
-    p = dpp_xor2(w);
-    w = (w & t.keep2) | (rotr32(p, t.rot2) & ~t.keep2);
-    p = dpp_xor1(w);
-    w = (w & t.keep1) | (rotr32(p, t.rot1) & ~t.keep1);
+    w = bit_select(w, rotr32(dpp_xor8(w), 16u), t.keep4);
+    w = bit_select(w, rotr32(dpp_xor2(w), t.rot2), t.keep2);
+    w = bit_select(w, rotr32(dpp_xor1(w), t.rot1), t.keep1);
     return w;
 }
 
@@ -1235,13 +1239,15 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
 //
 // The K range is walked in super-blocks of 128 rows, wavefront w taking
 // super-blocks w, w + NW, ...  In a super-block, lane (g, e) of strip j loads
-// rows 32g + 4e .. 32g + 4e + 3 of its strip (16 bytes, all eight columns) and
-// x rows 32g .. 32g + 31 of its batch row; dword i of the codes transposed
-// across the eight lanes e gives column e at rows 32g + 4e' + i (e' = 0..7),
-// the B operand of MFMA i, and component i of the eight x quads the matching
-// A operand.  The scales of the workgroup's K range sit in LDS (read once,
-// coalesced); the next super-block's codes and x are loaded while the current
-// one is computed.
+// rows 16e + 4g .. 16e + 4g + 3 of its strip (16 bytes, all eight columns; the
+// 32 lanes of a strip read its 512 bytes once) and, for t = 0..7, x rows
+// 16t + 4g .. 16t + 4g + 3 of its batch row (the four lane groups of a batch
+// row read 64 contiguous bytes per load, one cache line).  Dword i of the
+// codes transposed across the eight lanes e gives column e at rows
+// 16e' + 4g + i (e' = 0..7), the B operand of MFMA i; component i of the
+// eight x quads is the matching A operand.  The scales of the workgroup's K
+// range sit in LDS (read once, coalesced); the next super-block's codes and x
+// are loaded while the current one is computed.
 template <int NW, int C, int NG, bool XA, int MB>
 struct SkinnyRegs {
     uint4 w[NG][C];      // 4 rows x 8 columns of each strip
@@ -1291,7 +1297,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (32 * g + 4 * e) * 4;
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (16 * e + 4 * g) * 4;
     bool row_live[MB];
     int xrow[MB];
 #pragma unroll
@@ -1309,12 +1315,12 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
         for (int q = 0; q < NG; ++q)
 #pragma unroll
             for (int c = 0; c < C; ++c) r.w[q][c] = buf_load16(rW[q], wv[c], sb * (kSkinnySB * 4));
-        const int k0 = sb * kSkinnySB + 32 * g;
+        const int k0 = sb * kSkinnySB + 4 * g;
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const int kk = k0 + 4 * t;
+                const int kk = k0 + 16 * t;
                 if constexpr (XA) {
                     r.xq[b][t] = buf_load4f<true>(rX, in && row_live[b] && kk < K ? xrow[b] + kk * 4 : kOobOff, 0);
                 } else {
@@ -1342,12 +1348,12 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB>& r, int sb) {
         // A super-block past the range has x = 0; its scale reads stay inside
         // the range's LDS rows.
-        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + 8 * g;
+        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + g;
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
             float4 s4[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) s4[t] = ssc[q][lr + t];
+            for (int t = 0; t < 8; ++t) s4[t] = ssc[q][lr + 4 * t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 uint4 ah[MB], am[MB], al[MB];
@@ -1392,6 +1398,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     for (; sb < sb_hi; sb += 2 * NW) {
         load(rb, sb + NW);
         compute(ra, sb);
+        if (sb + NW >= sb_hi) break;  // wave-uniform: no empty super-block computed
         load(ra, sb + 2 * NW);
         compute(rb, sb + NW);
     }

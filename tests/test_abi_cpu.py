@@ -51,9 +51,12 @@ def test_int4_sizes(lib, K, N, G):
 def test_workspace_sizes(lib):
     # The GEMV (M <= 16, or up to 128 rows of small work) and GEMMs with at
     # least one tile per CU need no workspace; smaller GEMM grids split K and
-    # keep KS * M * N fp32 partials.
+    # keep KS * M * N fp32 partials, as does the INT4 skinny kernel over a
+    # narrow weight (4 K ranges for 16 x 4096 -> 4096).
     assert lib.sgq_linear_workspace_bytes(4, 1, 4096, 4096) == 0
-    assert lib.sgq_linear_workspace_bytes(4, 16, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(4, 8, 4096, 4096) == 0
+    assert lib.sgq_linear_workspace_bytes(4, 16, 4096, 4096) == 4 * 16 * 4096 * 4
+    assert lib.sgq_linear_workspace_bytes(8, 16, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0  # GEMV: 2^27 multiply-adds
     assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0  # 256 or 512 tiles
     ws = lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)  # GEMM of 8 or 16 tiles: split K
@@ -292,23 +295,24 @@ def test_plan_skinny_mfma(lib):
     kernel (path 4, whole K) when its 32- or 64-column workgroups fill at least
     5/8 of the CUs, and need 2C strips per scale column; 17..32 rows take its
     super-block form, and weights too narrow to fill the device split K
-    (k_splits > 1) once M * K * N reaches 2^29.  Everything else stays on the
-    GEMV (path 0) or the GEMM (path 1)."""
+    (k_splits > 1) from 5 rows once M (rounded up to 8) * K * N reaches 2^28.
+    Everything else stays on the GEMV (path 0) or the GEMM (path 1)."""
     for M in range(5, 33):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (4, 1)  # 172 workgroups of 64 columns
         assert _plan(lib, 4, M, 2048, 6144, 128, 256) == (4, 1)  # 192 of 32
-    for M in range(1, 33):  # 128 column blocks of 16, too little work to split: GEMV, or GEMM from 2^28
-        assert _plan(lib, 4, M, 5632, 2048, 128, 256)[0] == (0 if M * 5632 * 2048 <= 1 << 28 else 1)
-        assert _plan(lib, 4, M, 2048, 2048, 128, 256)[0] == 0
+    for M in range(1, 33):  # 128 column blocks of 16: split K from 24 rows' worth of work (2^28), else GEMV
+        assert _plan(lib, 4, M, 5632, 2048, 128, 256) == ((4, 4) if M >= 17 else (0, 1))
+        assert _plan(lib, 4, M, 2048, 2048, 128, 256) == (0, 1)
     for M in (1, 2, 3, 4):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (0, 1)
     assert _plan(lib, 4, 33, 4096, 11008, 128, 256)[0] == 1  # the GEMM from 33 rows
     # Narrow weights: K split into 4 ranges of 2752 rows (64 column groups x 4
-    # = 256 workgroups) from M * K * N >= 2^29.
-    assert _plan(lib, 4, 11, 11008, 4096, 128, 256) == (0, 1)
-    for M in (12, 16, 17, 32):
+    # = 256 workgroups) from 5 rows with M (rounded up to 8) * K * N >= 2^28.
+    assert _plan(lib, 4, 4, 11008, 4096, 128, 256) == (0, 1)
+    for M in (5, 8, 11, 12, 16, 17, 32):
         assert _plan(lib, 4, M, 11008, 4096, 128, 256) == (4, 4)
-    assert _plan(lib, 4, 16, 4096, 4096, 128, 256) == (0, 1)  # 2^28: the GEMV
+    assert _plan(lib, 4, 8, 4096, 4096, 128, 256) == (0, 1)  # 2^27: the GEMV
+    assert _plan(lib, 4, 9, 4096, 4096, 128, 256) == (4, 4)
     assert _plan(lib, 4, 32, 4096, 4096, 128, 256) == (4, 4)
     assert _plan(lib, 8, 8, 4096, 11008, 0, 256) == (0, 1)  # INT8 stays on the GEMV
     assert _plan(lib, 4, 8, 2048, 6144, 8, 256) == (0, 1)  # one strip per scale column

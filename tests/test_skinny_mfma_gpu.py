@@ -81,12 +81,14 @@ def test_skinny_shapes(sgq, dev, oracle, synth, M, K, N, G):
 def test_skinny_boundaries(sgq, dev):
     # Four rows, narrow weights of little work and groups whose scale column
     # holds a single strip stay on the GEMV; 5..32 rows over wide weights, and
-    # narrow ones from M * K * N = 2^29, take the MFMA kernel; 33 rows the GEMM.
+    # narrow ones from (M rounded up to 8) * K * N = 2^28, take the MFMA
+    # kernel; 33 rows the GEMM.
     assert _path(sgq, 4, 4096, 11008, 128) == 0
     assert _path(sgq, 33, 4096, 11008, 128) == 1
     assert _path(sgq, 8, 5632, 2048, 128) == 0
     assert _path(sgq, 8, 2048, 6144, 8) == 0
-    assert _path(sgq, 8, 11008, 4096, 128) == 0
+    assert _path(sgq, 4, 11008, 4096, 128) == 0
+    assert _path(sgq, 8, 11008, 4096, 128) == SKINNY
     assert _path(sgq, 16, 11008, 4096, 128) == SKINNY
     for M in range(5, 33):
         assert _path(sgq, M, 4096, 11008, 128) == SKINNY
