@@ -65,6 +65,12 @@ CONFIGS = {
                        scheme=2, bias=False, seed=2),
     "c4": dict(name="C4: INT8 per-tensor QuantizedLinear 4096->4096, prefill M=2048", bits=8, M=2048, K=4096,
                N=4096, G=0, scheme=0, bias=False, seed=3),
+    # Batches past C3's 16 rows (the crossover leg's shapes), for --config runs
+    # and profiles of the skinny kernel's two-row-block form.
+    "c3_gate_m32": dict(name="C3 shape: INT4 g128 gate/up 4096->11008, M=32", bits=4, M=32, K=4096, N=11008,
+                        G=128, scheme=2, bias=False, seed=2),
+    "c3_down_m32": dict(name="C3 shape: INT4 g128 down 11008->4096, M=32", bits=4, M=32, K=11008, N=4096,
+                        G=128, scheme=2, bias=False, seed=2),
 }
 
 
