@@ -93,8 +93,9 @@ int64_t sgq_quantize_workspace_bytes(int bits, int64_t rows, int64_t cols, int64
  * GEMV) when its grid of output tiles (32 or 64 rows by 128 columns for
  * batches of up to 32 or 64 rows; else 128 rows by 256 columns for INT8, 128
  * for INT4) is smaller than the GPU, and for INT4 the skinny MFMA kernel over
- * weights too narrow to fill the GPU (M >= 4 with M * K * N >= 2^29) or, with
- * 17..32 rows, over a K longer than 8192 rows.  The size is the largest any
+ * weights too narrow to fill the GPU (M >= 5 with (M rounded up to 8) * K * N
+ * >= 2^28) or, with 17..32 rows, over a K longer than 8192 rows (the INT8
+ * skinny kernel never splits K).  The size is the largest any
  * group size and device could need.  0 otherwise (the GEMV and the other
  * kernels own whole outputs per workgroup), and the workspace arguments may
  * then be NULL/0.  The contents need no initialisation and are overwritten by
@@ -107,9 +108,11 @@ int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
  * MI355X has 256, a partition fewer).  *path: 0 the GEMV, 1 the three-term
  * bf16 MFMA GEMM, 2 the fp32 MFMA GEMM (INT4 groups that are not a multiple
  * of 128), 3 the generic kernel of the flat INT4 layout, 4 the skinny bf16
- * MFMA kernel (INT4, 5..32 rows over a weight wide enough to fill the
- * device with workgroups of 32 or 64 columns; 4..32 rows over narrower
- * weights with M * K * N >= 2^29, K split).  *k_splits: 1, or the number of
+ * MFMA kernels (INT4: 5..32 rows over a weight wide enough to fill the
+ * device with workgroups of 32 or 64 columns, and 5..32 rows over narrower
+ * weights with (M rounded up to 8) * K * N >= 2^28, K split; INT8: 5..128
+ * rows with (M rounded up to 8) * K * N >= 2^26, above 16 rows only while
+ * M * K * N <= 2^28, whole K).  *k_splits: 1, or the number of
  * workgroups sharing each output tile's K range (the GEMM on grids smaller
  * than the device, the skinny kernel's K ranges).  sgq_linear_workspace_bytes sizes for the
  * largest device, so it covers every plan.  Host-only; this library's own
@@ -192,9 +195,12 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  * and with it nn::QuantizedLinear::forward (include/sovereigngrad/nn.hpp:956-958):
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
- * Dispatch: M <= 16 runs the wavefront GEMV (row groups of 8), as do up to
- * 128 rows when M * K * N <= 2^28; larger batches the LDS-staged MFMA
- * GEMM, whose fp32 products run on the bf16 matrix cores as three exact bf16
+ * Dispatch (sgq_linear_plan): 5..128 rows with (M rounded up to 8) * K * N
+ * >= 2^26 (above 16 rows only while M * K * N <= 2^28) run the skinny bf16
+ * MFMA kernel (whole K per workgroup, no workspace); other batches of up to
+ * 16 rows, and up to 128 rows with M * K * N <= 2^28, the wavefront GEMV (row
+ * groups of 8); larger batches the LDS-staged MFMA GEMM.  Both MFMA kernels
+ * run the fp32 products on the bf16 matrix cores as three exact bf16
  * products each (fp32 accumulation; as accurate as an fp32 product).
  * workspace: sgq_linear_workspace_bytes(8, M, K, N) bytes, else
  * SGQ_ERR_WORKSPACE. */
@@ -206,8 +212,9 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
  * and nn::QuantizedLinear4Bit::forward (include/sovereigngrad/nn.hpp:994-996).
  * scales: the reference-layout scales (used by the FLAT layout); devscales:
  * the device scales written by sgq_quantize_int4/sgq_pack_int4 (TILED layout).
- * Dispatch (sgq_linear_plan): the skinny bf16 MFMA kernel for the batches of
- * 4..32 rows it takes, else as sgq_linear_int8.  workspace:
+ * Dispatch (sgq_linear_plan): the INT4 skinny bf16 MFMA kernel for the
+ * batches of 5..32 rows it takes, else the GEMV for up to 16 rows (and up to
+ * 128 rows with M * K * N <= 2^28), else the GEMM.  workspace:
  * sgq_linear_workspace_bytes(4, M, K, N) bytes, else SGQ_ERR_WORKSPACE. */
 int sgq_linear_int4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
                     const float* devscales, int64_t group_size, const float* bias, float* y, void* workspace,
@@ -237,9 +244,12 @@ int sgq_linear_int4_noalloc(const float* x, int64_t M, int64_t K, int64_t N, con
  * silu(v) = v / (1 + exp(-v)) as Tensor::silu (src/ops.cpp:561-575,
  * include/sovereigngrad/simd.hpp:103-108), * as mul (src/ops.cpp:239-253).
  * The two weights share K, N, scheme / group_size.  The batches the forward
- * runs on the GEMV or on the skinny MFMA kernel (above), with the tiled layout, run both weights in one launch (x read
- * once per strip pair, no intermediate in HBM; a split K adds its reduce kernel); otherwise two projections (GEMM or
- * flat INT4) and an elementwise kernel.  Biases may be NULL.  workspace:
+ * runs on the GEMV or on the INT4 skinny MFMA kernel (above), with the tiled
+ * layout, run both weights in one launch (x read once per strip pair, no
+ * intermediate in HBM; a split K adds its reduce kernel); otherwise two
+ * projections (the INT8 skinny kernel, the GEMM or flat INT4) and an
+ * elementwise kernel, so that the sums are those of two forward calls.
+ * Biases may be NULL.  workspace:
  * sgq_swiglu_workspace_bytes(bits, M, K, N, group_size) bytes (group_size is
  * ignored for bits 8), else SGQ_ERR_WORKSPACE. */
 int64_t sgq_swiglu_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size);

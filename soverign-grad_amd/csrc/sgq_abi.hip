@@ -93,8 +93,11 @@ int64_t swiglu_ws_bytes(int bits, bool flat, int64_t M, int64_t K, int64_t N, in
     if (bits == 4 && !flat && K > 0)
         skinny = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, group_size), kMaxCus), M, N, 2);
     int64_t other = 0;
-    // The one-launch GEMV form takes the batches the plain forward runs on the GEMV.
-    if (flat || !linear_uses_gemv(M, K, N) || K == 0) {
+    // The one-launch GEMV form takes the batches the plain forward runs on the
+    // GEMV; INT8 batches of the skinny kernel run it once per weight, up into
+    // the workspace (no split K: those batches are within the GEMV's).
+    const bool skinny8 = bits == 8 && K > 0 && skinny8_plan(M, K, N, kMaxCus).C > 0;
+    if (flat || skinny8 || !linear_uses_gemv(M, K, N) || K == 0) {
         const int64_t split = (!flat && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
         other = align_up(M * N * 4) + split;
     }
@@ -518,7 +521,10 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_int8: packed and per-channel scales must be 16-byte aligned");
     if (!forward_fits(8, M, K, N, 0))
         return fail(SGQ_ERR_UNSUPPORTED, "sgq_linear_int8: K = %lld is too long for this batch", (long long)K);
-    if (linear_uses_gemv(M, K, N)) {
+    const Skinny8Plan sp = skinny8_plan(M, K, N, device_cus(s));
+    if (sp.C > 0) {
+        SGQ_HIP(launch_skinny_i8(x, M, K, N, packed, scales, per_tensor, bias, sp, y, s), "skinny_i8");
+    } else if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i8(x, M, K, N, packed, scales, per_tensor, bias, y, s), "gemv_i8");
     } else {
         const int st = check_linear_ws("sgq_linear_int8", 8, M, K, N, workspace, workspace_bytes);
@@ -581,6 +587,15 @@ int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_INVALID_ARGUMENT, "%s: packed and per-channel scales must be 16-byte aligned", fn);
     if (!forward_fits(8, M, K, N, 0))
         return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
+    // The skinny kernel's batches take it for both projections, so that the
+    // gated MLP's sums are those of two forward calls.
+    const Skinny8Plan sp = skinny8_plan(M, K, N, device_cus(s));
+    if (sp.C > 0) {
+        SGQ_HIP(launch_skinny_i8(x, M, K, N, packed_gate, scales_gate, per_tensor, bias_gate, sp, h, s), "skinny_i8");
+        SGQ_HIP(launch_skinny_i8(x, M, K, N, packed_up, scales_up, per_tensor, bias_up, sp, u, s), "skinny_i8");
+        SGQ_HIP(launch_silu_mul(h, u, M * N, s), "silu_mul");
+        return ok();
+    }
     if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_swiglu_gemv_i8(x, M, K, N, packed_gate, scales_gate, bias_gate, packed_up, scales_up, bias_up,
                                       per_tensor, h, s),

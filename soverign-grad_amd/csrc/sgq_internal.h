@@ -190,6 +190,30 @@ inline SkinnyPlan skinny_plan(int64_t M, int64_t K, const I4Geom& g, int64_t cus
     if (p.C == 0) p.S = 1;
     return p;
 }
+// INT8 batches on the bf16 matrix cores (k_skinny8): workgroups of MB row
+// blocks of 16 (two above 16 rows) by C column blocks of 16 over all of K, no
+// workspace.  C = 2 where that still gives a workgroup per CU.  The GEMV
+// keeps four rows and little work (its time is a fixed ~3 us plus
+// round_up(M, 8) * K * N at the VALU rate); above 16 rows the GEMM keeps the
+// shapes past the GEMV's small work (its wider tiles read each x row for more
+// columns).
+constexpr int64_t kSkinny8MinRows = 5;
+constexpr int64_t kSkinny8MaxRows = 128;
+constexpr int64_t kSkinny8MinWork = (int64_t)1 << 26;  // round_up(M, 8) * K * N
+struct Skinny8Plan {
+    int C = 0;   // column blocks of 16 per workgroup; 0: not this kernel
+    int MB = 1;  // row blocks of 16
+};
+inline Skinny8Plan skinny8_plan(int64_t M, int64_t K, int64_t N, int64_t cus) {
+    Skinny8Plan p;
+    // x rows of a tile ((16 MB) * K * 4 bytes) through 32-bit offsets.
+    if (M < kSkinny8MinRows || M > kSkinny8MaxRows || K < 1 || K >= kSkinnyMaxK || N < 1) return p;
+    if (round_up(M, 8) * K * N < kSkinny8MinWork) return p;
+    if (M > kGemvMaxM && !linear_uses_gemv(M, K, N)) return p;
+    p.MB = M > 16 ? 2 : 1;
+    p.C = ceil_div(M, 16 * p.MB) * ceil_div(ceil_div(N, 4), 8) >= cus ? 2 : 1;
+    return p;
+}
 // Workspace of a skinny launch with NG weights: the K ranges' partial sums.
 inline int64_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t N, int NG) {
     return p.C > 0 && p.S > 1 ? (int64_t)NG * p.S * M * N * 4 : 0;
@@ -245,6 +269,9 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
                           bool per_tensor, const float* bias, float* y, hipStream_t s);
 hipError_t launch_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, hipStream_t s);
+// INT8 forward on k_skinny8 for a plan of skinny8_plan (C > 0).
+hipError_t launch_skinny_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                            bool per_tensor, const float* bias, const Skinny8Plan& p, float* y, hipStream_t s);
 // Skinny MFMA forward (plan p from skinny_plan, p.C > 0) of ng (1 or 2) tiled
 // INT4 weights of one shape on one input: ng == 1 writes y = x * W + bias,
 // ng == 2 the gated MLP h = silu(x * Wg + bg) * (x * Wu + bu).  With split K,

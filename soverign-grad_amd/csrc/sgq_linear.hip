@@ -1466,6 +1466,159 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
         }
 }
 
+// INT8 batches of a few to 128 rows of little work on the bf16 matrix cores
+// (src/quantization.cpp:189-197 for those shapes), the INT8 counterpart of
+// k_skinny3.  Each 16 rows of a row tile are the rows of one
+// v_mfma_f32_16x16x32_bf16 (MB row blocks share every B operand), with the
+// three-term split of k_gemm3: A = x (per tensor; the epilogue multiplies by
+// scales[0]) or x * scales[k] (per channel) as three bf16 planes, B = codes
+// (exact in bf16), fp32 accumulation.  A workgroup owns C column blocks of
+// 16 (4C strips) and MB row blocks over all of K; its NW wavefronts take the
+// 32-row k blocks in turn, U per batch of loads, every load of a batch issued
+// before the first is used, and are summed through LDS in wavefront order.
+// The order of every sum depends on K and NW only.
+//
+// B operand straight from the strip layout, without a transpose: dword d of
+// an INT8 chunk is column 4j + d over the chunk's four rows, so lane l
+// (g = l >> 4; column n = l & 15 of its block: strip n >> 2, dword n & 3)
+// takes that dword of row quads 2g and 2g + 1 of the k block, rows
+// 8g .. 8g + 7 of its column.  A block past the end reads x (and per-channel
+// scales) as zeros; its code dwords are whatever follows and are multiplied
+// by zero.
+struct Skinny8Args {
+    const float* x;  // [M, K]
+    int M, K, N;
+    const uint4* W;
+    const float* S;  // per tensor: scales[0]; per channel: scales[K]
+    const float* bias;
+    int RQ, NS, Kpad;
+    int ncg;      // column groups (workgroups per row tile)
+    FastDiv cgd;  // division by ncg
+    float* y;
+    int nblk;
+};
+
+template <int NW, int U, int C, int MB, bool PT, bool XA>
+__global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int K = a.K;
+    const int v = xcd_swizzle(blockIdx.x, a.nblk);  // row tile major: an XCD's workgroups share x rows
+    const int rt = a.cgd.div(v), cg = v - rt * a.ncg;
+    const int m0 = rt * 16 * MB, s0 = cg * 4 * C;
+    const int mrows = min(16 * MB, a.M - m0), nstr = min(4 * C, a.NS - s0);
+    // Rows past M and strips past NS lie past the ends of these buffers and read as zeros.
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)s0 * a.RQ, (uint32_t)nstr * (uint32_t)a.RQ * 16u);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.S, PT ? 4u : (uint32_t)K * 4u);
+    int wv[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) wv[c] = ((4 * c + (n >> 2)) * a.RQ + 2 * g) * 16 + (n & 3) * 4;
+    floatx4 acc[MB][C];
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[b][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int nkb = (a.Kpad + 31) >> 5;
+    for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
+        uint32_t w[U][C][2];
+        float xv[U][MB][8], sv[U][8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kb = kb0 + u * NW;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                w[u][c][0] = __builtin_amdgcn_raw_buffer_load_b32(rW, wv[c], kb * 128, 0);
+                w[u][c][1] = __builtin_amdgcn_raw_buffer_load_b32(rW, wv[c] + 16, kb * 128, 0);
+            }
+            const int k0 = kb * 32 + 8 * g;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kk = k0 + 4 * h;
+#pragma unroll
+                for (int b = 0; b < MB; ++b) {
+                    const int xo = (16 * b + n) * K * 4;
+                    if constexpr (XA) {
+                        const float4 xq = buf_load4f<true>(rX, kk < K ? xo + kk * 4 : kOobOff, 0);
+                        xv[u][b][4 * h] = xq.x, xv[u][b][4 * h + 1] = xq.y, xv[u][b][4 * h + 2] = xq.z,
+                                     xv[u][b][4 * h + 3] = xq.w;
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            xv[u][b][4 * h + i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                rX, kk + i < K ? xo + (kk + i) * 4 : kOobOff, 0, 0));
+                    }
+                }
+                if constexpr (!PT) {
+                    const float4 sq = buf_load4f<XA>(rS, kk * 4, 0);
+                    sv[u][4 * h] = sq.x, sv[u][4 * h + 1] = sq.y, sv[u][4 * h + 2] = sq.z, sv[u][4 * h + 3] = sq.w;
+                }
+            }
+        }
+        // Every load of the batch is issued before the first is used.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            bf16x8 bq[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+                // bytes of the column's dword in each chunk: k = 0..3, then 4..7
+                const uint32_t lo = w[u][c][0], hi = w[u][c][1];
+                const uint4 bb = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<1>(lo)),
+                                            pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<3>(lo)),
+                                            pack_hi16(cvt_sbyte<0>(hi), cvt_sbyte<1>(hi)),
+                                            pack_hi16(cvt_sbyte<2>(hi), cvt_sbyte<3>(hi)));
+                bq[c] = __builtin_bit_cast(bf16x8, bb);
+            }
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                float xs[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xs[i] = PT ? xv[u][b][i] : xv[u][b][i] * sv[u][i];
+                uint4 ah, am, al;
+                split3(xs, ah, am, al);
+#pragma unroll
+                for (int c = 0; c < C; ++c) {
+                    acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), bq[c], acc[b][c], 0, 0, 0);
+                    acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), bq[c], acc[b][c], 0, 0, 0);
+                    acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), bq[c], acc[b][c], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // Accumulator element r of lane l is output row 4 * (l >> 4) + r of
+    // column l & 15 of its block.  The wavefronts' partial tiles are summed
+    // in wavefront order through LDS; thread t then owns output t
+    // (t + NW * 64, ...): block bc = t >> 8, row (t >> 4) & 15, column t & 15.
+    constexpr int NBC = MB * C;
+    constexpr int OPT = (256 * NBC + NW * 64 - 1) / (NW * 64);
+    __shared__ float red[NW][NBC][4][64];
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][b * C + c][r][lane] = acc[b][c][r];
+    __syncthreads();
+    const float s_all = PT ? a.S[0] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+        const int t = threadIdx.x + i * NW * 64;
+        const int bc = t >> 8, mi = (t >> 4) & 15, nl = t & 15;
+        const int m = m0 + 16 * (bc / C) + mi, col = 16 * (cg * C + bc % C) + nl;
+        if (t < 256 * NBC && m < a.M && col < a.N) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) s += red[w2][bc][mi & 3][16 * (mi >> 2) + nl];
+            if constexpr (PT) s = s * s_all;
+            // h + m + l turns an infinite x into inf - inf: recompute a
+            // non-finite total as the reference's k-order sum.
+            if (!isfinite(s)) s = output_exact<8>(a.x + (int64_t)m * K, a.W, a.S, PT ? 1 : 0, a.Kpad, a.RQ, col, 0, K);
+            a.y[(int64_t)m * a.N + col] = a.bias ? s + a.bias[col] : s;
+        }
+    }
+}
+
 // The skinny kernel's K ranges added in range order, plus the bias; NG == 2:
 // h = silu(gate + bias) * (up + bias2).  part is [NG][S][M*N].
 template <int NG>
@@ -1754,7 +1907,50 @@ hipError_t skinny_dispatch(const SkinnyPlan& p, const float* x, int64_t M, int64
 #undef SGQ_SKINNY
 }
 
+template <int C, int MB, bool PT, bool XA>
+hipError_t skinny8_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                          const float* bias, float* y, hipStream_t s) {
+    const I8Geom g(K, N);
+    Skinny8Args a{};
+    a.x = x;
+    a.M = (int)M;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.W = (const uint4*)packed;
+    a.S = scales;
+    a.bias = bias;
+    a.RQ = (int)g.RQ;
+    a.NS = (int)g.NS;
+    a.Kpad = (int)g.Kpad;
+    a.ncg = (int)ceil_div(g.NS, 4 * C);
+    a.cgd = FastDiv((uint32_t)a.ncg);
+    a.y = y;
+    a.nblk = (int)(ceil_div(M, 16 * MB) * a.ncg);
+    constexpr int U = MB == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
+    k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_skinny_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
+                            bool per_tensor, const float* bias, const Skinny8Plan& p, float* y, hipStream_t s) {
+    const bool xa = x_aligned4(x, K);
+#define SGQ_SKINNY8(C_, MB_)                                                                      \
+    if (p.C == C_ && p.MB == MB_) {                                                                \
+        if (per_tensor)                                                                           \
+            return xa ? skinny8_launch<C_, MB_, true, true>(x, M, K, N, packed, scales, bias, y, s)  \
+                      : skinny8_launch<C_, MB_, true, false>(x, M, K, N, packed, scales, bias, y, s); \
+        return xa ? skinny8_launch<C_, MB_, false, true>(x, M, K, N, packed, scales, bias, y, s)     \
+                  : skinny8_launch<C_, MB_, false, false>(x, M, K, N, packed, scales, bias, y, s);   \
+    }
+    SGQ_SKINNY8(1, 1)
+    SGQ_SKINNY8(2, 1)
+    SGQ_SKINNY8(1, 2)
+    SGQ_SKINNY8(2, 2)
+#undef SGQ_SKINNY8
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_skinny_i4(const float* x, int64_t M, int64_t K, int64_t N, int ng, const void* const* packed,
                             const float* const* devscales, const float* const* bias, const I4Geom& g,
@@ -1909,6 +2105,9 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
             *ks = sp.S;
             return;
         }
+    } else if (skinny8_plan(M, K, N, cus < kMaxCus ? cus : kMaxCus).C > 0) {
+        *path = 4;
+        return;
     }
     if (linear_uses_gemv(M, K, N)) {
         *path = 0;

@@ -72,10 +72,13 @@ def test_workspace_sizes(lib):
 
 def test_swiglu_workspace_sizes(lib):
     # One-launch GEMV (tiled, M <= 16): none.  Otherwise the up projection
-    # (M*N floats, 256-byte aligned) followed by the GEMM's split-K partials.
+    # (M*N floats, 256-byte aligned) followed by the GEMM's split-K partials;
+    # INT8 batches of the skinny kernel need the up projection only.
     assert lib.sgq_swiglu_workspace_bytes(4, 1, 4096, 11008, 128) == 0
     assert lib.sgq_swiglu_workspace_bytes(8, 16, 1024, 1024, 0) == 0
-    assert lib.sgq_swiglu_workspace_bytes(8, 128, 1024, 1024, 0) == 0  # GEMV form, as the plain forward
+    assert lib.sgq_swiglu_workspace_bytes(8, 32, 1024, 1024, 0) == 0  # GEMV form, as the plain forward
+    assert lib.sgq_swiglu_workspace_bytes(8, 128, 1024, 1024, 0) == 128 * 1024 * 4  # skinny kernel, twice
+    assert lib.sgq_swiglu_workspace_bytes(8, 8, 4096, 4096, 0) == 8 * 4096 * 4
     assert lib.sgq_swiglu_workspace_bytes(4, 2048, 4096, 4096, 128) == 2048 * 4096 * 4
     u = 256 * 1024 * 4
     assert lib.sgq_swiglu_workspace_bytes(8, 256, 4096, 1024, 0) == u + lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)
@@ -290,6 +293,30 @@ def test_plan_follows_the_device_cu_count(lib):
     assert lib.sgq_linear_plan(8, 1, 4, 4, 0, -1, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == 1
 
 
+def test_plan_skinny_int8(lib):
+    """INT8 batches of 5..128 rows take the skinny bf16 MFMA kernel (path 4,
+    no K split) once (M rounded up to 8) * K * N reaches 2^26; above 16 rows
+    only within the GEMV's small work (M * K * N <= 2^28).  Four rows and less
+    work stay on the GEMV; larger work above 16 rows on the GEMM.  The choice
+    does not depend on the CU count."""
+    for cus in (256, 80, 8):
+        assert _plan(lib, 8, 128, 1024, 1024, 0, cus) == (4, 1)  # C1
+        assert _plan(lib, 8, 4, 4096, 4096, 0, cus) == (0, 1)
+        for M in (5, 8, 16):
+            assert _plan(lib, 8, M, 4096, 4096, 0, cus) == (4, 1)
+            assert _plan(lib, 8, M, 11008, 4096, 0, cus) == (4, 1)
+        assert _plan(lib, 8, 8, 2048, 2048, 0, cus) == (0, 1)  # 2^25
+        assert _plan(lib, 8, 9, 2048, 2048, 0, cus) == (4, 1)  # 16 * 2^22 = 2^26
+        assert _plan(lib, 8, 16, 1024, 1024, 0, cus) == (0, 1)
+        assert _plan(lib, 8, 17, 1024, 1024, 0, cus) == (0, 1)  # 24 * 2^20 < 2^26
+        assert _plan(lib, 8, 64, 1024, 1024, 0, cus) == (4, 1)
+        assert _plan(lib, 8, 64, 2048, 2048, 0, cus) == (4, 1)  # 2^28
+        assert _plan(lib, 8, 65, 2048, 2048, 0, cus)[0] == 1
+        assert _plan(lib, 8, 17, 4096, 4096, 0, cus)[0] == 1
+        assert _plan(lib, 8, 129, 1024, 1024, 0, cus)[0] == 1
+    assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0
+
+
 def test_plan_skinny_mfma(lib):
     """Batches of 5..16 rows over a wide INT4 weight take the skinny bf16 MFMA
     kernel (path 4, whole K) when its 32- or 64-column workgroups fill at least
@@ -314,7 +341,7 @@ def test_plan_skinny_mfma(lib):
     assert _plan(lib, 4, 8, 4096, 4096, 128, 256) == (0, 1)  # 2^27: the GEMV
     assert _plan(lib, 4, 9, 4096, 4096, 128, 256) == (4, 4)
     assert _plan(lib, 4, 32, 4096, 4096, 128, 256) == (4, 4)
-    assert _plan(lib, 8, 8, 4096, 11008, 0, 256) == (0, 1)  # INT8 stays on the GEMV
+    assert _plan(lib, 8, 8, 4096, 11008, 0, 256) == (4, 1)  # INT8: its own skinny kernel, no split
     assert _plan(lib, 4, 8, 2048, 6144, 8, 256) == (0, 1)  # one strip per scale column
     assert _plan(lib, 4, 8, 2048, 6144, 16, 256) == (0, 1)  # two strips: 16 columns, too narrow
     assert _plan(lib, 4, 8, 2048, 5120, 32, 256) == (4, 1)  # four strips: 160 workgroups of 32

@@ -31,7 +31,9 @@ def _weights(sgq, dev, synth, bits_, K, N, G, scheme, seed):
         ("gemv_int4_M1", 4, 1, 4096, 4096, 128, 0, False),
         ("gemv_int4_M8", 4, 8, 2048, 6144, 128, 0, True),
         ("gemv_int8_M5", 8, 5, 1000, 700, 0, 1, True),
-        ("gemm_int8_splitk_M128", 8, 128, 1024, 1024, 0, 0, True),
+        ("skinny_int8_M128", 8, 128, 1024, 1024, 0, 0, True),
+        ("skinny_int8_pc_M8", 8, 8, 4096, 4096, 0, 1, False),
+        ("gemm_int8_splitk_M256", 8, 256, 4096, 1024, 0, 0, True),
         ("gemm_int8_pc_M300", 8, 300, 1024, 768, 0, 1, False),
         ("gemm_int4_M256", 4, 256, 1024, 1024, 128, 0, True),
         ("gemm_int4_g32_M40", 4, 40, 512, 256, 32, 0, True),
@@ -66,7 +68,7 @@ def test_linear_graph_replays_match_eager(sgq, dev, synth, name, bits_, M, K, N,
         assert helpers.same_bits(y2.cpu().numpy(), y2_eager.cpu().numpy()), (name, rep)
 
 
-@pytest.mark.parametrize("bits_,M", [(4, 8), (4, 64), (8, 3)])
+@pytest.mark.parametrize("bits_,M", [(4, 8), (4, 64), (8, 3), (8, 64)])
 def test_swiglu_graph_replays_match_eager(sgq, dev, synth, bits_, M):
     K, N, G = 1024, 1536, 128
     wg = _weights(sgq, dev, synth, bits_, K, N, G, 0, 81)
