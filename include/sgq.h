@@ -112,7 +112,7 @@ int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
  * device with workgroups of 32 or 64 columns, and 5..32 rows over narrower
  * weights with (M rounded up to 8) * K * N >= 2^28, K split; INT8: 5..128
  * rows with (M rounded up to 8) * K * N >= 2^26, above 16 rows only while
- * M * K * N <= 2^28, whole K).  *k_splits: 1, or the number of
+ * M * K * N <= 2^29, whole K).  *k_splits: 1, or the number of
  * workgroups sharing each output tile's K range (the GEMM on grids smaller
  * than the device, the skinny kernel's K ranges).  sgq_linear_workspace_bytes sizes for the
  * largest device, so it covers every plan.  Host-only; this library's own
@@ -196,7 +196,7 @@ int sgq_dequantize_codes(const float* qdata_f32, const float* scales, int bits, 
  *   y[M,N] = x[M,K] . (codes * scales) (+ bias[N])   fp32 accumulate.
  * scales are the reference-layout scales (1 or K floats).  bias may be NULL.
  * Dispatch (sgq_linear_plan): 5..128 rows with (M rounded up to 8) * K * N
- * >= 2^26 (above 16 rows only while M * K * N <= 2^28) run the skinny bf16
+ * >= 2^26 (above 16 rows only while M * K * N <= 2^29) run the skinny bf16
  * MFMA kernel (whole K per workgroup, no workspace); other batches of up to
  * 16 rows, and up to 128 rows with M * K * N <= 2^28, the wavefront GEMV (row
  * groups of 8); larger batches the LDS-staged MFMA GEMM.  Both MFMA kernels

@@ -67,6 +67,8 @@ int64_t int4_groups(int64_t total, int64_t G) { return ceil_div(total, G <= 0 ? 
 // size is the largest either could need on any device and for any group
 // size (neither is an argument here).
 int64_t linear_ws_bytes(int bits, int64_t M, int64_t K, int64_t N) {
+    // The INT8 skinny kernel's batches (on any device) need none.
+    if (bits == 8 && skinny8_plan(M, K, N, kMaxCus).C > 0) return 0;
     const int64_t gemm = linear_uses_gemv(M, K, N) ? 0 : gemm_workspace_bytes(M, K, N);
     const int64_t skinny = bits == 4 ? skinny_ws_bound(M, K, N, 1) : 0;
     return gemm > skinny ? gemm : skinny;
@@ -95,10 +97,11 @@ int64_t swiglu_ws_bytes(int bits, bool flat, int64_t M, int64_t K, int64_t N, in
     int64_t other = 0;
     // The one-launch GEMV form takes the batches the plain forward runs on the
     // GEMV; INT8 batches of the skinny kernel run it once per weight, up into
-    // the workspace (no split K: those batches are within the GEMV's).
+    // the workspace (no split K).
     const bool skinny8 = bits == 8 && K > 0 && skinny8_plan(M, K, N, kMaxCus).C > 0;
     if (flat || skinny8 || !linear_uses_gemv(M, K, N) || K == 0) {
-        const int64_t split = (!flat && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
+        const int64_t split =
+            (!flat && !skinny8 && !linear_uses_gemv(M, K, N)) ? gemm_workspace_bytes(M, K, N) : 0;
         other = align_up(M * N * 4) + split;
     }
     return skinny > other ? skinny : other;

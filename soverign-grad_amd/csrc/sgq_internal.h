@@ -194,12 +194,19 @@ inline SkinnyPlan skinny_plan(int64_t M, int64_t K, const I4Geom& g, int64_t cus
 // blocks of 16 (two above 16 rows) by C column blocks of 16 over all of K, no
 // workspace.  C = 2 where that still gives a workgroup per CU.  The GEMV
 // keeps four rows and little work (its time is a fixed ~3 us plus
-// round_up(M, 8) * K * N at the VALU rate); above 16 rows the GEMM keeps the
-// shapes past the GEMV's small work (its wider tiles read each x row for more
-// columns).
+// round_up(M, 8) * K * N at the VALU rate); above 16 rows the GEMM keeps
+// M * K * N > 2^29 (its wider tiles read each x row for more columns).
+// Measured on MI355X (INT8 per tensor, us, GEMV or GEMM -> skinny): 1024^2 at
+// 128 rows 11.2 -> 6.8; 2048^2 at 9 / 64 / 128 rows 6.5 / 16.8 / 27.5 -> 5.7
+// / 11.2 / 12.5; 4096^2 at 8 / 16 / 32 rows 11.0 / 17.2 / 20.3 -> 9.3 / 11.8
+// / 19.6.  Left to the GEMV: 1024^2 at 16 rows (3.9 vs 5.5), 2048^2 at 8
+// (4.7 vs 5.6).  Left to the GEMM: 4096^2 at 80 / 128 rows (30.6 / 33.9 vs
+// 40.2 / 41.4), 4096 -> 11008 at 32 rows (28.6 vs 41.5); 4096^2 at 64 rows
+// (24.6 vs 22.2) falls past the bound too.
 constexpr int64_t kSkinny8MinRows = 5;
 constexpr int64_t kSkinny8MaxRows = 128;
 constexpr int64_t kSkinny8MinWork = (int64_t)1 << 26;  // round_up(M, 8) * K * N
+constexpr int64_t kSkinny8MaxWork = (int64_t)1 << 29;  // M * K * N, above 16 rows
 struct Skinny8Plan {
     int C = 0;   // column blocks of 16 per workgroup; 0: not this kernel
     int MB = 1;  // row blocks of 16
@@ -209,7 +216,7 @@ inline Skinny8Plan skinny8_plan(int64_t M, int64_t K, int64_t N, int64_t cus) {
     // x rows of a tile ((16 MB) * K * 4 bytes) through 32-bit offsets.
     if (M < kSkinny8MinRows || M > kSkinny8MaxRows || K < 1 || K >= kSkinnyMaxK || N < 1) return p;
     if (round_up(M, 8) * K * N < kSkinny8MinWork) return p;
-    if (M > kGemvMaxM && !linear_uses_gemv(M, K, N)) return p;
+    if (M > kGemvMaxM && M * K * N > kSkinny8MaxWork) return p;
     p.MB = M > 16 ? 2 : 1;
     p.C = ceil_div(M, 16 * p.MB) * ceil_div(ceil_div(N, 4), 8) >= cus ? 2 : 1;
     return p;

@@ -57,7 +57,7 @@ def test_workspace_sizes(lib):
     assert lib.sgq_linear_workspace_bytes(4, 8, 4096, 4096) == 0
     assert lib.sgq_linear_workspace_bytes(4, 16, 4096, 4096) == 4 * 16 * 4096 * 4
     assert lib.sgq_linear_workspace_bytes(8, 16, 4096, 4096) == 0
-    assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0  # GEMV: 2^27 multiply-adds
+    assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0  # INT8 skinny kernel: whole K
     assert lib.sgq_linear_workspace_bytes(8, 2048, 4096, 4096) == 0  # 256 or 512 tiles
     ws = lib.sgq_linear_workspace_bytes(8, 256, 4096, 1024)  # GEMM of 8 or 16 tiles: split K
     assert ws > 0 and ws % (256 * 1024 * 4) == 0 and 2 <= ws // (256 * 1024 * 4) <= 16
@@ -296,9 +296,9 @@ def test_plan_follows_the_device_cu_count(lib):
 def test_plan_skinny_int8(lib):
     """INT8 batches of 5..128 rows take the skinny bf16 MFMA kernel (path 4,
     no K split) once (M rounded up to 8) * K * N reaches 2^26; above 16 rows
-    only within the GEMV's small work (M * K * N <= 2^28).  Four rows and less
-    work stay on the GEMV; larger work above 16 rows on the GEMM.  The choice
-    does not depend on the CU count."""
+    only while M * K * N <= 2^29.  Four rows and less work stay on the GEMV;
+    larger work above 16 rows on the GEMM.  The choice does not depend on the
+    CU count, and the kernel needs no workspace."""
     for cus in (256, 80, 8):
         assert _plan(lib, 8, 128, 1024, 1024, 0, cus) == (4, 1)  # C1
         assert _plan(lib, 8, 4, 4096, 4096, 0, cus) == (0, 1)
@@ -310,11 +310,15 @@ def test_plan_skinny_int8(lib):
         assert _plan(lib, 8, 16, 1024, 1024, 0, cus) == (0, 1)
         assert _plan(lib, 8, 17, 1024, 1024, 0, cus) == (0, 1)  # 24 * 2^20 < 2^26
         assert _plan(lib, 8, 64, 1024, 1024, 0, cus) == (4, 1)
-        assert _plan(lib, 8, 64, 2048, 2048, 0, cus) == (4, 1)  # 2^28
-        assert _plan(lib, 8, 65, 2048, 2048, 0, cus)[0] == 1
-        assert _plan(lib, 8, 17, 4096, 4096, 0, cus)[0] == 1
+        assert _plan(lib, 8, 64, 2048, 2048, 0, cus) == (4, 1)
+        assert _plan(lib, 8, 128, 2048, 2048, 0, cus) == (4, 1)  # 2^29
+        assert _plan(lib, 8, 32, 4096, 4096, 0, cus) == (4, 1)  # 2^29
+        assert _plan(lib, 8, 128, 2048, 2056, 0, cus)[0] == 1
+        assert _plan(lib, 8, 33, 4096, 4096, 0, cus)[0] == 1
         assert _plan(lib, 8, 129, 1024, 1024, 0, cus)[0] == 1
-    assert lib.sgq_linear_workspace_bytes(8, 128, 1024, 1024) == 0
+    for M, K, N in [(128, 1024, 1024), (128, 2048, 2048), (32, 4096, 4096), (16, 11008, 4096)]:
+        assert lib.sgq_linear_workspace_bytes(8, M, K, N) == 0
+        assert lib.sgq_swiglu_workspace_bytes(8, M, K, N, 0) == M * N * 4  # the up projection only
 
 
 def test_plan_skinny_mfma(lib):

@@ -54,13 +54,14 @@ def _quantized(sgq, dev, oracle, synth, K, N, scheme, seed):
 
 
 def test_skinny_int8_boundaries(sgq, dev):
-    # Four rows and little work stay on the GEMV; above 16 rows, shapes past
-    # the GEMV's small work take the GEMM.
+    # Four rows and little work stay on the GEMV; above 16 rows, shapes with
+    # M * K * N > 2^29 take the GEMM.
     assert _path(sgq, 4, 4096, 4096) == (0, 1)
     assert _path(sgq, 8, 2048, 2048) == (0, 1)
     assert _path(sgq, 32, 1024, 1024) == (0, 1)
     assert _path(sgq, 129, 1024, 1024)[0] == 1
-    assert _path(sgq, 32, 4096, 4096)[0] == 1
+    assert _path(sgq, 33, 4096, 4096)[0] == 1
+    assert _path(sgq, 128, 2048, 2056)[0] == 1
     for M in (5, 8, 16):
         assert _path(sgq, M, 4096, 4096) == (SKINNY, 1)
     assert _path(sgq, 17, 1024, 1024) == (0, 1)
@@ -78,7 +79,8 @@ def test_skinny_int8_boundaries(sgq, dev):
 @pytest.mark.parametrize("M,K,N", [(128, 1024, 1024), (100, 1024, 1024), (65, 1024, 1024), (17, 2048, 2048),
                                    (48, 2048, 2048), (5, 4096, 4096), (8, 4096, 4096), (13, 4096, 4096),
                                    (16, 4096, 4096), (16, 4096, 11008), (16, 11008, 4096), (96, 1040, 1000),
-                                   (40, 2051, 1034), (12, 4100, 4098)])
+                                   (40, 2051, 1034), (12, 4100, 4098), (32, 4096, 4096), (128, 2048, 2048),
+                                   (128, 4096, 1024)])
 def test_skinny_int8_shapes(sgq, dev, oracle, synth, scheme, M, K, N):
     assert _path(sgq, M, K, N) == (SKINNY, 1)
     W, b, qw, (q, s) = _quantized(sgq, dev, oracle, synth, K, N, scheme, 81)
