@@ -317,8 +317,10 @@ int64_t sgq_llama_decode_workspace_bytes(int64_t B, int64_t D, int64_t H, int64_
  *              16-byte aligned.
  * Batches the forward runs on the GEMV (B <= 16, or up to 128 when every
  * projection's B * K * N <= 2^28) run every projection on it (q, k, v in one
- * launch; the RMSNorms folded in; the residual adds in the epilogues);
- * larger B on the MFMA GEMM.  fp32 results throughout;
+ * launch; the RMSNorms folded in; the residual adds in the epilogues), except
+ * that 5..16 rows run the norm-fused q/k/v and gate/up launches on the skinny
+ * bf16 MFMA kernel where its plan takes the projection's total width (e.g.
+ * the NanoLLaMA shape); larger B on the MFMA GEMM.  fp32 results throughout;
  * outputs match the reference's full-sequence forward within 1e-5 relative. */
 int sgq_llama_block_decode_int4(const sgq_llama_block_int4* block, const float* x, float* out, int64_t B,
                                 float* k_cache, float* v_cache, int64_t max_tokens, const int32_t* pos,

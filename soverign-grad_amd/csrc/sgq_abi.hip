@@ -121,6 +121,17 @@ bool decode_uses_gemv(int64_t B, int64_t D, int64_t H) {
     return linear_uses_gemv(B, D, 3 * D) && linear_uses_gemv(B, D, H) && linear_uses_gemv(B, H, D);
 }
 
+// The block's norm-fused projections on the GEMV path run the skinny MFMA
+// kernel's whole-K form instead where the forward's plan gives it for the
+// projection's total width (q, k and v side by side: 3 * N), with two column
+// blocks per workgroup (the norm-fused form), which must tile each weight.
+SkinnyPlan decode_skinny_plan(int64_t B, int64_t K, int64_t N, int nw, int64_t G, int cus) {
+    const I4Geom g(K, N, G);
+    SkinnyPlan p = skinny_plan(B, K, I4Geom(K, nw * N, G), cus);
+    if (p.C == 0 || p.form != 0 || p.S != 1 || g.spc % 4 != 0 || g.NS % 4 != 0) return SkinnyPlan{};
+    return p;
+}
+
 DecodeWs decode_ws(int64_t B, int64_t D, int64_t H, int64_t max_len) {
     DecodeWs w;
     int64_t o = 0;
@@ -740,12 +751,24 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
     // attn->forward(norm1->forward(x)), then the residual: h = x + o(ctx).
     // The GEMV path applies each RMSNorm inside the projection that reads it.
     const bool gemv = decode_uses_gemv(B, D, H);
+    const int cus = gemv ? device_cus(s) : 0;
     if (gemv) {
         const void* pk[3] = {blk->q.packed, blk->k.packed, blk->v.packed};
         const float* ds[3] = {blk->q.devscales, blk->k.devscales, blk->v.devscales};
         const float* bs[3] = {blk->q.bias, blk->k.bias, blk->v.bias};
-        SGQ_HIP(launch_gemv_i4_multi(x, B, D, D, 3, pk, ds, bs, gdd, qkv, 3 * D, nullptr, blk->norm1, blk->eps, s),
-                "gemv_qkv");
+        const SkinnyPlan sq = decode_skinny_plan(B, D, D, 3, G, cus);
+        if (sq.C > 0) {
+            SkinnyExtra ex;
+            ex.nw = 3;
+            ex.ldy = 3 * D;
+            ex.gamma = blk->norm1;
+            ex.eps = blk->eps;
+            SGQ_HIP(launch_skinny_i4(x, B, D, D, 1, pk, ds, bs, gdd, sq, qkv, nullptr, s, &ex), "skinny_qkv");
+        } else {
+            SGQ_HIP(launch_gemv_i4_multi(x, B, D, D, 3, pk, ds, bs, gdd, qkv, 3 * D, nullptr, blk->norm1, blk->eps,
+                                         s),
+                    "gemv_qkv");
+        }
         SGQ_HIP(launch_attention_decode(qkv, qkv + D, qkv + 2 * D, 3 * D, B, D, k_cache, v_cache, max_tokens, pos,
                                         max_len, blk->attn_scale, part, ctx, s),
                 "attention");
@@ -769,10 +792,21 @@ int sgq_llama_block_decode_int4(const sgq_llama_block_int4* blk, const float* x,
     }
     // h + mlp->forward(norm2->forward(h))
     if (gemv) {
-        SGQ_HIP(launch_swiglu_gemv_i4(h, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
-                                      blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s, blk->norm2,
-                                      blk->eps),
-                "swiglu_gemv");
+        const SkinnyPlan sg = decode_skinny_plan(B, D, H, 1, G, cus);
+        if (sg.C > 0) {
+            const void* pk[2] = {blk->gate.packed, blk->up.packed};
+            const float* ds[2] = {blk->gate.devscales, blk->up.devscales};
+            const float* bs[2] = {blk->gate.bias, blk->up.bias};
+            SkinnyExtra ex;
+            ex.gamma = blk->norm2;
+            ex.eps = blk->eps;
+            SGQ_HIP(launch_skinny_i4(h, B, D, H, 2, pk, ds, bs, gdh, sg, hid, nullptr, s, &ex), "skinny_gate_up");
+        } else {
+            SGQ_HIP(launch_swiglu_gemv_i4(h, B, D, H, blk->gate.packed, blk->gate.devscales, blk->gate.bias,
+                                          blk->up.packed, blk->up.devscales, blk->up.bias, gdh, hid, s, blk->norm2,
+                                          blk->eps),
+                    "swiglu_gemv");
+        }
         SGQ_HIP(launch_gemv_i4_multi(hid, B, H, D, 1, &blk->down.packed, &blk->down.devscales, &blk->down.bias, ghd,
                                      out, D, h, nullptr, 0.0f, s),
                 "gemv_down");

@@ -283,9 +283,20 @@ hipError_t launch_skinny_i8(const float* x, int64_t M, int64_t K, int64_t N, con
 // INT4 weights of one shape on one input: ng == 1 writes y = x * W + bias,
 // ng == 2 the gated MLP h = silu(x * Wg + bg) * (x * Wu + bu).  With split K,
 // ws holds skinny_ws_bytes(p, M, N, ng) bytes (16-byte aligned).
+// The whole-K form (p.form == 0, p.S == 1) can also run nw (1..3, ng == 1)
+// weights of one shape side by side, weight w writing columns w * N .. w * N
+// + N - 1 of rows of ldy floats, and fold an RMSNorm of x (gamma, eps) into
+// the projections, as launch_gemv_i4_multi does.
+struct SkinnyExtra {
+    int nw = 1;
+    int64_t ldy = 0;  // 0: N
+    const float* gamma = nullptr;
+    float eps = 0.0f;
+};
 hipError_t launch_skinny_i4(const float* x, int64_t M, int64_t K, int64_t N, int ng, const void* const* packed,
                             const float* const* devscales, const float* const* bias, const I4Geom& g,
-                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s);
+                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s,
+                            const SkinnyExtra* extra = nullptr);
 // nw (1..3) tiled INT4 weights of one shape [K, N] side by side on one input:
 // weight w writes y[m * ldy + w * N + n] (+ res at the same index when res is
 // set).  gamma (optional): the input is rms_norm(x, gamma, eps), applied

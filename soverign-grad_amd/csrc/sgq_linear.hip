@@ -1079,16 +1079,23 @@ __device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
 struct SkinnyArgs {
     const float* x;  // [M, K]
     int M, K, N;
-    const uint4* W[2];  // NG weights of equal shape (gate, up)
-    const float* SC[2];
-    const float* bias[2];
+    const uint4* W[3];  // NG weights of equal shape (gate, up), or (NG == 1) nw weights side by side
+    const float* SC[3];
+    const float* bias[3];
     int spc, Kpad, RQ;
     FastDiv wpc;  // workgroups (column groups) per scale column
-    float* y;     // [M, N]
+    float* y;     // [M, ldy]
     float* part;  // split K: [NG][2^slog][M][N] partial sums
     int nblk;     // grid size
     int slog;     // log2 of the number of K ranges
     int sbs;      // super-blocks (128 rows) per K range
+    // Whole-K form only: weight w of nw side by side writes columns
+    // w * N .. w * N + N - 1 of y; NORM: the RMSNorm weight and epsilon.
+    int ldy;
+    int wgpw;     // workgroups per weight
+    FastDiv wgd;  // division by wgpw
+    const float* gamma;
+    float eps;
 };
 
 // The whole-K form for one row block (5..16 rows over wide weights, no K
@@ -1097,24 +1104,43 @@ struct SkinnyArgs {
 // used.  Lane (g, e) of strip j loads one dword, row 8g + e of its strip in
 // k block kb, and an 8x8 nibble transpose leaves it with rows 8g .. 8g + 7 of
 // column e (its B operand); x and the scales are loaded per k block.  NG == 2:
-// the gated MLP, h = silu(gate + bias) * (up + bias2).  XA: x rows are
-// 16-byte aligned and K % 4 == 0 (float4 loads); otherwise one float per load.
-template <int NW, int U, int C, int NG, bool XA>
+// the gated MLP, h = silu(gate + bias) * (up + bias2).  NG == 1 runs a.wgpw
+// workgroups per weight over nw weights of one shape side by side (a LLaMA
+// block's q, k and v).  XA: x rows are 16-byte aligned and K % 4 == 0 (float4
+// loads); otherwise one float per load.
+//
+// NORM: the input rows are RMS-normalised first (rms_norm, src/ops.cpp:
+// 1532-1556: x * inv_rms * gamma, inv_rms = 1 / sqrt(sum(x^2) / K + eps)), as
+// in the GEMV: A = x * (gamma * s), and the epilogue multiplies by inv_rms,
+// one factor per row, from the sum of x^2 over the rows the workgroup reads.
+template <int NW, int U, int C, int NG, bool XA, bool NORM>
 __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int K = a.K;
-    const int v = xcd_swizzle(blockIdx.x, a.nblk);
+    const int vv = xcd_swizzle(blockIdx.x, a.nblk);
+    const int wt = NG == 1 ? a.wgd.div(vv) : 0;  // weight of the side-by-side set
+    const int v = vv - wt * a.wgpw;
     const int blk0 = v * C;  // first column block
     const int sc = a.wpc.div(v);
+    const uint4* Wq[NG];
+    const float* SCq[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        Wq[q] = a.W[NG == 1 ? wt : q];
+        SCq[q] = a.SC[NG == 1 ? wt : q];
+    }
     __amdgpu_buffer_rsrc_t rW[NG], rS[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        rW[q] = make_rsrc(a.W[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
-        rS[q] = make_rsrc(a.SC[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
+        rW[q] = make_rsrc(Wq[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
+        rS[q] = make_rsrc(SCq[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
     }
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
+    __amdgpu_buffer_rsrc_t rG;
+    if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
+    float sq = 0.0f;  // NORM: sum of x^2 of this lane's row over its k
     int wv[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + 32 * g + 4 * e;
@@ -1132,7 +1158,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     // and are multiplied by zero), so partial batches need no branch.
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][NG][C];
-        float xv[U][8], sv[U][NG][8];
+        float xv[U][8], sv[U][NG][8], gv[NORM ? U : 1][8];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kb = kb0 + u * NW;
@@ -1156,21 +1182,29 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                 }
 #pragma unroll
                 for (int q = 0; q < NG; ++q) {
-                    const float4 sq = buf_load4f<true>(rS[q], kk * 4, 0);
-                    sv[u][q][4 * h] = sq.x, sv[u][q][4 * h + 1] = sq.y, sv[u][q][4 * h + 2] = sq.z,
-                                 sv[u][q][4 * h + 3] = sq.w;
+                    const float4 s4 = buf_load4f<true>(rS[q], kk * 4, 0);
+                    sv[u][q][4 * h] = s4.x, sv[u][q][4 * h + 1] = s4.y, sv[u][q][4 * h + 2] = s4.z,
+                                 sv[u][q][4 * h + 3] = s4.w;
+                }
+                if constexpr (NORM) {
+                    const float4 g4 = buf_load4f<XA>(rG, kk * 4, 0);
+                    gv[u][4 * h] = g4.x, gv[u][4 * h + 1] = g4.y, gv[u][4 * h + 2] = g4.z, gv[u][4 * h + 3] = g4.w;
                 }
             }
         }
         // Every load of the batch is issued before the first is used.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u) {
+            if constexpr (NORM) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sq = fmaf(xv[u][i], xv[u][i], sq);
+            }
 #pragma unroll
             for (int q = 0; q < NG; ++q) {
                 float xs[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xs[i] = xv[u][i] * sv[u][q][i];
+                for (int i = 0; i < 8; ++i) xs[i] = NORM ? xv[u][i] * (gv[u][i] * sv[u][q][i]) : xv[u][i] * sv[u][q][i];
                 uint4 ah, am, al;
                 split3(xs, ah, am, al);
 #pragma unroll
@@ -1181,6 +1215,24 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), b, acc[q][c], 0, 0, 0);
                 }
             }
+        }
+    }
+    // NORM: the rows' sums of x^2 added in a fixed order: the four lane
+    // groups of a wavefront by lane exchanges, then the wavefronts through
+    // LDS; inv_rms per row.
+    __shared__ float sqr[NORM ? NW : 1][16];
+    __shared__ float inv_rms[16];
+    if constexpr (NORM) {
+        sq += xor_lane<32>(sq, lane);
+        sq += xor_lane<16>(sq, lane);
+        if (lane < 16) sqr[wave][lane] = sq;
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) ss += sqr[w2][threadIdx.x];
+            inv_rms[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
+        }
     }
     // Accumulator element r of lane l is output row 4 * (l >> 4) + r of
     // column lane l & 15 of its block.  The wavefronts' partial tiles are
@@ -1211,9 +1263,11 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                 // h + m + l turns an infinite x * s into inf - inf: recompute
                 // a non-finite total as the reference's k-order sum.
                 if (!isfinite(s))
-                    s = i4_column_exact<false>(a.W[q], a.SC[q], strip, el, a.spc, a.Kpad, a.RQ, a.x + (int64_t)m * K,
-                                               nullptr, 0, K);
-                if (a.bias[q]) s = s + a.bias[q][col];
+                    s = i4_column_exact<NORM>(Wq[q], SCq[q], strip, el, a.spc, a.Kpad, a.RQ, a.x + (int64_t)m * K,
+                                              a.gamma, 0, K);
+                if constexpr (NORM) s = s * inv_rms[m];
+                const float* bq = a.bias[NG == 1 ? wt : q];
+                if (bq) s = s + bq[col];
             }
             o[q][i] = s;
         }
@@ -1226,7 +1280,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
         if (t < 256 * C && m < a.M && col < a.N) {
             float r0 = o[0][i];
             if constexpr (NG == 2) r0 = silu_f32(o[0][i]) * o[1][i];
-            a.y[(int64_t)m * a.N + col] = r0;
+            a.y[(int64_t)m * a.ldy + (int64_t)wt * a.N + col] = r0;
         }
     }
 }
@@ -1833,18 +1887,27 @@ constexpr int kSkinnyWholeKWaves = 16;
 template <int C, int NG, int MB, bool XA>
 hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* const* packed,
                          const float* const* devscales, const float* const* bias, const I4Geom& g, int form, int S,
-                         float* y, float* part, hipStream_t s) {
+                         float* y, float* part, const SkinnyExtra& ex, hipStream_t s) {
     if (form == 0 && S != 1) return hipErrorInvalidValue;
+    // Side-by-side weights, a row stride and the folded RMSNorm: whole-K form only.
+    const bool plain = ex.nw == 1 && ex.ldy == N && !ex.gamma;
+    if ((!plain && form != 0) || ex.nw < 1 || ex.nw > 3 || (NG == 2 && ex.nw != 1)) return hipErrorInvalidValue;
     SkinnyArgs a{};
     a.x = x;
     a.M = (int)M;
     a.K = (int)K;
     a.N = (int)N;
-    for (int q = 0; q < NG; ++q) {
+    const int nq = NG == 1 ? ex.nw : NG;
+    for (int q = 0; q < nq; ++q) {
         a.W[q] = (const uint4*)packed[q];
         a.SC[q] = devscales[q];
         a.bias[q] = bias[q];
     }
+    a.ldy = (int)ex.ldy;
+    a.wgpw = (int)(g.NS / (2 * C));
+    a.wgd = FastDiv((uint32_t)a.wgpw);
+    a.gamma = ex.gamma;
+    a.eps = ex.eps;
     a.spc = (int)g.spc;
     a.Kpad = (int)g.Kpad;
     a.RQ = (int)g.RQ;
@@ -1859,7 +1922,16 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     if (form == 0) {
         if constexpr (MB == 1) {
             constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
-            k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+            a.nblk *= ex.nw;
+            if (ex.gamma) {
+                // The norm-fused form keeps two column blocks (register budget).
+                if constexpr (C == 2)
+                    k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, true><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+                else
+                    return hipErrorInvalidValue;
+            } else {
+                k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+            }
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
@@ -1883,20 +1955,22 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
 template <int NG>
 hipError_t skinny_dispatch(const SkinnyPlan& p, const float* x, int64_t M, int64_t K, int64_t N,
                            const void* const* packed, const float* const* devscales, const float* const* bias,
-                           const I4Geom& g, float* y, float* part, hipStream_t s) {
+                           const I4Geom& g, float* y, float* part, const SkinnyExtra& ex, hipStream_t s) {
     // The super-block form of the gated MLP, and two row blocks of
     // unaligned x, keep two column blocks per workgroup, within the register
     // budget (C does not change the order of any sum).
     if (p.C != 2 && p.C != 4) return hipErrorInvalidValue;
 #define SGQ_SKINNY(C_, MB_, XA_) \
-    return skinny_launch<C_, NG, MB_, XA_>(x, M, K, N, packed, devscales, bias, g, p.form, p.S, y, part, s)
+    return skinny_launch<C_, NG, MB_, XA_>(x, M, K, N, packed, devscales, bias, g, p.form, p.S, y, part, ex, s)
     const bool xa = x_aligned4(x, K);
-    if (p.C == 4 && p.MB == 1 && (NG == 1 || p.form == 0)) {
+    // The norm-fused form runs two column blocks per workgroup (C does not
+    // change the order of any sum).
+    if (p.C == 4 && p.MB == 1 && (NG == 1 || p.form == 0) && !ex.gamma) {
         if (xa) SGQ_SKINNY(4, 1, true);
         SGQ_SKINNY(4, 1, false);
     }
     if constexpr (NG == 1) {
-        if (p.C == 4 && xa) SGQ_SKINNY(4, 2, true);
+        if (p.C == 4 && xa && !ex.gamma) SGQ_SKINNY(4, 2, true);
     }
     if (p.MB == 1) {
         if (xa) SGQ_SKINNY(2, 1, true);
@@ -1954,10 +2028,13 @@ hipError_t launch_skinny_i8(const float* x, int64_t M, int64_t K, int64_t N, con
 
 hipError_t launch_skinny_i4(const float* x, int64_t M, int64_t K, int64_t N, int ng, const void* const* packed,
                             const float* const* devscales, const float* const* bias, const I4Geom& g,
-                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s) {
+                            const SkinnyPlan& p, float* y, void* ws, hipStream_t s, const SkinnyExtra* extra) {
     if (p.C == 0 || (p.S > 1 && !ws)) return hipErrorInvalidValue;
-    if (ng == 1) return skinny_dispatch<1>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, s);
-    if (ng == 2) return skinny_dispatch<2>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, s);
+    SkinnyExtra ex;
+    if (extra) ex = *extra;
+    if (ex.ldy == 0) ex.ldy = N;
+    if (ng == 1) return skinny_dispatch<1>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, ex, s);
+    if (ng == 2) return skinny_dispatch<2>(p, x, M, K, N, packed, devscales, bias, g, y, (float*)ws, ex, s);
     return hipErrorInvalidValue;
 }
 

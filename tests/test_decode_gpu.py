@@ -175,6 +175,26 @@ def test_block_decode_nanollama_shape(sgq, dev, oracle, synth):
             assert _row_err(outs[b][t], ref[t]) <= TOL, (b, t)
 
 
+@pytest.mark.parametrize("B", [5, 13, 16])
+def test_block_decode_skinny_batches(sgq, dev, oracle, synth, B):
+    # 5..16 sequences at the NanoLLaMA shape run the norm-fused q/k/v and
+    # gate/up projections on the skinny MFMA kernel (q, k and v side by
+    # side); the first and last sequences are checked against the oracle.
+    dm = _decode_mod(sgq)
+    D, H, G, heads = 2048, 5632, 128, 16
+    codes, scales, biases, g1, g2 = _random_block(oracle, synth, D, H, G, 1050 + B)
+    blk = _block_from_case(sgq, dev, codes, scales, biases, g1, g2, heads, G)
+    lengths = [2 + (b % 2) for b in range(B)]
+    xs = [synth.normal((L, D), 1150 + b, synth.STREAM_X) for b, L in enumerate(lengths)]
+    outs = _run_sequences(sgq, dev, blk, xs, max_tokens=8)
+    for b in (0, B - 1):
+        ref = _oracle_rows(oracle, xs[b], codes, scales, biases, g1, g2, dm.attention_scale(D, heads), G)
+        for t in range(lengths[b]):
+            e = _row_err(outs[b][t], ref[t])
+            print(f"  case B={B} seq={b} t={t} rel_err={e:.3e}", flush=True)
+            assert e <= TOL, (b, t, e)
+
+
 def test_block_decode_long_context_chunks(sgq, dev, oracle, synth):
     # 70 positions with B = 2: the attention runs several key chunks and the
     # combine kernel; every row is checked.
