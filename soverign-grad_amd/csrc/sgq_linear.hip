@@ -743,6 +743,23 @@ __device__ __forceinline__ void split3(const float* v, uint4& h, uint4& m, uint4
     l = make_uint4(pl[0], pl[1], pl[2], pl[3]);
 }
 
+// split3 of four floats (two dwords per plane).
+__device__ __forceinline__ void split3_4(const float* v, uint2& h, uint2& m, uint2& l) {
+#pragma clang fp contract(off)
+    uint32_t ph[2], pm[2], pl[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float a = v[2 * i], b = v[2 * i + 1];
+        ph[i] = pack_hi16(a, b);
+        const float ra = a - trunc_bf16(a), rb = b - trunc_bf16(b);
+        pm[i] = pack_hi16(ra, rb);
+        pl[i] = pack_hi16(ra - trunc_bf16(ra), rb - trunc_bf16(rb));
+    }
+    h = make_uint2(ph[0], ph[1]);
+    m = make_uint2(pm[0], pm[1]);
+    l = make_uint2(pl[0], pl[1]);
+}
+
 // One output of the forward as the reference forms it: sum over k in
 // [k0, k1) of x[k] * (q[k][n] * s), in k order (the non-finite fallback).
 template <int BITS>
@@ -1113,7 +1130,13 @@ struct SkinnyArgs {
 // 1532-1556: x * inv_rms * gamma, inv_rms = 1 / sqrt(sum(x^2) / K + eps)), as
 // in the GEMV: A = x * (gamma * s), and the epilogue multiplies by inv_rms,
 // one factor per row, from the sum of x^2 over the rows the workgroup reads.
-template <int NW, int U, int C, int NG, bool XA, bool NORM>
+//
+// HALF (M <= 8): A rows 8..15 are not outputs, so their lanes do half of the
+// real rows' work.  Lane n < 8 loads and splits k 8g .. 8g + 3 of row n, lane
+// n + 8 k 8g + 4 .. 8g + 7 of the same row, and a row_ror:8 exchange gives
+// lane n the upper half of its operand.  The bf16 planes are the same bits as
+// without HALF; A rows 8..15 then hold copies whose outputs are never read.
+template <int NW, int U, int C, int NG, bool XA, bool NORM, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
@@ -1144,8 +1167,10 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     int wv[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + 32 * g + 4 * e;
-    const bool row_live = n < a.M;
-    const int xrow = n * K * 4;
+    constexpr int XV = HALF ? 4 : 8;  // x values per lane and k block
+    const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
+    const bool row_live = xr < a.M;
+    const int xrow = xr * K * 4;
     const NibbleT tp = nibble_t(e);
     floatx4 acc[NG][C];
 #pragma unroll
@@ -1158,7 +1183,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     // and are multiplied by zero), so partial batches need no branch.
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][NG][C];
-        float xv[U][8], sv[U][NG][8], gv[NORM ? U : 1][8];
+        float xv[U][XV], sv[U][NG][XV], gv[NORM ? U : 1][XV];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kb = kb0 + u * NW;
@@ -1167,9 +1192,9 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
 #pragma unroll
                 for (int c = 0; c < C; ++c)
                     w[u][q][c] = __builtin_amdgcn_raw_buffer_load_b32(rW[q], wv[c], kb * 128, 0);
-            const int k0 = kb * 32 + 8 * g;
+            const int k0 = kb * 32 + 8 * g + xk;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < XV / 4; ++h) {
                 const int kk = k0 + 4 * h;
                 if constexpr (XA) {
                     const float4 xq = buf_load4f<true>(rX, row_live && kk < K ? xrow + kk * 4 : kOobOff, 0);
@@ -1198,15 +1223,23 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
         for (int u = 0; u < U; ++u) {
             if constexpr (NORM) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) sq = fmaf(xv[u][i], xv[u][i], sq);
+                for (int i = 0; i < XV; ++i) sq = fmaf(xv[u][i], xv[u][i], sq);
             }
 #pragma unroll
             for (int q = 0; q < NG; ++q) {
-                float xs[8];
+                float xs[XV];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xs[i] = NORM ? xv[u][i] * (gv[u][i] * sv[u][q][i]) : xv[u][i] * sv[u][q][i];
+                for (int i = 0; i < XV; ++i) xs[i] = NORM ? xv[u][i] * (gv[u][i] * sv[u][q][i]) : xv[u][i] * sv[u][q][i];
                 uint4 ah, am, al;
-                split3(xs, ah, am, al);
+                if constexpr (HALF) {
+                    uint2 h2, m2, l2;
+                    split3_4(xs, h2, m2, l2);
+                    ah = make_uint4(h2.x, h2.y, dpp_xor8(h2.x), dpp_xor8(h2.y));
+                    am = make_uint4(m2.x, m2.y, dpp_xor8(m2.x), dpp_xor8(m2.y));
+                    al = make_uint4(l2.x, l2.y, dpp_xor8(l2.x), dpp_xor8(l2.y));
+                } else {
+                    split3(xs, ah, am, al);
+                }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     const bf16x8 b = nibbles_bf16x16(nibble_transpose8(w[u][q][c], tp));
@@ -1225,6 +1258,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     if constexpr (NORM) {
         sq += xor_lane<32>(sq, lane);
         sq += xor_lane<16>(sq, lane);
+        if constexpr (HALF) sq += xor_lane<8>(sq, lane);  // the two halves of a row's k
         if (lane < 16) sqr[wave][lane] = sq;
         __syncthreads();
         if (threadIdx.x < 16) {
@@ -1923,15 +1957,22 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
         if constexpr (MB == 1) {
             constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
             a.nblk *= ex.nw;
+#define SGQ_SKINNY3(NORM_)                                                                                 \
+    if (M <= 8)                                                                                            \
+        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, true><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a); \
+    else                                                                                                   \
+        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
             if (ex.gamma) {
                 // The norm-fused form keeps two column blocks (register budget).
-                if constexpr (C == 2)
-                    k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, true><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
-                else
+                if constexpr (C == 2) {
+                    SGQ_SKINNY3(true)
+                } else {
                     return hipErrorInvalidValue;
+                }
             } else {
-                k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+                SGQ_SKINNY3(false)
             }
+#undef SGQ_SKINNY3
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
