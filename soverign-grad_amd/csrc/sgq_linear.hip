@@ -1336,14 +1336,19 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
 // eight x quads is the matching A operand.  The scales of the workgroup's K
 // range sit in LDS (read once, coalesced); the next super-block's codes and x
 // are loaded while the current one is computed.
-template <int NW, int C, int NG, bool XA, int MB>
+template <int NW, int C, int NG, bool XA, int MB, bool HALF>
 struct SkinnyRegs {
-    uint4 w[NG][C];      // 4 rows x 8 columns of each strip
-    float4 xq[MB][8];    // 32 consecutive k of each batch row
+    uint4 w[NG][C];                // 4 rows x 8 columns of each strip
+    float4 xq[MB][HALF ? 4 : 8];  // x quads of each batch row (HALF: half of them)
 };
 
-template <int NW, int C, int NG, bool XA, int MB, bool SPLIT>
+// HALF (one row block, M <= 8): as in k_skinny3, lane n < 8 takes x quads
+// t = 0..3 of row n and lane n + 8 quads t = 4..7 of the same row; a
+// row_ror:8 exchange completes each A operand (the same bf16 planes).
+template <int NW, int C, int NG, bool XA, int MB, bool SPLIT, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
+    static_assert(!HALF || MB == 1, "the half-row form has one row block");
+    constexpr int XT = HALF ? 4 : 8;  // x quads per lane, row block and super-block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
@@ -1386,28 +1391,29 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     int wv[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (16 * e + 4 * g) * 4;
+    const int xr = HALF ? (n & 7) : n, toff = HALF ? 4 * (n >> 3) : 0;
     bool row_live[MB];
     int xrow[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-        row_live[b] = n + 16 * b < a.M;
-        xrow[b] = row_live[b] ? (n + 16 * b) * K * 4 : 0;
+        row_live[b] = xr + 16 * b < a.M;
+        xrow[b] = row_live[b] ? (xr + 16 * b) * K * 4 : 0;
     }
     const NibbleT tp = nibble_t(e);
 
     // Loads of super-block sb; one past the range reads x as zeros (and codes
     // that are then multiplied by zero).
-    auto load = [&](SkinnyRegs<NW, C, NG, XA, MB>& r, int sb) {
+    auto load = [&](SkinnyRegs<NW, C, NG, XA, MB, HALF>& r, int sb) {
         const bool in = sb < sb_hi;
 #pragma unroll
         for (int q = 0; q < NG; ++q)
 #pragma unroll
             for (int c = 0; c < C; ++c) r.w[q][c] = buf_load16(rW[q], wv[c], sb * (kSkinnySB * 4));
-        const int k0 = sb * kSkinnySB + 4 * g;
+        const int k0 = sb * kSkinnySB + 4 * g + 16 * toff;
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
+            for (int t = 0; t < XT; ++t) {
                 const int kk = k0 + 16 * t;
                 if constexpr (XA) {
                     r.xq[b][t] = buf_load4f<true>(rX, in && row_live[b] && kk < K ? xrow[b] + kk * 4 : kOobOff, 0);
@@ -1433,24 +1439,32 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
 #pragma unroll
             for (int c = 0; c < C; ++c) acc[q][b][c] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB>& r, int sb) {
+    auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB, HALF>& r, int sb) {
         // A super-block past the range has x = 0; its scale reads stay inside
         // the range's LDS rows.
-        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + g;
+        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + g + 4 * toff;
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
-            float4 s4[8];
+            float4 s4[XT];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) s4[t] = ssc[q][lr + 4 * t];
+            for (int t = 0; t < XT; ++t) s4[t] = ssc[q][lr + 4 * t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 uint4 ah[MB], am[MB], al[MB];
 #pragma unroll
                 for (int b = 0; b < MB; ++b) {
-                    float xs[8];
+                    float xs[XT];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) xs[t] = f4get(r.xq[b][t], i) * f4get(s4[t], i);
-                    split3(xs, ah[b], am[b], al[b]);
+                    for (int t = 0; t < XT; ++t) xs[t] = f4get(r.xq[b][t], i) * f4get(s4[t], i);
+                    if constexpr (HALF) {
+                        uint2 h2, m2, l2;
+                        split3_4(xs, h2, m2, l2);
+                        ah[b] = make_uint4(h2.x, h2.y, dpp_xor8(h2.x), dpp_xor8(h2.y));
+                        am[b] = make_uint4(m2.x, m2.y, dpp_xor8(m2.x), dpp_xor8(m2.y));
+                        al[b] = make_uint4(l2.x, l2.y, dpp_xor8(l2.x), dpp_xor8(l2.y));
+                    } else {
+                        split3(xs, ah[b], am[b], al[b]);
+                    }
                 }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
@@ -1472,7 +1486,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
 
     // Two register sets: the loads of the next super-block are in flight
     // while the current one is computed.
-    SkinnyRegs<NW, C, NG, XA, MB> ra, rb;
+    SkinnyRegs<NW, C, NG, XA, MB, HALF> ra, rb;
     int sb = sb_lo + wave;
     load(ra, sb);
 #pragma unroll
@@ -1977,10 +1991,15 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
         }
         return hipErrorInvalidValue;
     }
-    if (S > 1)
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    const bool half = MB == 1 && M <= 8;
+    if (S > 1 && half)
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    else if (S > 1)
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+    else if (half)
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
     else
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
     if (S > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
