@@ -1600,8 +1600,13 @@ struct Skinny8Args {
     int nblk;
 };
 
-template <int NW, int U, int C, int MB, bool PT, bool XA>
+// HALF (one row block, M <= 8): lane n < 8 loads and splits k 8g .. 8g + 3
+// of row n, lane n + 8 k 8g + 4 .. 8g + 7 of the same row, and a row_ror:8
+// exchange completes each A operand (the same bf16 planes), as in k_skinny3.
+template <int NW, int U, int C, int MB, bool PT, bool XA, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
+    static_assert(!HALF || MB == 1, "the half-row form has one row block");
+    constexpr int XV = HALF ? 4 : 8;  // x values per lane, row block and k block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int K = a.K;
@@ -1616,6 +1621,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
     int wv[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) wv[c] = ((4 * c + (n >> 2)) * a.RQ + 2 * g) * 16 + (n & 3) * 4;
+    const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
     floatx4 acc[MB][C];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
@@ -1624,7 +1630,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
     const int nkb = (a.Kpad + 31) >> 5;
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][C][2];
-        float xv[U][MB][8], sv[U][8];
+        float xv[U][MB][XV], sv[U][XV];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kb = kb0 + u * NW;
@@ -1633,13 +1639,13 @@ __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
                 w[u][c][0] = __builtin_amdgcn_raw_buffer_load_b32(rW, wv[c], kb * 128, 0);
                 w[u][c][1] = __builtin_amdgcn_raw_buffer_load_b32(rW, wv[c] + 16, kb * 128, 0);
             }
-            const int k0 = kb * 32 + 8 * g;
+            const int k0 = kb * 32 + 8 * g + xk;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < XV / 4; ++h) {
                 const int kk = k0 + 4 * h;
 #pragma unroll
                 for (int b = 0; b < MB; ++b) {
-                    const int xo = (16 * b + n) * K * 4;
+                    const int xo = (16 * b + xr) * K * 4;
                     if constexpr (XA) {
                         const float4 xq = buf_load4f<true>(rX, kk < K ? xo + kk * 4 : kOobOff, 0);
                         xv[u][b][4 * h] = xq.x, xv[u][b][4 * h + 1] = xq.y, xv[u][b][4 * h + 2] = xq.z,
@@ -1674,11 +1680,19 @@ __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
             }
 #pragma unroll
             for (int b = 0; b < MB; ++b) {
-                float xs[8];
+                float xs[XV];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) xs[i] = PT ? xv[u][b][i] : xv[u][b][i] * sv[u][i];
+                for (int i = 0; i < XV; ++i) xs[i] = PT ? xv[u][b][i] : xv[u][b][i] * sv[u][i];
                 uint4 ah, am, al;
-                split3(xs, ah, am, al);
+                if constexpr (HALF) {
+                    uint2 h2, m2, l2;
+                    split3_4(xs, h2, m2, l2);
+                    ah = make_uint4(h2.x, h2.y, dpp_xor8(h2.x), dpp_xor8(h2.y));
+                    am = make_uint4(m2.x, m2.y, dpp_xor8(m2.x), dpp_xor8(m2.y));
+                    al = make_uint4(l2.x, l2.y, dpp_xor8(l2.x), dpp_xor8(l2.y));
+                } else {
+                    split3(xs, ah, am, al);
+                }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     acc[b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), bq[c], acc[b][c], 0, 0, 0);
@@ -2061,7 +2075,10 @@ hipError_t skinny8_launch(const float* x, int64_t M, int64_t K, int64_t N, const
     a.y = y;
     a.nblk = (int)(ceil_div(M, 16 * MB) * a.ncg);
     constexpr int U = MB == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
-    k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+    if (MB == 1 && M <= 8)
+        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, MB == 1><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+    else
+        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
