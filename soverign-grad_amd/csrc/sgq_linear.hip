@@ -2207,9 +2207,14 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t c
     GemmPlan p{1, (int)KT};
     if (cus < 1) cus = 1;
     if (cus > kMaxCus) cus = kMaxCus;
-    if (tiles < t.per_cu * cus && KT >= 4) {
-        int64_t ks = ceil_div(t.per_cu * cus, tiles);  // about per_cu workgroups per CU
-        if (ks > KT / 2) ks = KT / 2;                     // at least two stages per split
+    // Splits fill the resident slots, rounded down: a grid just past them
+    // runs its last few workgroups as a second pass (4096->11008 at 128 rows,
+    // 86 tiles of 128 x 128: 6 splits, 516 workgroups on 512 slots, 94 us; 5
+    // splits 61 us).
+    const int64_t slots = t.per_cu * cus;
+    if (tiles < slots && KT >= 4) {
+        int64_t ks = slots / tiles;
+        if (ks > KT / 2) ks = KT / 2;  // at least two stages per split
         if (ks > kMaxSplits) ks = kMaxSplits;
         if (ks > 1) {
             p.sps = (int)ceil_div(KT, ks);
@@ -2220,12 +2225,16 @@ GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t c
 }
 
 // Tile of the three-term GEMM for a code width and batch (the fp32 kernel
-// uses the 128 x 128 tile), with the workgroups a CU holds at once: two of
-// the 128 x 128 tiles, one of the 128 x 256 (its LDS and registers fill the
-// CU); of the small-batch tiles (28 and 40 KB of LDS) four and three.
+// uses the 128 x 128 tile), with the workgroups a split-K grid gives each CU:
+// two of the 128 x 128 tiles, one of the 128 x 256 (its LDS and registers fill
+// the CU), four of the 32-row tile (28 KB of LDS) and two of the 64-row tile.
+// Three of the latter fit (40 KB of LDS) but cost more in partial tiles
+// (KS * M * N * 4 bytes, written and read back) than they gain: 2048->6144 at
+// 64 rows 16 splits 31.6 us, 10 splits 24.3 us; 4096->11008 at 48 rows 9
+// splits 50.4 us, 5 splits 42.1 us.
 GemmTile gemm_tile(int bits, int64_t M) {
     if (M <= 32) return GemmTile{32, kBN, 4};
-    if (M <= 64) return GemmTile{64, kBN, 3};
+    if (M <= 64) return GemmTile{64, kBN, 2};
     return bits == 8 ? GemmTile{kBM, 2 * kBN, 1} : GemmTile{kBM, kBN, 2};
 }
 

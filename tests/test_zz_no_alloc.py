@@ -72,7 +72,9 @@ def test_noalloc_skinny_split_k(sgq, dev, oracle, synth):
 
 def test_noalloc_refuses_oversized_scratch(sgq, dev):
     lib = sgq.load_library()
-    M, K, N = 384, 8192, 8192  # split-K partials of 3 x 384 x 8192 floats: 36 MiB
+    # The skinny kernel over K = 131072 takes 16 K ranges of 8192 rows:
+    # partials of 16 x 32 x 16512 floats, 32.25 MiB.
+    M, K, N = 32, 131072, 16512
     assert lib.sgq_linear_workspace_bytes(4, M, K, N) > 32 << 20
     stream = torch.cuda.current_stream(dev).cuda_stream
     rc = lib.sgq_linear_int4_noalloc(16, M, K, N, 256, 256, 256, 128, None, 256, stream)
