@@ -100,7 +100,14 @@ __device__ __forceinline__ int seq_keys(const int32_t* pos, int b, int64_t max_t
 // workgroup), so every phase issues all of its loads before using any: the
 // scores split D over the four wavefronts (each lane holds its slice of q and
 // loads its slice of all CS keys at once), and the value sum loads KB keys'
-// rows per batch.
+// rows per batch.  Cached keys and values are read once per step: their loads
+// take the non-temporal cache policy (ld_stream4), so they do not displace
+// the step's weights and activations.
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream4(const float* row, int64_t i) {
+    const f32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(row) + i);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 template <int CS>
 __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict__ q, const float* __restrict__ knew,
                                                          const float* __restrict__ vnew, int64_t ldq, int64_t D,
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
         for (int u = 0; u < KB; ++u) {
             const int j = j0 + u;
             const float* vr = (u >= n || j == p) ? vn : vcb + (int64_t)j * D;
-            vpre[ci][u] = i < D4 ? ((const float4*)vr)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            vpre[ci][u] = i < D4 ? ld_stream4(vr, i) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
     const int64_t s0 = wave * ((D4 + NWV - 1) / NWV), s1 = min(D4, s0 + (D4 + NWV - 1) / NWV);
@@ -156,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
             for (int u = 0; u < KB; ++u) {
                 const int t = t0 + u, j = j0 + t;
                 const float* kr = (t >= n || j == p) ? kn : kcb + (int64_t)j * D;
-                kv[u] = ((const float4*)kr)[i];
+                kv[u] = ld_stream4(kr, i);
             }
 #pragma unroll
             for (int u = 0; u < KB; ++u) {
@@ -222,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_partial(const float* __restrict
             for (int u = 0; u < KB; ++u) {
                 const int t = t0 + u, j = j0 + t;
                 const float* vr = (t >= n || j == p) ? vn : vcb + (int64_t)j * D;
-                vv[u] = ((const float4*)vr)[i];
+                vv[u] = ld_stream4(vr, i);
             }
             fma_batch(o, vv, t0);
         }
