@@ -293,6 +293,26 @@ def test_plan_follows_the_device_cu_count(lib):
     assert lib.sgq_linear_plan(8, 1, 4, 4, 0, -1, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == 1
 
 
+def test_plan_splits_fill_one_pass(lib):
+    """A split-K grid never runs past the device's resident slots (one 128x256
+    INT8 tile, two 128x128 INT4 or 64-row tiles, four 32-row tiles per CU):
+    the split count is rounded down, so no few workgroups run as a second
+    pass.  Each case below is one the previous, rounded-up plan overfilled."""
+    cases = [  # bits, M, K, N, G, tiles, workgroups per CU
+        (4, 128, 4096, 11008, 128, 86, 2),  # was 6 splits: 516 workgroups on 512 slots
+        (4, 256, 4096, 11008, 128, 172, 2),  # was 3: 516
+        (8, 128, 4096, 11008, 0, 43, 1),  # was 6: 258 on 256
+        (4, 48, 4096, 11008, 128, 86, 2),  # 64-row tile, was planned at three per CU
+        (8, 32, 4096, 11008, 0, 86, 4),  # 32-row tile: four per CU
+    ]
+    for bits, M, K, N, G, tiles, per_cu in cases:
+        for cus in (256, 200, 64):
+            path, ks = _plan(lib, bits, M, K, N, G, cus)
+            assert path == 1, (bits, M, K, N, path)
+            assert ks == max(1, min(16, per_cu * cus // tiles)), (bits, M, K, N, cus, ks)
+            assert ks * tiles <= per_cu * cus or ks == 1, (bits, M, K, N, cus, ks)
+
+
 def test_plan_skinny_int8(lib):
     """INT8 batches of 5..128 rows take the skinny bf16 MFMA kernel (path 4,
     no K split) once (M rounded up to 8) * K * N reaches 2^26; above 16 rows
