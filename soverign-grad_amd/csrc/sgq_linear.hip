@@ -1009,6 +1009,11 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
     if (kt0 + 1 < kt1) load(r1, kt0 + 1);
     store(r0, kt0 & 1);
     lds_barrier();
+    // lgkmcnt(0) before the loop: a kernel-argument scalar load still pending
+    // at the loop header made the compiler wait for all sixteen operand reads
+    // (lgkmcnt(0)) before the first MFMA of every other stage, instead of for
+    // the few that MFMA reads.  C4 162.1 -> 159.7 us (builds interleaved).
+    __builtin_amdgcn_s_waitcnt(0xC07F);
     for (int kt = kt0; kt < kt1; kt += 2) {
         stage(kt, r1, r0);
         if (kt + 1 < kt1) stage(kt + 1, r0, r1);
