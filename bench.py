@@ -231,6 +231,92 @@ class Case:
         return float(np.max(np.abs(yg.astype(np.float64) - yref)) / max(np.max(np.abs(yref)), 1e-30))
 
 
+# Weights of the M=1 size sweep (INT4 g128, K x N): C2's 9 MB up to 285 MB.
+GEMV_SWEEP = [(4096, 4096), (4096, 8192), (4096, 11008), (4096, 16384), (8192, 16384), (8192, 28672),
+              (4096, 65536), (8192, 65536)]
+
+
+def gemv_size_sweep(pkg, dev, steps: int) -> dict:
+    """The M=1 INT4 g128 forward over weights from 9 MB to 285 MB.
+
+    Per shape: copies of the weight totalling more than 300 MB, a graph of
+    `steps` calls over them, five replays each after an untimed sweep of all
+    copies (as in Case.time_graph); the median per-call time.  Weights are
+    W ~ N(0, 0.02) from torch's device generator (the counter RNG of the
+    other legs is too slow at 537 M values), quantized on the device.  Each
+    shape's output is checked against x @ dequantize(W) in fp64, where
+    dequantize is the library's own bit-exact GPU dequantize.  The fit
+    t = t0 + bytes / bw over all shapes separates the per-call fixed cost
+    from the streaming rate."""
+    import torch
+
+    lib = pkg.load_library()
+    gen = torch.Generator(device=dev)
+    rows = []
+    for K, N in GEMV_SWEEP:
+        G = 128
+        nbytes = K * N // 2 + K * N // G * 4 + 4 * K + 4 * N
+        copies = max(2, -(-300_000_000 // nbytes))
+        gen.manual_seed(K * 131 + N)
+        W = torch.randn((K, N), generator=gen, device=dev) * 0.02
+        qw = pkg.quantize_int4(W, G, keep_qdata=False)
+        del W
+        x = torch.randn((1, K), generator=gen, device=dev)
+        y = torch.empty((1, N), device=dev)
+        packed = [qw.packed] + [qw.packed.clone() for _ in range(copies - 1)]
+        dsc = [qw.devscales] + [qw.devscales.clone() for _ in range(copies - 1)]
+        nws = lib.sgq_linear_workspace_bytes(4, 1, K, N)
+        ws = torch.zeros(max(nws, 256), dtype=torch.uint8, device=dev)
+
+        def launch(i):
+            j = i % copies
+            rc = lib.sgq_linear_int4(x.data_ptr(), 1, K, N, packed[j].data_ptr(), qw.scales.data_ptr(),
+                                     dsc[j].data_ptr(), G, None, y.data_ptr(), ws.data_ptr(), ws.numel(),
+                                     torch.cuda.current_stream(dev).cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"sgq launch failed: {lib.sgq_last_error().decode()}")
+
+        for i in range(3):
+            launch(i)
+        torch.cuda.synchronize()
+        yref = (x.double() @ pkg.dequantize_int4(qw).double()).float()
+        err = float((y - yref).abs().max() / yref.abs().max())
+        if err > 1e-5:
+            raise SystemExit(f"parity failure in bench (gemv sweep {K}x{N}): rel err {err}")
+        cap = torch.cuda.Stream(dev)
+        g, sweep = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(steps):
+                launch(i)
+        with torch.cuda.graph(sweep, stream=cap):
+            for i in range(copies):
+                launch(i)
+        g.replay()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(5):
+            sweep.replay()
+            s.record()
+            g.replay()
+            e.record()
+            torch.cuda.synchronize()
+            times.append(s.elapsed_time(e) * 1e3 / steps)
+        us = statistics.median(times)
+        rows.append({"K": K, "N": N, "bytes": nbytes, "copies": copies, "us_per_call": round(us, 3),
+                     "GB_s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "rel_err_vs_fp64": err})
+        log(f"[bench] gemv sweep {K}x{N}: {us:.3f} us/call, {nbytes / us / 1e3:.1f} GB/s")
+        del g, sweep, packed, dsc, qw, ws
+        torch.cuda.empty_cache()
+    b = np.array([r["bytes"] for r in rows], dtype=np.float64)
+    t = np.array([r["us_per_call"] for r in rows], dtype=np.float64)
+    slope, t0 = np.polyfit(b, t, 1)
+    return {"workload": "INT4 g128 QuantizedLinear forward, M=1, over weights of 9 MB to 285 MB",
+            "launch": f"one hipGraph of {steps} calls per shape, median of 5 replays", "shapes": rows,
+            "fit_t0_us": round(float(t0), 3), "fit_GB_s": round(float(1e-3 / slope), 1)}
+
+
 def calibration_copy(dev, mib: int = 64) -> None:
     """One device-to-device copy of a known size (64 MiB read + 64 MiB written),
     run before the timed region so that a `rocprofv3 --pmc FETCH_SIZE` /
@@ -707,6 +793,8 @@ def main() -> int:
                     help="only time the 22-layer block decode step at CTX cached positions (for profiling)")
     ap.add_argument("--c5-only", action="store_true",
                     help="only time the 110-call C5 decode step (for profiling)")
+    ap.add_argument("--gemv-size-sweep", action="store_true",
+                    help="only time the M=1 INT4 forward over weights of 9 MB to 285 MB")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -727,6 +815,9 @@ def main() -> int:
         if r["rel_err_vs_oracle"] > 1e-5:
             raise SystemExit("parity failure in bench (c5)")
         print(json.dumps(r), flush=True)
+        return 0
+    if args.gemv_size_sweep:
+        print(json.dumps(gemv_size_sweep(pkg, dev, 200)), flush=True)
         return 0
     if args.block_decode:
         r = block_decode_step(pkg, dev, Oracle(), max(2, min(10, args.steps)), args.block_decode)
