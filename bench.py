@@ -938,6 +938,8 @@ def main() -> int:
             torch.cuda.empty_cache()
         others["c3_crossover"] = c3_crossover(pkg, dev, oracle, OTHER_STEPS)
         torch.cuda.empty_cache()
+        others["c2_size_sweep"] = gemv_size_sweep(pkg, dev, 200)
+        torch.cuda.empty_cache()
         for M in (1, 8):
             key = f"c3_swiglu_m{M}"
             others[key] = swiglu_pair(pkg, dev, oracle, OTHER_STEPS, M)
