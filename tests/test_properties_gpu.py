@@ -14,6 +14,9 @@ forms, the three-term GEMM with and without split K, the fp32 MFMA GEMM):
   order does not depend on other columns), and the rewritten columns must
   follow the new codes: negated codes give the negated output within the
   forward's tolerance.  A strip or scale-column indexing mistake breaks it.
+- row permutation: each output row is formed from its own x row by the same
+  operations wherever it sits in a tile or row group, so permuting the rows
+  of x permutes the rows of y bit for bit.  A row-stride mistake breaks it.
 
 Reference semantics: quantized_matmul_int8/int4 (src/quantization.cpp:189-206)
 is linear in x and computes each output column from that column's codes and
@@ -108,3 +111,19 @@ def test_column_independence(sgq, dev, name, bits, M, K, N, g):
     assert torch.equal(y2[:, keep], y[:, keep]), name
     changed, ref = y2[:, n0:n0 + width], -y[:, n0:n0 + width]
     assert ((changed - ref).abs().max() / ref.abs().max()).item() <= TOL, name
+
+
+@pytest.mark.parametrize("name,bits,M,K,N,g", [c for c in CASES if c[2] > 1], ids=[c[0] for c in CASES if c[2] > 1])
+def test_row_permutation(sgq, dev, name, bits, M, K, N, g):
+    # Each output row is formed from its own x row by the same operations
+    # wherever the row sits in a tile, row block or row group, so permuting
+    # the rows of x permutes the rows of y bit for bit.
+    qw, xs = _weights(sgq, dev, bits, K, N, g, 3000 + M)
+    x = _x(dev, M, K, xs)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(M)
+    perm = torch.randperm(M, generator=gen, device=dev)
+    y = sgq.quantized_matmul(x, qw).clone()
+    yp = sgq.quantized_matmul(x[perm].contiguous(), qw)
+    torch.cuda.synchronize()
+    assert torch.equal(yp, y[perm]), (name, (yp - y[perm]).abs().max().item())
