@@ -127,3 +127,44 @@ def test_row_permutation(sgq, dev, name, bits, M, K, N, g):
     yp = sgq.quantized_matmul(x[perm].contiguous(), qw)
     torch.cuda.synchronize()
     assert torch.equal(yp, y[perm]), (name, (yp - y[perm]).abs().max().item())
+
+
+# The gated MLP (silu(x . Wg) * (x . Wu)) in one library call: (name, bits, M, K, N, group or scheme).
+SWIGLU_CASES = [
+    ("c3_m1_gemv", 4, 1, 4096, 11008, 128),
+    ("c3_m8_skinny", 4, 8, 4096, 11008, 128),
+    ("c3_m32_skinny", 4, 32, 4096, 11008, 128),
+    ("c5_m8_skinny", 4, 8, 2048, 5632, 128),
+    ("int4_m256_gemm", 4, 256, 2048, 5632, 128),
+    ("int8_m8_skinny8", 8, 8, 4096, 4096, 0),
+    ("int8_m256_gemm", 8, 256, 2048, 5632, 1),
+]
+
+
+@pytest.mark.parametrize("name,bits,M,K,N,g", SWIGLU_CASES, ids=[c[0] for c in SWIGLU_CASES])
+def test_swiglu_rows_and_columns(sgq, dev, name, bits, M, K, N, g):
+    # Row permutation and column independence of the gated MLP: silu and the
+    # product act elementwise on two forwards that each have both properties.
+    qg, xs = _weights(sgq, dev, bits, K, N, g, 4000 + M)
+    qu, _ = _weights(sgq, dev, bits, K, N, g, 5000 + M)
+    x = _x(dev, M, K, xs)
+    h = sgq.quantized_swiglu(x, qg, qu).clone()
+    if M > 1:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(M)
+        perm = torch.randperm(M, generator=gen, device=dev)
+        hp = sgq.quantized_swiglu(x[perm].contiguous(), qg, qu)
+        torch.cuda.synchronize()
+        assert torch.equal(hp, h[perm]), name
+    width = g if bits == 4 else 64
+    n0 = (N // 2) // width * width
+    q2 = qu.qdata.clone()
+    q2[:, n0:n0 + width] = -q2[:, n0:n0 + width]
+    qu2 = sgq.pack_int4(q2, qu.scales, g) if bits == 4 else sgq.pack_int8(q2, qu.scales, g)
+    h2 = sgq.quantized_swiglu(x, qg, qu2)
+    torch.cuda.synchronize()
+    keep = torch.ones(N, dtype=torch.bool, device=dev)
+    keep[n0:n0 + width] = False
+    assert torch.equal(h2[:, keep], h[:, keep]), name
+    changed, ref = h2[:, n0:n0 + width], -h[:, n0:n0 + width]
+    assert ((changed - ref).abs().max() / ref.abs().max()).item() <= TOL, name
