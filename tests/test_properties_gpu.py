@@ -168,3 +168,38 @@ def test_swiglu_rows_and_columns(sgq, dev, name, bits, M, K, N, g):
     assert torch.equal(h2[:, keep], h[:, keep]), name
     changed, ref = h2[:, n0:n0 + width], -h[:, n0:n0 + width]
     assert ((changed - ref).abs().max() / ref.abs().max()).item() <= TOL, name
+
+
+@pytest.mark.parametrize("B", [4, 8, 16])
+def test_block_decode_sequence_permutation(sgq, dev, B):
+    # One LLaMA block decode step at the NanoLLaMA shape with ragged cached
+    # lengths: permuting the sequences (their tokens, caches and positions)
+    # permutes the outputs and the appended cache rows bit for bit, since each
+    # sequence's projections, attention chunks and combine do not depend on its
+    # index in the batch.
+    import soverign_grad_amd.decode as dm
+
+    D, H, heads, G, T, L = 2048, 5632, 16, 128, 160, 129
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77 + B)
+    shapes = dm.projection_shapes(D, H)
+    W = {k: torch.randn(shapes[k], generator=gen, device=dev) * 0.02 for k in dm.PROJECTIONS}
+    b = {k: torch.randn((shapes[k][1],), generator=gen, device=dev) * 0.02 for k in dm.PROJECTIONS}
+    g1 = 1.0 + 0.1 * torch.randn((D,), generator=gen, device=dev)
+    g2 = 1.0 + 0.1 * torch.randn((D,), generator=gen, device=dev)
+    blk = dm.QuantizedLLaMABlock.from_float(W, b, g1, g2, heads, G)
+    x = torch.randn((B, D), generator=gen, device=dev)
+    kc = torch.randn((B, T, D), generator=gen, device=dev)
+    vc = torch.randn((B, T, D), generator=gen, device=dev)
+    pos = torch.randint(0, L - 1, (B,), generator=gen, device=dev, dtype=torch.int32)
+    pos[0] = 0
+    pos[-1] = L - 2
+    perm = torch.randperm(B, generator=gen, device=dev)
+    k1, v1 = kc.clone(), vc.clone()
+    y = blk.decode(x, k1, v1, pos, L).clone()
+    k2, v2 = kc[perm].contiguous(), vc[perm].contiguous()
+    yp = blk.decode(x[perm].contiguous(), k2, v2, pos[perm].contiguous(), L)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all()
+    assert torch.equal(yp, y[perm])
+    assert torch.equal(k2, k1[perm]) and torch.equal(v2, v1[perm])
