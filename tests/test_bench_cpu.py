@@ -1,0 +1,59 @@
+"""bench.py's contract pieces that need no GPU: the one-GPU refusal and the
+algorithmic bytes and flops its roofline fractions divide by.
+
+The byte counts follow the per-call formula K*N*bits/8 + 4*(#scales) + 4*M*K
++ 4*M*N (+ 4*N bias), #scales = 1 (per tensor), K (per row) or K*N/G (INT4
+groups along the flattened [K, N], src/quantization.cpp:113-159), worked out
+by hand below for each BASELINE config.
+"""
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+
+def _run_bench(args, env_extra=None):
+    env = dict(os.environ)
+    env.update(env_extra or {})
+    return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True, text=True,
+                          env=env, timeout=120)
+
+
+@pytest.mark.parametrize("args,env", [(["--gpus", "2"], None), (["--gpus", "8"], None),
+                                      ([], {"WORLD_SIZE": "2"})])
+def test_more_than_one_gpu_is_refused(args, env):
+    r = _run_bench(args, env)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout == ""  # no bench line
+
+
+def test_algorithmic_bytes_and_flops():
+    import bench
+
+    c = bench.CONFIGS
+    # C1: 1024x1024 INT8 codes, one per-tensor scale, x 128x1024, y 128x1024, bias 1024.
+    assert bench.alg_bytes(c["c1"]) == 1024 * 1024 + 4 + 4 * 128 * 1024 + 4 * 128 * 1024 + 4 * 1024 == 2_101_252
+    # C2: 4096x4096 nibbles, 131072 group scales, x and y of 4096.
+    assert bench.alg_bytes(c["c2"]) == 8_388_608 + 524_288 + 16_384 + 16_384 == 8_945_664
+    # C3 gate at M=1: 4096x11008 nibbles, 352256 group scales, x 4096, y 11008.
+    assert bench.alg_bytes(c["c3_gate_m1"]) == 22_544_384 + 1_409_024 + 4 * 4096 + 4 * 11008 == 24_013_824
+    # C4: 4096x4096 INT8 codes, one scale, x and y of 2048x4096.
+    assert bench.alg_bytes(c["c4"]) == 16_777_216 + 4 + 2 * 4 * 2048 * 4096 == 83_886_084
+    assert bench.alg_flops(c["c4"]) == 2 * 2048 * 4096 * 4096 == 68_719_476_736
+    assert bench.alg_flops(c["c2"]) == 2 * 4096 * 4096
+
+
+def test_size_sweep_starts_at_c2():
+    import bench
+
+    K, N = bench.GEMV_SWEEP[0]
+    assert (K, N) == (bench.CONFIGS["c2"]["K"], bench.CONFIGS["c2"]["N"])
+    codes = [K * N // 2 for K, N in bench.GEMV_SWEEP]
+    assert codes == sorted(codes)
+    assert codes[-1] > 256_000_000  # the largest weight alone exceeds the 256 MB Infinity Cache
