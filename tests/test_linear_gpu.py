@@ -492,3 +492,19 @@ def test_dequantize_matches_reference_product(sgq, dev, oracle, synth):
     qx4 = sgq.quantize_int4(_to_dev(W, dev), 24)
     q4, s4 = oracle.quantize_int4(W, 24)
     assert helpers.same_value_allow_zero_sign(_np(sgq.dequantize_int4(qx4)), oracle.dequantize_int4(q4, s4, 24))
+
+
+def test_plan_uses_the_device_cu_count(sgq, dev):
+    # compute_units = 0 plans for the current device: the same plan as its CU
+    # count given explicitly, on the first query and on the cached ones after.
+    lib = sgq.load_library()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    shapes = [(4, 1, 4096, 4096, 128), (4, 16, 11008, 4096, 128), (4, 256, 4096, 4096, 128), (8, 512, 4096, 1024, 0),
+              (8, 128, 1024, 1024, 0), (4, 8, 2048, 6144, 128)]
+    for bits_, M, K, N, G in shapes:
+        want_p, want_k = ctypes.c_int(), ctypes.c_int()
+        assert lib.sgq_linear_plan(bits_, M, K, N, G, cus, ctypes.byref(want_p), ctypes.byref(want_k)) == 0
+        for _ in range(3):
+            p, k = ctypes.c_int(), ctypes.c_int()
+            assert lib.sgq_linear_plan(bits_, M, K, N, G, 0, ctypes.byref(p), ctypes.byref(k)) == 0
+            assert (p.value, k.value) == (want_p.value, want_k.value), (bits_, M, K, N, G, cus)
