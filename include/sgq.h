@@ -120,6 +120,19 @@ int64_t sgq_linear_workspace_bytes(int bits, int64_t M, int64_t K, int64_t N);
 int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int* path,
                     int* k_splits);
 
+/* How the MFMA GEMM of this shape places its workgroups on a device of
+ * `compute_units` CUs (0: the current device's) and `xcds` XCDs (0: the
+ * current device's, hipDeviceAttributeNumberOfXccs; a full MI355X has 8, its
+ * compute partitions 4, 2 or 1).  *rect_rows: tile rows of the output
+ * rectangle each XCD takes when the grid splits into one rectangle per XCD
+ * without a K split (0: the plain order); *xcd_log2: log2 of the XCD count
+ * the kernels permute workgroup ids by (0, the identity, for a count that is
+ * not a power of two).  Host-only; this library's own extension (the
+ * reference has no launch planning).  Placement changes speed only, never a
+ * result. */
+int sgq_gemm_xcd_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int xcds,
+                      int* rect_rows, int* xcd_log2);
+
 /* Zero-fills a workspace with a kernel (no hipMemset), on `stream`. */
 int sgq_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
 

@@ -52,6 +52,8 @@ SIGNATURES = {
     "sgq_quantize_workspace_bytes": (_i64, [_int, _i64, _i64, _i64]),
     "sgq_linear_workspace_bytes": (_i64, [_int, _i64, _i64, _i64]),
     "sgq_linear_plan": (_int, [_int, _i64, _i64, _i64, _i64, _int, ctypes.POINTER(_int), ctypes.POINTER(_int)]),
+    "sgq_gemm_xcd_plan": (_int, [_int, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_int),
+                                 ctypes.POINTER(_int)]),
     "sgq_workspace_init": (_int, [_vp, _i64, _vp]),
     "sgq_quantize_int8": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _i64, _vp]),
     "sgq_quantize_int4": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),

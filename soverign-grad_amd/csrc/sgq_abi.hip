@@ -93,7 +93,10 @@ int check_linear_ws(const char* fn, int bits, int64_t M, int64_t K, int64_t N, c
 int64_t swiglu_ws_bytes(int bits, bool flat, int64_t M, int64_t K, int64_t N, int64_t group_size) {
     int64_t skinny = 0;
     if (bits == 4 && !flat && K > 0)
-        skinny = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, group_size), kMaxCus), M, N, 2);
+        for (int64_t cus : {(int64_t)1, kMaxCus}) {  // every device (see skinny_ws_bound)
+            const int64_t w = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, group_size), cus), M, N, 2);
+            if (w > skinny) skinny = w;
+        }
     int64_t other = 0;
     // The one-launch GEMV form takes the batches the plain forward runs on the
     // GEMV; INT8 batches of the skinny kernel run it once per weight, up into
@@ -108,6 +111,17 @@ int64_t swiglu_ws_bytes(int bits, bool flat, int64_t M, int64_t K, int64_t N, in
 }
 
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
+
+// The launch about to run takes `need` bytes of workspace (its plan on this
+// device): refuse it when the caller passed less.  The size queries bound
+// every device's need, so this only fails for a workspace sized by hand.
+int check_launch_ws(const char* fn, int64_t need, const void* workspace, int64_t workspace_bytes) {
+    if (need <= 0) return SGQ_OK;
+    if (!workspace || workspace_bytes < need)
+        return fail(SGQ_ERR_WORKSPACE, "%s: this device's launch needs %lld bytes of workspace", fn, (long long)need);
+    if (!aligned16(workspace)) return fail(SGQ_ERR_WORKSPACE, "%s: workspace must be 16-byte aligned", fn);
+    return SGQ_OK;
+}
 
 // LLaMA block decode workspace, each region 256-byte aligned:
 //   n [B*D] | qkv [3*B*D] | ctx [B*D] | h [B*D] | hid [B*H] | tmp [B*max(D,H)]
@@ -259,12 +273,18 @@ int linear_int4(const char* fn, const float* x, int64_t M, int64_t K, int64_t N,
         return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
     const int st = check_linear_ws(fn, 4, M, K, N, workspace, workspace_bytes);
     if (st != SGQ_OK) return st;
-    const SkinnyPlan sp = skinny_plan(M, K, g, device_cus(s));
+    const int cus = device_cus(s);
+    const SkinnyPlan sp = skinny_plan(M, K, g, cus);
     if (sp.C > 0) {
+        const int lw = check_launch_ws(fn, skinny_ws_bytes(sp, M, N, 1), workspace, workspace_bytes);
+        if (lw != SGQ_OK) return lw;
         SGQ_HIP(launch_skinny_i4(x, M, K, N, 1, &packed, &devscales, &bias, g, sp, y, workspace, s), "skinny_i4");
     } else if (linear_uses_gemv(M, K, N)) {
         SGQ_HIP(launch_gemv_i4(x, M, K, N, packed, devscales, g, bias, y, s), "gemv_i4");
     } else {
+        const int lw = check_launch_ws(fn, gemm_launch_ws_bytes(4, M, K, N, (int)g.spc, cus), workspace,
+                                       workspace_bytes);
+        if (lw != SGQ_OK) return lw;
         SGQ_HIP(launch_gemm_i4(x, M, K, N, packed, devscales, g, bias, y, workspace, s), "gemm_i4");
     }
     return ok();
@@ -324,6 +344,20 @@ int sgq_linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_siz
         return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_linear_plan: bad argument");
     const int64_t cus = compute_units > 0 ? compute_units : device_cus(nullptr);
     linear_plan(bits, M, K, N, group_size, cus, path, k_splits);
+    return ok();
+}
+
+int sgq_gemm_xcd_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int compute_units, int xcds,
+                      int* rect_rows, int* xcd_log2_out) {
+    if (bad_dims(M, K) || bad_dims(K, N) || (bits != 8 && bits != 4) || compute_units < 0 || xcds < 0 ||
+        !rect_rows || !xcd_log2_out)
+        return fail(SGQ_ERR_INVALID_ARGUMENT, "sgq_gemm_xcd_plan: bad argument");
+    const int64_t cus = compute_units > 0 ? compute_units : device_cus(nullptr);
+    int64_t x = xcds > 0 ? xcds : device_xcds(nullptr);
+    if (x > kMaxXcds) x = kMaxXcds;
+    const int mode = bits == 4 ? (int)I4Geom(K, N, group_size).spc : 0;
+    *rect_rows = gemm_rect_rows(bits, M, K, N, mode, cus < kMaxCus ? cus : kMaxCus, x);
+    *xcd_log2_out = xcd_log2((int)x);
     return ok();
 }
 
@@ -543,6 +577,9 @@ int sgq_linear_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
     } else {
         const int st = check_linear_ws("sgq_linear_int8", 8, M, K, N, workspace, workspace_bytes);
         if (st != SGQ_OK) return st;
+        const int lw = check_launch_ws("sgq_linear_int8", gemm_launch_ws_bytes(8, M, K, N, 0, device_cus(s)),
+                                       workspace, workspace_bytes);
+        if (lw != SGQ_OK) return lw;
         SGQ_HIP(launch_gemm_i8(x, M, K, N, packed, scales, per_tensor, bias, y, workspace, s), "gemm_i8");
     }
     return ok();
@@ -616,6 +653,9 @@ int sgq_swiglu_int8(const float* x, int64_t M, int64_t K, int64_t N, const void*
                 "swiglu_gemv_i8");
         return ok();
     }
+    const int lw = check_launch_ws(fn, align_up(M * N * 4) + gemm_launch_ws_bytes(8, M, K, N, 0, device_cus(s)),
+                                   workspace, workspace_bytes);
+    if (lw != SGQ_OK) return lw;
     void* split = (char*)workspace + align_up(M * N * 4);
     SGQ_HIP(launch_gemm_i8(x, M, K, N, packed_gate, scales_gate, per_tensor, bias_gate, h, split, s), "gemm_i8");
     SGQ_HIP(launch_gemm_i8(x, M, K, N, packed_up, scales_up, per_tensor, bias_up, u, split, s), "gemm_i8");
@@ -659,8 +699,11 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
         return fail(SGQ_ERR_UNSUPPORTED, "%s: K = %lld is too long for this batch", fn, (long long)K);
     // The same path as two forward calls of these shapes, so the gate and up
     // sums are the plain forward's.
-    const SkinnyPlan sp = skinny_plan(M, K, g, device_cus(s));
+    const int cus = device_cus(s);
+    const SkinnyPlan sp = skinny_plan(M, K, g, cus);
     if (sp.C > 0) {
+        const int lw = check_launch_ws(fn, skinny_ws_bytes(sp, M, N, 2), workspace, workspace_bytes);
+        if (lw != SGQ_OK) return lw;
         const void* pk[2] = {packed_gate, packed_up};
         const float* ds[2] = {devscales_gate, devscales_up};
         const float* bs[2] = {bias_gate, bias_up};
@@ -673,6 +716,9 @@ int sgq_swiglu_int4(const float* x, int64_t M, int64_t K, int64_t N, const void*
                 "swiglu_gemv_i4");
         return ok();
     }
+    const int lw = check_launch_ws(fn, align_up(M * N * 4) + gemm_launch_ws_bytes(4, M, K, N, (int)g.spc, cus),
+                                   workspace, workspace_bytes);
+    if (lw != SGQ_OK) return lw;
     void* split = (char*)workspace + align_up(M * N * 4);
     SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_gate, devscales_gate, g, bias_gate, h, split, s), "gemm_i4");
     SGQ_HIP(launch_gemm_i4(x, M, K, N, packed_up, devscales_up, g, bias_up, u, split, s), "gemm_i4");

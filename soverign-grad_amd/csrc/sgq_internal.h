@@ -36,9 +36,8 @@ constexpr int64_t kPadK = 16;  // rows are padded to a multiple of this
 
 // Compute units the launch heuristics plan for: the count of the device a
 // stream runs on (a partition of an MI355X reports its own share), at most
-// kMaxCus, the full MI355X.  Split-K workspaces are sized for kMaxCus, an upper
-// bound for every smaller count: the number of K splits never grows as the CU
-// count shrinks.
+// kMaxCus, the full MI355X.  Split-K workspaces are sized for the largest
+// need over every count from 1 to kMaxCus.
 constexpr int64_t kMaxCus = 256;
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -225,14 +224,25 @@ inline Skinny8Plan skinny8_plan(int64_t M, int64_t K, int64_t N, int64_t cus) {
 inline int64_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t N, int NG) {
     return p.C > 0 && p.S > 1 ? (int64_t)NG * p.S * M * N * 4 : 0;
 }
-// The largest such workspace over every group size on the largest device
-// (the split count never grows as the CU count falls).
+// The largest such workspace over every group size and every device of 1 to
+// kMaxCus CUs.  Neither extreme alone bounds it: the K splits of the narrow
+// form grow with the CU count, while a device with few CUs can call a weight
+// wide that a larger one calls narrow or leaves to the GEMV, and the wide
+// form's two-row-block batches split K (as far as the scales of a range fit
+// LDS) whatever the CU count.  The wide test (at most a CU count) holds on
+// every device below some count and the narrow splits are monotone in it, so
+// one CU (every weight that can be wide is) and kMaxCus (the most narrow
+// splits) cover all of them; the CPU tests sweep every count to confirm it.
+// The group sizes stand for every other: the plan depends on the group only
+// through the column blocks per workgroup (2 when spc % 4 == 0, 4 when spc %
+// 8 == 0), which 32 and 64 realise wherever any larger group does.
 inline int64_t skinny_ws_bound(int64_t M, int64_t K, int64_t N, int NG) {
     int64_t ws = 0;
-    for (int64_t G : {16, 32, 64, 128}) {
-        const int64_t w = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, G), kMaxCus), M, N, NG);
-        if (w > ws) ws = w;
-    }
+    for (int64_t G : {16, 32, 64, 128})
+        for (int64_t cus : {(int64_t)1, kMaxCus}) {
+            const int64_t w = skinny_ws_bytes(skinny_plan(M, K, I4Geom(K, N, G), cus), M, N, NG);
+            if (w > ws) ws = w;
+        }
     return ws;
 }
 
@@ -314,12 +324,26 @@ struct GemmTile {
     int64_t bm, bn, per_cu;  // tile rows and columns, workgroups resident per CU
 };
 int device_cus(hipStream_t s);
+// XCDs of the device `s` runs on (hipDeviceAttributeNumberOfXccs, 1 if the
+// runtime does not say, at most kMaxXcds), read once per device; the kernels
+// that place workgroups by XCD take xcd_log2 of it (0, the identity order,
+// for a count that is not a power of two).
+constexpr int kMaxXcds = 16;
+int device_xcds(hipStream_t s);
+int xcd_log2(int xcds);
+// Tile rows of the GEMM's per-XCD rectangles for this shape on a device of
+// `cus` CUs and `xcds` XCDs (0: the plain order; the grid splits K or does
+// not tile into one rectangle per XCD).  mode: INT4 strips per scale column.
+int gemm_rect_rows(int bits, int64_t M, int64_t K, int64_t N, int mode, int64_t cus, int64_t xcds);
 GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus);
 // Tile of the three-term GEMM for a code width and batch: 32 or 64 rows by
 // 128 columns for batches of up to 32 or 64 rows, else 128 x 256 (INT8) or
 // 128 x 128 (INT4).
 GemmTile gemm_tile(int bits, int64_t M);
 int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+// The workspace bytes the GEMM launch of this shape (INT4: mode = spc, INT8:
+// unused) takes on `cus` compute units: what launch_gemm_i8/i4 writes.
+int64_t gemm_launch_ws_bytes(int bits, int64_t M, int64_t K, int64_t N, int mode, int64_t cus);
 // The plan a forward of this shape runs on `cus` compute units: path 0 the
 // GEMV, 1 the three-term bf16 GEMM, 2 the fp32 GEMM, 3 the flat INT4 kernel,
 // 4 the skinny MFMA kernel; ks the K splits (1: none).

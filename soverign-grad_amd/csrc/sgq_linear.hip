@@ -149,17 +149,18 @@ __device__ __forceinline__ float4 buf_load4f(__amdgpu_buffer_rsrc_t r, int voff,
 // correctly rounded.
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
-// Workgroups are dispatched round-robin over the 8 XCDs (workgroup b runs on
-// XCD b % 8), and each XCD has its own L2.  Strips that share a scale column
-// (and, for the MFMA GEMM, tiles that share operands) should run on the same
-// XCD, so the first 8*(n/8) workgroup ids are permuted to give XCD x the
-// contiguous range [x*(n/8), (x+1)*(n/8)); the remaining ids map to themselves.
-// A bijection on [0, n).
-constexpr int kXcds = 8;
-__device__ __forceinline__ int xcd_swizzle(int b, int n) {
-    const int per = n / kXcds;
-    const int sw = (b % kXcds) * per + b / kXcds;
-    return b >= per * kXcds ? b : sw;  // a select, not a branch, ahead of the first loads
+// Workgroups are dispatched round-robin over the device's X = 2^xlog XCDs
+// (workgroup b runs on XCD b % X; a full MI355X has 8, its partitions 4, 2 or
+// 1, read per device as device_xcds), and each XCD has its own L2.  Strips
+// that share a scale column (and, for the MFMA GEMM, tiles that share
+// operands) should run on the same XCD, so the first X*(n/X) workgroup ids are
+// permuted to give XCD x the contiguous range [x*(n/X), (x+1)*(n/X)); the
+// remaining ids map to themselves.  A bijection on [0, n) for any xlog (0: the
+// identity), so the XCD count only affects speed.
+__device__ __forceinline__ int xcd_swizzle(int b, int n, int xlog) {
+    const int per = n >> xlog;
+    const int sw = (b & ((1 << xlog) - 1)) * per + (b >> xlog);
+    return b >= (per << xlog) ? b : sw;  // a select, not a branch, ahead of the first loads
 }
 
 // Workgroup barrier ordering LDS accesses only: waits for this wave's LDS
@@ -187,6 +188,7 @@ struct GemvArgs {
     int nblk;                // grid x (passed here: reading the hidden gridDim argument cost a second
                              // dependent round of kernel-argument loads ahead of the first data load)
     int cus;                 // compute units of the launch's device (host-side heuristics only)
+    int xlog;                // log2 of the device's XCD count (xcd_swizzle)
 };
 
 // ---------------------------------------------------------------------------
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
     // division on the way to the first load: every index here is a shift, a
     // mask or a grid coordinate (a runtime division costs about 30 dependent
     // instructions, all of them ahead of the loads).
-    const int vg = xcd_swizzle(blockIdx.x, a.nblk);
+    const int vg = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
     const int prow = vg & ((1 << a.Plog) - 1);
     const int jg = vg >> a.Plog;
     const int m0 = prow * MT;
@@ -824,7 +826,7 @@ template <int BITS, bool KALIGN4, bool PT, class SH>
 __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(
     const float* __restrict__ x, int M, int K, int N, const uint4* __restrict__ W, const float* __restrict__ S,
     int mode, int Kpad, int RQ, int NS, int KS, int sps, const float* __restrict__ bias, float* __restrict__ y,
-    float* __restrict__ part, int xr) {
+    float* __restrict__ part, int xr, int xlog) {
     // mode: INT8 -> per-tensor flag (also the template flag PT, so that no
     // stage holds a branch); INT4 -> strips per scale column (a multiple of
     // 16: one scale column per 128-column tile).  Workgroup b computes split
@@ -845,15 +847,15 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
     // go round-robin over the 8 XCDs, each with its own L2): C4's L2 misses
     // had every XCD fetch nearly all of x.  Measured 1-2% faster on the large
     // shapes; with a split (small grids) the plain order measured better.
-    const int bsw = KS == 1 ? xcd_swizzle(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+    const int bsw = KS == 1 ? xcd_swizzle(blockIdx.x, gridDim.x, xlog) : (int)blockIdx.x;
     const int tile = bsw / KS, split = bsw - tile * KS;
     int tm = tile / ntn, tn = tile - tm * ntn;
     if (xr > 0) {
-        // The grid's tiles fall into 8 rectangles of xr tile rows by per / xr
-        // tile columns, one per XCD (its share of the swizzled ids), so an
-        // XCD's L2 fetches xr row blocks of x and per / xr column blocks of
-        // codes instead of every column block (C4: 16 MiB per XCD, not 20).
-        const int per = gridDim.x / kXcds, x = tile / per, l = tile - x * per;
+        // The grid's tiles fall into one rectangle of xr tile rows by per / xr
+        // tile columns per XCD (its share of the swizzled ids), so an XCD's
+        // L2 fetches xr row blocks of x and per / xr column blocks of codes
+        // instead of every column block (C4 on 8 XCDs: 16 MiB per XCD, not 20).
+        const int per = (int)gridDim.x >> xlog, x = tile / per, l = tile - x * per;
         const int bw = per / xr, rects_m = (gridDim.x / ntn) / xr;
         tm = (x % rects_m) * xr + l % xr;
         tn = (x / rects_m) * bw + l / xr;
@@ -1137,6 +1139,7 @@ struct SkinnyArgs {
     FastDiv wgd;  // division by wgpw
     const float* gamma;
     float eps;
+    int xlog;     // log2 of the device's XCD count
 };
 
 // The whole-K form for one row block (5..16 rows over wide weights, no K
@@ -1166,7 +1169,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     const int g = lane >> 4, n = lane & 15;
     const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int K = a.K;
-    const int vv = xcd_swizzle(blockIdx.x, a.nblk);
+    const int vv = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
     const int wt = NG == 1 ? a.wgd.div(vv) : 0;  // weight of the side-by-side set
     const int v = vv - wt * a.wgpw;
     const int blk0 = v * C;  // first column block
@@ -1379,7 +1382,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     const int K = a.K;
     // Workgroup v: K range v % S of column group v / S (the ranges of one
     // column group are neighbours, so they share an XCD's L2 for the scales).
-    const int v = xcd_swizzle(blockIdx.x, a.nblk);
+    const int v = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
     const int split = SPLIT ? (v & ((1 << a.slog) - 1)) : 0;
     const int cgrp = SPLIT ? (v >> a.slog) : v;
     const int blk0 = cgrp * C;  // first column block
@@ -1622,6 +1625,7 @@ struct Skinny8Args {
     FastDiv cgd;  // division by ncg
     float* y;
     int nblk;
+    int xlog;  // log2 of the device's XCD count
 };
 
 // HALF (one row block, M <= 8): lane n < 8 loads and splits k 8g .. 8g + 3
@@ -1634,7 +1638,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int K = a.K;
-    const int v = xcd_swizzle(blockIdx.x, a.nblk);  // row tile major: an XCD's workgroups share x rows
+    const int v = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);  // row tile major: an XCD's workgroups share x rows
     const int rt = a.cgd.div(v), cg = v - rt * a.ncg;
     const int m0 = rt * 16 * MB, s0 = cg * 4 * C;
     const int mrows = min(16 * MB, a.M - m0), nstr = min(4 * C, a.NS - s0);
@@ -1941,6 +1945,7 @@ template <int BITS, int NG>
 hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.M = (int)M;
     a.cus = device_cus(s);
+    a.xlog = xcd_log2(device_xcds(s));
     constexpr int kRowsMax = 8;  // rows per workgroup beyond four
     // All rows in one launch: M <= 4 as one row group, larger M in row groups
     // of kRowsMax (each a workgroup of its own over the same strip), their
@@ -2016,6 +2021,7 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     a.slog = slog;
     a.sbs = (int)ceil_div(ceil_div(g.Kpad, kSkinnySB), S);
     a.nblk = (int)(g.NS / (2 * C)) << slog;  // skinny_plan: 2C divides spc, which divides NS
+    a.xlog = xcd_log2(device_xcds(s));
     if (form == 0) {
         if constexpr (MB == 1) {
             constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
@@ -2109,6 +2115,7 @@ hipError_t skinny8_launch(const float* x, int64_t M, int64_t K, int64_t N, const
     a.cgd = FastDiv((uint32_t)a.ncg);
     a.y = y;
     a.nblk = (int)(ceil_div(M, 16 * MB) * a.ncg);
+    a.xlog = xcd_log2(device_xcds(s));
     constexpr int U = MB == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
     if (MB == 1 && M <= 8)
         k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, MB == 1><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
@@ -2249,6 +2256,40 @@ int device_cus(hipStream_t s) {
     return cus;
 }
 
+// XCD count per device, read once like the CU count (0: not read yet).  A
+// full MI355X has 8; its compute partitions report 4, 2 or 1.
+std::atomic<int> g_device_xcds[kCuCacheDevices];
+
+int device_xcds(hipStream_t s) {
+    int dev = 0;
+    if (hipStreamGetDevice(s, &dev) != hipSuccess) {
+        (void)hipGetLastError();
+        if (hipGetDevice(&dev) != hipSuccess) {
+            (void)hipGetLastError();
+            return 1;
+        }
+    }
+    const bool cache = dev >= 0 && dev < kCuCacheDevices;
+    if (cache) {
+        const int c = g_device_xcds[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int x = 0;
+    if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x < 1) {
+        (void)hipGetLastError();
+        x = 1;  // unknown: the identity workgroup order, correct on any device
+    }
+    x = x < kMaxXcds ? x : kMaxXcds;
+    if (cache) g_device_xcds[dev].store(x, std::memory_order_relaxed);
+    return x;
+}
+
+int xcd_log2(int xcds) {
+    int l = 0;
+    while ((2 << l) <= xcds) ++l;
+    return (1 << l) == xcds ? l : 0;  // not a power of two: the identity order
+}
+
 GemmPlan gemm_plan(int64_t M, int64_t K, int64_t N, const GemmTile& t, int64_t cus) {
     const int64_t tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
     const int64_t KT = ceil_div(round_up(K, kPadK), kBK);
@@ -2303,6 +2344,12 @@ int64_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
 // of 16 strips, i.e. a group that is a multiple of 128).
 static bool gemm_three_term(int bits, int mode) { return bits == 8 || mode % 16 == 0; }
 
+int64_t gemm_launch_ws_bytes(int bits, int64_t M, int64_t K, int64_t N, int mode, int64_t cus) {
+    const bool three = gemm_three_term(bits, mode);
+    const GemmPlan p = gemm_plan(M, K, N, three ? gemm_tile(bits, M) : GemmTile{kBM, kBN, 2}, cus);
+    return p.KS > 1 ? (int64_t)p.KS * M * N * 4 : 0;
+}
+
 void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, int64_t cus, int* path, int* ks) {
     *ks = 1;
     if (bits == 4 && !I4Geom(K, N, group_size).tiled) {
@@ -2330,25 +2377,34 @@ void linear_plan(int bits, int64_t M, int64_t K, int64_t N, int64_t group_size, 
     *ks = gemm_plan(M, K, N, three ? gemm_tile(bits, M) : GemmTile{kBM, kBN, 2}, cus).KS;
 }
 
-namespace {
-// Tile rows per XCD rectangle for a grid of tm x tn tiles without a K split:
-// the divisor a of both tm and per = tm * tn / 8 (per / a dividing tn) that
-// minimises what one XCD's L2 fetches, a row blocks of x (xb bytes each) and
-// per / a column blocks of codes (wb bytes each); 0 when the grid does not
-// tile into 8 such rectangles (the plain XCD order then).
-int xcd_rect_rows(int64_t tm, int64_t tn, int64_t xb, int64_t wb) {
+// Tile rows per XCD rectangle for a grid of tm x tn tiles without a K split
+// on a device of `xcds` XCDs: the divisor a of both tm and per = tm * tn /
+// xcds (per / a dividing tn) that minimises what one XCD's L2 fetches, a row
+// blocks of x (xb bytes each) and per / a column blocks of codes (wb bytes
+// each); 0 when the grid does not tile into xcds such rectangles (the plain
+// XCD order then).
+int xcd_rect_rows_impl(int64_t tm, int64_t tn, int64_t xb, int64_t wb, int64_t xcds) {
     const int64_t T = tm * tn;
-    if (T % kXcds != 0) return 0;
-    const int64_t per = T / kXcds;
+    if (xcds < 1 || T % xcds != 0) return 0;
+    const int64_t per = T / xcds;
     int best = 0;
     int64_t cost = 0;
     for (int64_t a = 1; a <= per && a <= tm; ++a) {
-        if (per % a || tm % a || tn % (per / a) || (tm / a) * (tn / (per / a)) != kXcds) continue;
+        if (per % a || tm % a || tn % (per / a) || (tm / a) * (tn / (per / a)) != xcds) continue;
         const int64_t c = a * xb + (per / a) * wb;
         if (best == 0 || c < cost) best = (int)a, cost = c;
     }
     return best;
 }
+
+int gemm_rect_rows(int bits, int64_t M, int64_t K, int64_t N, int mode, int64_t cus, int64_t xcds) {
+    const bool three = gemm_three_term(bits, mode);
+    const GemmTile t = three ? gemm_tile(bits, M) : GemmTile{kBM, kBN, 2};
+    if (!three || gemm_plan(M, K, N, t, cus).KS != 1) return 0;
+    return xcd_rect_rows_impl(ceil_div(M, t.bm), ceil_div(N, t.bn), t.bm * K * 4, t.bn * K * bits / 8, xcds);
+}
+
+namespace {
 
 template <int BITS>
 hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* sc, int mode,
@@ -2359,16 +2415,18 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
     const GemmPlan p = gemm_plan(M, K, N, t, device_cus(s));
     float* part = p.KS > 1 ? (float*)ws : nullptr;
     const dim3 grid((unsigned)(ceil_div(M, t.bm) * ceil_div(N, t.bn) * p.KS));
-    const int xr = p.KS == 1 ? xcd_rect_rows(ceil_div(M, t.bm), ceil_div(N, t.bn), t.bm * K * 4,
-                                             t.bn * K * BITS / 8)
+    const int xcds = device_xcds(s);
+    const int xr = p.KS == 1 ? xcd_rect_rows_impl(ceil_div(M, t.bm), ceil_div(N, t.bn), t.bm * K * 4,
+                                                  t.bn * K * BITS / 8, xcds)
                              : 0;
+    const int xlog = xcd_log2(xcds);
     const bool k4 = x_aligned4(x, K);
     const bool pt = BITS == 8 && mode;
     using Big = typename std::conditional<BITS == 8, G3Wide, G3Tile>::type;
 #define SGQ_GEMM3(SH, A4, PT_)                                                                                 \
     k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(x, (int)M, (int)K, (int)N,              \
                                                                     (const uint4*)packed, sc, mode, (int)Kpad, \
-                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part, xr)
+                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part, xr, xlog)
 #define SGQ_GEMM3_SHAPE(SH)               \
     if (k4 && pt)                         \
         SGQ_GEMM3(SH, true, true);        \

@@ -262,25 +262,61 @@ def _plan(lib, bits, M, K, N, G, cus):
     return path.value, ks.value
 
 
+def _ws_covers(lib, bits, M, K, N, G, cus):
+    """The size queries cover the plan this device runs: the forward's
+    workspace holds its K splits' partials, the gated MLP's those of both
+    weights (one skinny launch) or the up projection plus one GEMM's."""
+    path, ks = _plan(lib, bits, M, K, N, G, cus)
+    assert ks >= 1
+    if ks == 1:
+        return path, ks
+    part = ks * M * N * 4
+    ws = lib.sgq_linear_workspace_bytes(bits, M, K, N)
+    sw = lib.sgq_swiglu_workspace_bytes(bits, M, K, N, G)
+    assert ws >= part, (bits, M, K, N, G, cus, ks)
+    if path == 4:
+        assert sw >= 2 * part, (bits, M, K, N, G, cus, ks)
+    elif path in (1, 2):
+        assert sw >= -(-M * N * 4 // 256) * 256 + part, (bits, M, K, N, G, cus, ks)
+    return path, ks
+
+
 def test_plan_follows_the_device_cu_count(lib):
     """The launch plan takes the CU count of the device (a partitioned MI355X
-    reports fewer than 256): fewer CUs never mean more K splits, so the
-    workspace sized for 256 CUs covers every device."""
+    reports fewer than 256).  Fewer CUs can mean more K splits: a weight that
+    is narrow (or left to the GEMV) on 256 CUs can be wide on 32, where 17..32
+    rows split a long K into ranges.  The workspace queries must cover the
+    plan of every CU count from 1 to 256."""
     shapes = [(8, 128, 1024, 1024, 0), (8, 512, 4096, 4096, 0), (8, 256, 4096, 1024, 0), (4, 256, 4096, 1024, 128),
               (4, 300, 2048, 640, 32), (8, 2048, 4096, 4096, 0), (4, 64, 11008, 4096, 128), (8, 17, 8192, 512, 0),
               (4, 16, 11008, 4096, 128), (4, 32, 11008, 4096, 64), (4, 24, 16384, 11008, 128),
-              (4, 20, 28672, 8192, 128), (4, 32, 8192, 3072, 32)]
+              (4, 20, 28672, 8192, 128), (4, 32, 8192, 3072, 32),
+              # the GEMV on 256 CUs, a wide weight with two row blocks (K ranges) on a partition
+              (4, 24, 16384, 640, 128), (4, 24, 8320, 1280, 128)]
     for bits, M, K, N, G in shapes:
-        ws = lib.sgq_linear_workspace_bytes(bits, M, K, N)
-        prev = None
-        for cus in (256, 128, 80, 64, 32, 8, 1):
-            path, ks = _plan(lib, bits, M, K, N, G, cus)
-            assert ks >= 1
-            if path in (1, 2, 4) and ks > 1:
-                assert ws >= ks * M * N * 4, (bits, M, K, N, cus)
-            if prev is not None:
-                assert ks <= prev, (bits, M, K, N, cus, ks, prev)
-            prev = ks
+        for cus in range(1, 257):
+            _ws_covers(lib, bits, M, K, N, G, cus)
+    # The two shapes above: no workspace on the full chip's plan, K ranges below it.
+    assert _plan(lib, 4, 24, 16384, 640, 128, 256) == (0, 1)
+    assert _plan(lib, 4, 24, 16384, 640, 128, 32) == (4, 2)
+    assert _plan(lib, 4, 24, 8320, 1280, 128, 64)[0] == 4 and _plan(lib, 4, 24, 8320, 1280, 128, 64)[1] > 1
+    assert lib.sgq_linear_workspace_bytes(4, 24, 16384, 640) >= 2 * 24 * 640 * 4
+    assert lib.sgq_swiglu_workspace_bytes(4, 24, 16384, 640, 128) >= 2 * 2 * 24 * 640 * 4
+
+
+def test_workspace_covers_every_device_sweep(lib):
+    """Skinny batches (5..32 rows) over long K and narrow N, every group size
+    the skinny kernel takes, on every CU count from 1 to 256: the forward's
+    and the gated MLP's workspace queries hold each device's K-split partials."""
+    for M in range(5, 33):
+        for K in (8320, 11008, 16384, 24576):
+            for N in (256, 512, 640, 1280, 2048):
+                for G in (16, 32, 64, 128):
+                    for cus in range(1, 257):
+                        _ws_covers(lib, 4, M, K, N, G, cus)
+
+
+def test_plan_examples(lib):
     # C4 fills any device without splitting K; a small GEMM splits less on a partition.
     assert _plan(lib, 8, 2048, 4096, 4096, 0, 256) == (1, 1)
     assert _plan(lib, 8, 256, 4096, 1024, 0, 256)[1] > _plan(lib, 8, 256, 4096, 1024, 0, 32)[1]
@@ -291,6 +327,36 @@ def test_plan_follows_the_device_cu_count(lib):
     assert _plan(lib, 8, 256, 4096, 1024, 0, 1024) == _plan(lib, 8, 256, 4096, 1024, 0, 256)
     assert _plan(lib, 4, 8, 4096, 11008, 128, 1024) == _plan(lib, 4, 8, 4096, 11008, 128, 256)
     assert lib.sgq_linear_plan(8, 1, 4, 4, 0, -1, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == 1
+
+
+def _xcd_plan(lib, bits, M, K, N, G, cus, xcds):
+    rows, xlog = ctypes.c_int(-1), ctypes.c_int(-1)
+    assert lib.sgq_gemm_xcd_plan(bits, M, K, N, G, cus, xcds, ctypes.byref(rows), ctypes.byref(xlog)) == 0
+    return rows.value, xlog.value
+
+
+def test_gemm_places_tiles_by_the_device_xcd_count(lib):
+    """The GEMM's per-XCD rectangles and the workgroup permutation follow the
+    device's XCD count: a full MI355X (256 CUs, 8 XCDs) and a partition of
+    128 CUs on 4 XCDs.  C4's 16 x 16 tiles of 128 x 256: 8 XCDs take 4 x 8
+    rectangles (4 row blocks of x, 8 column blocks of codes per L2: 16 MiB);
+    4 XCDs take 64 tiles each, 4 x 16 (8 + 16 MiB, against 16 + 8 for 8 x 8,
+    the first of the equal costs)."""
+    assert _xcd_plan(lib, 8, 2048, 4096, 4096, 0, 256, 8) == (4, 3)
+    assert _xcd_plan(lib, 8, 2048, 4096, 4096, 0, 128, 4) == (4, 2)
+    # One XCD: one rectangle holds the whole grid, a single row block.
+    assert _xcd_plan(lib, 8, 2048, 4096, 4096, 0, 32, 1)[1] == 0
+    # A count that is not a power of two keeps the identity order.
+    assert _xcd_plan(lib, 8, 2048, 4096, 4096, 0, 192, 6)[1] == 0
+    # A grid that splits K has no rectangles.
+    assert _xcd_plan(lib, 8, 256, 4096, 1024, 0, 256, 8)[0] == 0
+    # Tiles that do not fall into one rectangle per XCD: 3 x 3 tiles on 8 XCDs.
+    assert _xcd_plan(lib, 8, 384, 4096, 768, 0, 8, 8)[0] == 0
+    for cus, xcds in ((256, 8), (128, 4), (64, 2)):
+        rows, xlog = _xcd_plan(lib, 8, 2048, 4096, 4096, 0, cus, xcds)
+        assert 1 << xlog == xcds
+        per = 16 * 16 // xcds
+        assert per % rows == 0 and 16 % rows == 0 and 16 % (per // rows) == 0
 
 
 def test_plan_splits_fill_one_pass(lib):

@@ -77,5 +77,11 @@ def test_noalloc_refuses_oversized_scratch(sgq, dev):
     M, K, N = 32, 131072, 16512
     assert lib.sgq_linear_workspace_bytes(4, M, K, N) > 32 << 20
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = lib.sgq_linear_int4_noalloc(16, M, K, N, 256, 256, 256, 128, None, 256, stream)
+    # Real device buffers (far smaller than the shape): the call must refuse
+    # before it launches anything, and no argument is a made-up address.
+    x, packed, scales, devscales, y = (torch.zeros(64, dtype=torch.float32, device=dev) for _ in range(5))
+    rc = lib.sgq_linear_int4_noalloc(x.data_ptr(), M, K, N, packed.data_ptr(), scales.data_ptr(),
+                                     devscales.data_ptr(), 128, None, y.data_ptr(), stream)
     assert rc == SGQ_ERR_UNSUPPORTED and b"scratch" in lib.sgq_last_error()
+    torch.cuda.synchronize()
+    assert not y.any()  # nothing was written
