@@ -333,11 +333,27 @@ def calibration_copy(dev, mib: int = 64) -> None:
 
 def measured_traffic(config: str):
     """HBM bytes per launch of the dominant kernel, from the committed
-    rocprofv3 PMC summary for this workload (None if there is none)."""
+    rocprofv3 PMC summary for this workload: None if there is none, or if it
+    measured other kernel sources than this build's (see csrc_digest)."""
     path = ROOT / "profiles" / f"traffic_{config}.json"
     if not path.exists():
         return None
-    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    t = json.loads(path.read_text())
+    return t.get("hbm_bytes_per_launch") if t.get("csrc_digest") == csrc_digest() else None
+
+
+def csrc_digest() -> str:
+    """A digest of the library's kernel sources (soverign-grad_amd/csrc): a
+    committed profile records the digest of the build it measured, so a
+    profile of other kernels is never reported as this build's."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "soverign-grad_amd" / "csrc").iterdir()):
+        if f.suffix in (".hip", ".h"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def profiled_kernel(config: str):
@@ -347,6 +363,24 @@ def profiled_kernel(config: str):
     if not path.exists():
         return None
     return json.loads(path.read_text())
+
+
+def rocprof_fields(prof: dict, nbytes: float, peak: float, per_second) -> dict:
+    """The committed kernel-trace figures of the dominant kernel: reported as
+    this build's (kernel_ns_rocprof, frac_kernel_rocprof) only when the
+    profile names the digest of these kernel sources; otherwise under
+    rocprof_historical, with both digests, so a stale profile never reads as
+    a measurement of this build."""
+    kns = prof.get("avg_ns_graph_replays") or prof.get("avg_ns")
+    frac = round(per_second(nbytes / (kns * 1e-9)) / peak, 4)
+    cur = csrc_digest()
+    if prof.get("csrc_digest") == cur:
+        return {"kernel_ns_rocprof": kns, "frac_kernel_rocprof": frac, "kernel": prof.get("kernel"),
+                "kernel_summary": prof.get("summary")}
+    return {"rocprof_historical": {"kernel_ns": kns, "frac": frac, "kernel": prof.get("kernel"),
+                                   "profiled_csrc_digest": prof.get("csrc_digest"), "current_csrc_digest": cur,
+                                   "summary": prof.get("summary"),
+                                   "note": "profiled on other kernel sources than this build's"}}
 
 
 def cpu_model() -> str:
@@ -370,15 +404,39 @@ def _ref_forward_ms(ref, c, x, q, s, b, budget_s: float, max_reps: int = 50):
     return statistics.median(secs) * 1e3, reps
 
 
+def _ref_breakdown(ref, c, x, q, s, b, budget_s: float) -> dict:
+    """The reference forward of one shape on this host, as BASELINE.md's CPU
+    plan asks: the whole forward on every thread (median of the calls that
+    fit in half of budget_s, at least 3), its dequantize / matmul / bias phases
+    (the same forward split at the phase boundaries, median of at least 3
+    calls in a quarter of it) and the whole forward on one thread (median of
+    at least 3 calls in the last quarter), each after one untimed call.  The
+    bias phase is the reference's add() (src/ops.cpp:132-171), its broadcast
+    path for a [1, N] bias over M > 1 rows; 0 without a bias."""
+    ms, reps = _ref_forward_ms(ref, c, x, q, s, b, budget_s / 2)
+    n_ph = int(max(3, min(50, (budget_s / 4) / max(ms / 1e3, 1e-6))))
+    ph = ref.time_phases(c["bits"], x, q, s, c["scheme"], c["G"], b, n_ph)
+    phases = {k: round(statistics.median(p[i] for p in ph) * 1e3, 4)
+              for i, k in enumerate(("dequantize_ms", "matmul_ms", "bias_ms"))}
+    prev = ref.set_threads(1)
+    try:
+        ms1, n1 = _ref_forward_ms(ref, c, x, q, s, b, budget_s / 4)
+    finally:
+        ref.set_threads(prev)
+    return {"ms": ms, "calls": reps, "phases_ms": phases, "phase_calls": n_ph, "ms_1thread": ms1, "calls_1thread": n1}
+
+
 CPU_OTHER = ["c1", "c3_gate_m1", "c3_gate_m16", "c3_down_m1", "c3_down_m16", "c4"]
 
 
 def cpu_baseline_others(budget_s: float):
     """The reference's CPU forward on the other BASELINE configs (C1, C3 at M=1
-    and 16, C4) and one C5 decode step, each on a bounded sample: the median
-    of the calls that fit in budget_s per config (at least 3).  C5's 110 calls
-    are 22 layers of the same five shapes, so one layer's five calls are timed
-    and the step is 22 times their sum.  None when oracle/_ref is absent."""
+    and 16, C4) and one C5 decode step, each on a bounded sample (see
+    _ref_breakdown): every-thread and one-thread medians, the dequantize /
+    matmul / bias phase medians, and the calls each median is over.  C5's 110
+    calls are 22 layers of the same five shapes, so one layer's five calls are
+    timed and the step is 22 times their sum.  None when oracle/_ref is
+    absent."""
     from oracle.oracle import Oracle, Reference, reference_available
     from soverign_grad_amd import synth
 
@@ -394,30 +452,43 @@ def cpu_baseline_others(budget_s: float):
         x = synth_normal((c["M"], c["K"]), seed, synth.STREAM_X, 0.0, 1.0)
         b = synth_normal((1, c["N"]), seed, synth.STREAM_BIAS, 0.0, 0.02) if c["bias"] else None
         q, sc = orc.quantize_int4(W, c["G"]) if c["bits"] == 4 else orc.quantize_int8(W, c["scheme"])
-        ms, reps = _ref_forward_ms(ref, c, x, q, sc, b, budget_s)
-        out[key] = {"workload": c["name"], "ms_per_call": round(ms, 3), "calls_timed": reps,
+        r = _ref_breakdown(ref, c, x, q, sc, b, budget_s)
+        ms = r["ms"]
+        out[key] = {"workload": c["name"], "ms_per_call": round(ms, 3), "calls_timed": r["calls"],
                     "GB_s": round(alg_bytes(c) / ms / 1e6, 3), "TFLOP_s": round(alg_flops(c) / ms / 1e9, 4),
+                    "phases_ms": r["phases_ms"], "phase_calls": r["phase_calls"],
+                    "one_thread": {"ms_per_call": round(r["ms_1thread"], 3), "calls_timed": r["calls_1thread"],
+                                   "GB_s": round(alg_bytes(c) / r["ms_1thread"] / 1e6, 3), "cores": 1},
                     "threads": threads, "cpu": model, "kind": "reference"}
-        log(f"[bench] cpu {key}: {ms:.2f} ms/call over {reps} calls")
+        log(f"[bench] cpu {key}: {ms:.2f} ms/call over {r['calls']} calls, phases {r['phases_ms']}, "
+            f"1 thread {r['ms_1thread']:.2f} ms")
     seed = synth.config_seed(4)
-    layer_ms, calls = 0.0, 0
+    step = {"ms": 0.0, "ms_1thread": 0.0, "dequantize_ms": 0.0, "matmul_ms": 0.0, "bias_ms": 0.0}
+    counts = []
     for i, (name, K, N) in enumerate(C5_MATS):
         c = dict(bits=4, M=C5_M, K=K, N=N, G=C5_G, scheme=2, bias=False)
         W = synth.normal((K, N), seed, 3 * i + synth.STREAM_W, 0.0, 0.02)
         x = synth.normal((C5_M, K), seed, 3 * i + synth.STREAM_X, 0.0, 1.0)
         q, sc = orc.quantize_int4(W, C5_G)
-        ms, reps = _ref_forward_ms(ref, c, x, q, sc, None, budget_s / len(C5_MATS))
-        layer_ms += ms
-        calls += reps
-    step_ms = C5_LAYERS * layer_ms
+        r = _ref_breakdown(ref, c, x, q, sc, None, budget_s / len(C5_MATS))
+        step["ms"] += C5_LAYERS * r["ms"]
+        step["ms_1thread"] += C5_LAYERS * r["ms_1thread"]
+        for k, v in r["phases_ms"].items():
+            step[k] += C5_LAYERS * v
+        counts.append(f"{name} {r['calls']}/{r['phase_calls']}/{r['calls_1thread']}")
+    step_ms = step["ms"]
     nbytes = C5_LAYERS * sum(K * N // 2 + 4 * (K * N // C5_G) + 4 * C5_M * (K + N) for _, K, N in C5_MATS)
     flops = C5_LAYERS * sum(2 * C5_M * K * N for _, K, N in C5_MATS)
     out["c5"] = {"workload": "C5: one NanoLLaMA decode step (110 INT4 g128 QuantizedLinear calls, M=8)",
                  "ms_per_step": round(step_ms, 3),
-                 "sample": f"one layer's 5 calls timed ({calls} calls in all, median per shape), step = 22 x layer",
+                 "sample": "one layer's 5 calls timed, median per shape, step = 22 x layer; calls per shape "
+                           "(forward / phases / one thread): " + ", ".join(counts),
                  "GB_s": round(nbytes / step_ms / 1e6, 3), "TFLOP_s": round(flops / step_ms / 1e9, 4),
+                 "phases_ms_per_step": {k: round(step[k], 3) for k in ("dequantize_ms", "matmul_ms", "bias_ms")},
+                 "one_thread": {"ms_per_step": round(step["ms_1thread"], 3),
+                                "GB_s": round(nbytes / step["ms_1thread"] / 1e6, 3), "cores": 1},
                  "threads": threads, "cpu": model, "kind": "reference"}
-    log(f"[bench] cpu c5: {step_ms:.1f} ms/step")
+    log(f"[bench] cpu c5: {step_ms:.1f} ms/step, 1 thread {step['ms_1thread']:.1f} ms/step")
     return out
 
 
@@ -863,10 +934,7 @@ def main() -> int:
     if prof and hbm_bound:
         # The same fraction with the kernel's own duration from the committed
         # rocprofv3 trace (no launch gaps), beside the event-timed one above.
-        kns = prof.get("avg_ns_graph_replays") or prof.get("avg_ns")
-        roofline["kernel_ns_rocprof"] = kns
-        roofline["frac_kernel_rocprof"] = round(nbytes / (kns * 1e-9) / 1e9 / HBM_PEAK_GBS, 4)
-        roofline["kernel_summary"] = prof.get("summary")
+        roofline.update(rocprof_fields(prof, nbytes, HBM_PEAK_GBS, lambda bps: bps / 1e9))
     out = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -923,10 +991,8 @@ def main() -> int:
         }
         p4 = profiled_kernel("c4")
         if p4:
-            kns = p4.get("median_ns") or p4.get("avg_ns")
-            out["secondary"]["roofline"]["kernel_ns_rocprof"] = kns
-            out["secondary"]["roofline"]["frac_kernel_rocprof"] = round(
-                alg_flops(c4) / (kns * 1e-9) / 1e12 / GEMM3_PEAK_TFLOPS, 4)
+            out["secondary"]["roofline"].update(
+                rocprof_fields(p4, alg_flops(c4), GEMM3_PEAK_TFLOPS, lambda fps: fps / 1e12))
         del case4
         torch.cuda.empty_cache()
 

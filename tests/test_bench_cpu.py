@@ -57,3 +57,23 @@ def test_size_sweep_starts_at_c2():
     codes = [K * N // 2 for K, N in bench.GEMV_SWEEP]
     assert codes == sorted(codes)
     assert codes[-1] > 256_000_000  # the largest weight alone exceeds the 256 MB Infinity Cache
+
+
+def test_committed_profiles_count_only_for_the_kernels_they_measured():
+    """A kernel-trace or traffic profile names the digest of the kernel
+    sources it measured; bench.py reports its figures as this build's only
+    when that digest is the current one, else under rocprof_historical."""
+    import bench
+
+    cur = bench.csrc_digest()
+    assert len(cur) == 16 and cur == bench.csrc_digest()
+    prof = {"kernel": "k", "avg_ns_graph_replays": 4000, "summary": "s", "csrc_digest": cur}
+    r = bench.rocprof_fields(prof, 8e6, 8000.0, lambda bps: bps / 1e9)
+    assert r["kernel_ns_rocprof"] == 4000 and abs(r["frac_kernel_rocprof"] - 0.25) < 1e-9
+    stale = dict(prof, csrc_digest="0" * 16)
+    r = bench.rocprof_fields(stale, 8e6, 8000.0, lambda bps: bps / 1e9)
+    assert "kernel_ns_rocprof" not in r and "frac_kernel_rocprof" not in r
+    h = r["rocprof_historical"]
+    assert h["kernel_ns"] == 4000 and h["profiled_csrc_digest"] == "0" * 16 and h["current_csrc_digest"] == cur
+    # No digest at all (a profile written before digests existed) is historical too.
+    assert "rocprof_historical" in bench.rocprof_fields({"avg_ns": 1}, 1.0, 1.0, lambda v: v)
