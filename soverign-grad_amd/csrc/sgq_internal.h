@@ -4,36 +4,27 @@
 // Device layouts
 // --------------
 // The reference keeps one fp32 per code (src/quantization.cpp:32-37,127-153);
-// this library streams packed codes instead, in layouts of its own.
+// this library streams packed codes instead.  Both packed layouts are
+// strip-major: the [K,N] weight is cut into strips of SW consecutive columns,
+// each strip is stored contiguously over all rows, four rows ("a row quad")
+// per 16-byte chunk.  Chunk (strip j, row quad rq) sits at byte
+// (j * RQ + rq) * 16 with RQ = Kpad / 4.  A workgroup that owns a few strips
+// therefore streams a few long contiguous runs, and a wavefront whose lanes
+// take consecutive row quads of a strip reads 16 * lanes contiguous bytes.
 //
-//   INT8 (strip-major): the [K,N] weight is cut into strips of 4 consecutive
-//     columns, each stored contiguously over all rows, four rows ("a row
-//     quad") per 16-byte chunk.  Chunk (strip j, row quad rq) sits at byte
-//     (j * RQ + rq) * 16 with RQ = Kpad / 4 (Kpad = K rounded up to 16);
-//     dword d of a chunk is column 4*j + d, byte r of that dword is row
-//     4*rq + r.  Two's-complement int8 codes.
+//   INT8 (SW = 4):  dword d of a chunk is column 4*j + d; byte r of that
+//                   dword is row 4*rq + r.  Two's-complement int8 codes.
+//   INT4 (SW = 8):  dword r of a chunk is row 4*rq + r; nibble e (bits
+//                   4e..4e+3) is column 8*j + e.  Two's-complement int4.
 //
-//   INT4 (k-octet blocks): the weight is cut into column blocks of 16 and,
-//     within each, k blocks of 32 rows (Kpad = K rounded up to 32, KB =
-//     Kpad / 32 of them).  Block (cb, kb) is 256 bytes at byte
-//     (cb * KB + kb) * 256, so a column block is one contiguous stream over
-//     all of K.  Dword t = 16 * g + c of a block (g = 0..3, c = 0..15) holds
-//     column 16 * cb + c at rows 32 * kb + 8 * g + i in nibble i (bits
-//     4i..4i+3), two's complement.  A dword is thus exactly the B operand of
-//     a v_mfma_f32_16x16x32_bf16 lane (eight consecutive k of one column, lane
-//     16 * g + c of the 64), and a block is that MFMA's whole B tile: the
-//     matrix-core kernels load it with one dword per lane and no exchange
-//     between lanes.  The GEMV reads 16 bytes per lane (four columns of one
-//     k octet), 1 KB contiguous per wavefront load.
-//
-// Rows past K and columns past N are padding with code 0.  INT4 keeps its
-// scales transposed, devscales[sc][Kpad], one column per `spc` strips of 8
-// columns (a column block is two strips): spc = group/8 when N % group == 0
-// (groups never straddle rows, so a whole group of columns shares one scale
-// per row), else spc = 1 (one scale per strip and row; valid because group %
-// 8 == 0 and N % 8 == 0 keep every strip inside one group).  INT4 flat (any
-// other shape) is the flattened tensor with two codes per byte, element i in
-// byte i/2, low nibble first.
+// Rows past K (Kpad = K rounded up to 16) and columns past N are padding
+// with code 0.  INT4 strip-major keeps its scales transposed,
+// devscales[sc][Kpad], one column per `spc` strips: spc = group/8 when
+// N % group == 0 (groups never straddle rows, so a whole group of columns
+// shares one scale per row), else spc = 1 (one scale per strip and row; valid
+// because group % 8 == 0 and N % 8 == 0 keep every strip inside one group).
+// INT4 flat (any other shape) is the flattened tensor with two codes per
+// byte, element i in byte i/2, low nibble first.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -41,8 +32,7 @@
 
 namespace sgq {
 
-constexpr int64_t kPadK = 16;   // INT8 rows are padded to a multiple of this
-constexpr int64_t kPadK4 = 32;  // INT4 rows: whole k blocks
+constexpr int64_t kPadK = 16;  // rows are padded to a multiple of this
 
 // Compute units the launch heuristics plan for: the count of the device a
 // stream runs on (a partition of an MI355X reports its own share), at most
@@ -83,24 +73,18 @@ struct I8Geom {
 };
 
 struct I4Geom {
-    int64_t K, N, G, Kpad, KB, NB, NS, spc, nsc;  // KB k blocks of 32 rows, NB column blocks of 16, NS strips of 8
+    int64_t K, N, G, Kpad, RQ, NS, spc, nsc;  // NS strips of 8 columns
     bool tiled;
     I4Geom(int64_t k, int64_t n, int64_t g)
-        : K(k), N(n), G(g <= 0 ? 32 : g), Kpad(round_up(k, kPadK4)), KB(Kpad / 32), NB(ceil_div(n, 16)), NS(n / 8) {
+        : K(k), N(n), G(g <= 0 ? 32 : g), Kpad(round_up(k, kPadK)), RQ(Kpad / 4), NS(n / 8) {
         tiled = (N % 8 == 0) && (G % 8 == 0);
         spc = (tiled && N % G == 0) ? G / 8 : 1;
         nsc = tiled ? ceil_div(NS, spc) : 0;
     }
-    int64_t blocks() const { return tiled ? NB * KB : 0; }
-    int64_t bytes() const { return tiled ? blocks() * 256 : ceil_div(K * N, 2); }
+    int64_t chunks() const { return tiled ? NS * RQ : 0; }
+    int64_t bytes() const { return tiled ? chunks() * 16 : ceil_div(K * N, 2); }
     int64_t devscale_count() const { return tiled ? nsc * Kpad : 0; }
 };
-
-// Byte offset of the dword holding rows 8*(k/8) .. +7 of column n, and the
-// nibble of row k in it, in the INT4 k-octet layout of KB k blocks.
-__host__ __device__ inline int64_t i4_dword_offset(int64_t n, int64_t k, int64_t KB) {
-    return (((n >> 4) * KB + (k >> 5)) * 64 + ((k >> 3) & 3) * 16 + (n & 15)) * 4;
-}
 
 constexpr int kGemvMaxM = 16;  // M <= this runs the GEMV, larger M the MFMA GEMM (but see below)
 // The plain forward also runs the GEMV for batches of up to this many rows

@@ -122,43 +122,6 @@ __device__ __forceinline__ void lane_reduce_tail(float* v, int lane, int& base) 
     }
 }
 
-// As lane_reduce_tail, over lane bits 2..5 only (xor masks 32, 16, 4, 8):
-// sums v[0..H) over the 16 lanes that share lane bits 0..1, which keep
-// separate totals.  On return v[0..red_hi_left(H)) holds the totals of
-// indices base + i; red_hi_writer(H) tells which lanes hold them.
-constexpr int red_bit_hi(int i) { return i == 0 ? 32 : i == 1 ? 16 : i == 2 ? 4 : 8; }
-template <int H, int I>
-__device__ __forceinline__ void lane_reduce_hi(float* v, int lane, int& base) {
-    static_assert((H & (H - 1)) == 0, "halving needs a power of two");
-    if constexpr (I < 4) {
-        constexpr int O = red_bit_hi(I);
-        if constexpr (H > 1) {
-            constexpr int h = H / 2;
-            const bool upper = (lane & O) != 0;
-            if constexpr (O >= 16) {
-#pragma unroll
-                for (int i = 0; i < h; ++i) v[i] = swap_add<O>(v[i], v[i + h]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < h; ++i) {
-                    const float send = upper ? v[i] : v[i + h];
-                    const float keep = upper ? v[i + h] : v[i];
-                    v[i] = keep + xor_lane<O>(send, lane);
-                }
-            }
-            if (upper) base += h;
-            lane_reduce_hi<h, I + 1>(v, lane, base);
-        } else if constexpr (O == 4 || O == 8) {
-            v[0] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[0]), 0x110 + O, 0xF, 0xF, true));
-            lane_reduce_hi<1, I + 1>(v, lane, base);
-        } else {
-            v[0] += xor_lane<O>(v[0], lane);
-            lane_reduce_hi<1, I + 1>(v, lane, base);
-        }
-    }
-}
-constexpr int red_hi_left(int H) { return H >= 16 ? H / 16 : 1; }
-
 // Lanes holding a total after lane_reduce_tail<H>: (lane & mask) == value.
 // Bits 4 and 8 reduced by row_shr must be set; bits reduced by a butterfly
 // must be clear (their lanes hold copies).
@@ -169,22 +132,6 @@ constexpr LaneSel red_tail_writer(int H) {
     LaneSel s{0, 0};
     for (int i = 0; i < 6; ++i) {
         const int o = red_bit(i);
-        if (H > 1) {
-            H /= 2;
-        } else {
-            s.mask |= o;
-            if (o == 4 || o == 8) s.value |= o;
-        }
-    }
-    return s;
-}
-
-// The same after lane_reduce_hi<H> (bits 0..1 are not reduced: every value
-// of them holds its own totals).
-constexpr LaneSel red_hi_writer(int H) {
-    LaneSel s{0, 0};
-    for (int i = 0; i < 4; ++i) {
-        const int o = red_bit_hi(i);
         if (H > 1) {
             H /= 2;
         } else {

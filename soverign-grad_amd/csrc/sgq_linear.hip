@@ -73,20 +73,19 @@ __device__ __forceinline__ float half_hi(uint32_t p) {
 }
 
 // One INT4 output summed in k order over rows [k0, k1) as code * (x * s)
-// (NORM: x * (gamma * s)), reading column n of the k-octet layout of KB k
-// blocks.  The GEMV falls back to this when its offset-corrected sum is not
-// finite (an infinite or NaN input, or an overflow), so that infinities and
-// NaNs come out as in the reference's x . (q * s) rather than as inf - inf;
-// the skinny MFMA kernel likewise over its K range.
+// (NORM: x * (gamma * s)), reading strip j of the strip-major layout, whose
+// dword k is row k.  The GEMV falls back to this when its offset-corrected
+// sum is not finite (an infinite or NaN input, or an overflow), so that
+// infinities and NaNs come out as in the reference's x . (q * s) rather than
+// as inf - inf; the skinny MFMA kernel likewise over its K range.
 template <bool NORM>
-__device__ float i4_column_exact(const void* W, const float* SC, int n, int spc, int Kpad, int KB,
+__device__ float i4_column_exact(const uint4* W, const float* SC, int j, int e, int spc, int Kpad, int RQ,
                                  const float* xrow, const float* gamma, int k0, int k1) {
-    const unsigned char* wb = reinterpret_cast<const unsigned char*>(W);
-    const float* sc = SC + (int64_t)((n >> 3) / spc) * Kpad;
+    const uint32_t* wd = reinterpret_cast<const uint32_t*>(W + (int64_t)j * RQ);
+    const float* sc = SC + (int64_t)(j / spc) * Kpad;
     float acc = 0.0f;
     for (int k = k0; k < k1; ++k) {
-        const uint32_t d = *reinterpret_cast<const uint32_t*>(wb + i4_dword_offset(n, k, KB));
-        const int q = ((int)(d << (28 - 4 * (k & 7)))) >> 28;
+        const int q = ((int)(wd[k] << (28 - 4 * e))) >> 28;
         const float s = NORM ? gamma[k] * sc[k] : sc[k];
         acc = fmaf((float)q, xrow[k] * s, acc);
     }
@@ -145,26 +144,6 @@ __device__ __forceinline__ float4 buf_load4f(__amdgpu_buffer_rsrc_t r, int voff,
     }
 }
 
-// Two floats at byte offset voff + soff (zero past the end).  AL: the buffer
-// holds an even number of floats from an 8-byte-aligned start, so a pair is
-// entirely in or out and one 64-bit load serves; otherwise two 32-bit loads.
-template <bool AL>
-__device__ __forceinline__ float2 buf_load2f(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    if (AL) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-        return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-    } else {
-        return make_float2(__uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 0, soff, 0)),
-                           __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff + 4, soff, 0)));
-    }
-}
-
-// v of lane J of this lane's quad (DPP quad_perm [J,J,J,J]).
-template <int J>
-__device__ __forceinline__ float quad_bcast(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), J * 0x55, 0xF, 0xF, false));
-}
-
 // silu(v) = v / (1 + exp(-v)), as simd::vec_silu (simd.hpp:103-108); the
 // device expf differs from libm's by at most a few ulp, the division is
 // correctly rounded.
@@ -197,8 +176,7 @@ struct GemvArgs {
     const uint4* W[3];
     const float* SC[3];
     const float* bias[3];
-    int mode, Kpad, RQ, NS;  // NS: strips of one weight (INT8 strips of 4 columns, INT4 of 8)
-    int KB, NB;              // INT4: k blocks of 32 rows, column blocks of 16
+    int mode, Kpad, RQ, NS;  // NS: strips of one weight
     const float* res;        // added to the output (same indexing), or null
     float* y;
     int ldy;                 // row stride of y and res
@@ -214,12 +192,13 @@ struct GemvArgs {
 };
 
 // ---------------------------------------------------------------------------
-// INT8 GEMV for M <= 8 rows per pass.  One workgroup of NW wavefronts per
-// strip (all K rows of 4 columns); scales[0] (per-tensor) or scales[k]
-// (per-row).  Thread t takes row quads rq = 64*NW*it + t, U of them in flight
-// at once.  The codes, the scales and x of one row quad all sit at byte 16*rq
-// of their buffers, so the loads share one lane offset and one SGPR
-// iteration offset.
+// GEMV / skinny GEMM for M <= 8 rows per pass.  One workgroup of NW
+// wavefronts per strip (all K rows of SW columns): BITS 4 -> 8 columns,
+// scales devscales[j / spc][k]; BITS 8 -> 4 columns, scales[0] (per-tensor)
+// or scales[k] (per-row).  Thread t takes row quads rq = 64*NW*it + t, U of
+// them in flight at once.  The codes, the
+// scales and x of one row quad all sit at byte 16*rq of their buffers, so the
+// four loads share one lane offset and one SGPR iteration offset.
 // ---------------------------------------------------------------------------
 //
 // NG == 2 is the gated MLP (SwiGLU::forward up to the down projection,
@@ -227,49 +206,94 @@ struct GemvArgs {
 // strip j of the gate weight and NW on strip j of the up weight -- x is read
 // by both groups from the same CU's caches -- and the epilogue writes
 // silu(gate + bias) * (up + bias2).
-template <int MT, int NW, int U, bool KALIGN4, int NG, bool STREAM>
+//
+// SPW > 1 strips per workgroup (adjacent strips j0 .. j0+SPW-1, which must
+// share their INT4 scale column: spc % SPW == 0) load each x and scale quad
+// once for all of them: fewer load instructions per code byte, which is what
+// bounds the single-row GEMV.
+//
+// With NG == 1, a.nw weights of equal shape may sit side by side along the
+// output (a LLaMA block's q, k and v projections of one input): workgroup
+// strips run over all of them and weight w writes columns w*N .. w*N+N-1 of
+// y.  a.res, when set, is added to every output (a residual connection).
+//
+// NORM: the input rows are first RMS-normalised (rms_norm, src/ops.cpp:
+// 1532-1556: x * inv_rms * gamma, inv_rms = 1 / sqrt(sum(x^2) / K + eps)).
+// inv_rms is one factor per row, so it comes out of the K sum: the workgroup
+// accumulates (x * gamma * s) * q and sum(x^2) of the x rows it reads anyway
+// (all of K), and multiplies by inv_rms in the epilogue.  No separate norm
+// launch and no normed copy of x.
+template <int BITS, int MT, int NW, int U, bool KALIGN4, int NG, int SPW, bool NORM, bool STREAM>
 __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
-    const int K = a.K, N = a.N, mode = a.mode, NS = a.NS;
-    constexpr int SW = 4;           // columns per strip
-    constexpr int RQ_IT = NW * 64;  // row quads per group iteration
-    constexpr int V = MT * SW;      // accumulators per lane
+    static_assert(NG == 1 || SPW == 1, "the gated form takes one strip of each weight");
+    const int K = a.K, N = a.N, mode = a.mode, Kpad = a.Kpad, RQ = a.RQ, NS = a.NS;
+    constexpr int SW = (BITS == 4) ? 8 : 4;  // columns per strip
+    constexpr int RQ_IT = NW * 64;           // row quads per group iteration
+    constexpr int CW = SPW * SW;             // columns per workgroup
+    constexpr int V = MT * CW;               // accumulators per lane
+    constexpr bool MIX = BITS == 4 && MT <= kGemvMixMaxRows;  // offset-binary fma_mix decode
     __shared__ float red[NG * NW][V];
+    __shared__ float sqr[NORM ? NG * NW : 1][MT];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
     const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
-    // Workgroup v covers row group p = v % P of strip v / P (P = 2^Plog): the
-    // row groups of one strip are neighbours in v, so they run on one XCD and
-    // the second read of the strip's codes hits its L2.  No integer division
-    // on the way to the first load: every index here is a shift, a mask or a
-    // grid coordinate.
+    // Strips of a scale column share an XCD's L2.  Workgroups of one weight
+    // cover (NS + SPW - 1) / SPW strip groups (x of the grid); with several
+    // weights side by side (NG == 1), y of the grid selects the weight.
+    // Workgroup v covers row group p = v % P of strip group v / P (P = 2^Plog):
+    // the row groups of one strip are neighbours in v, so they run on one XCD
+    // and the second read of the strip's codes hits its L2.  No integer
+    // division on the way to the first load: every index here is a shift, a
+    // mask or a grid coordinate (a runtime division costs about 30 dependent
+    // instructions, all of them ahead of the loads).
     const int vg = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
     const int prow = vg & ((1 << a.Plog) - 1);
-    const int j0 = vg >> a.Plog;
+    const int jg = vg >> a.Plog;
     const int m0 = prow * MT;
     const float* __restrict__ x = a.x + (int64_t)m0 * K;
     const int M = min(MT, a.M - m0);  // <= 0 for a padding group: no x rows, no outputs
-    const uint4* __restrict__ Wm = a.W[grp];
-    const float* __restrict__ SCm = a.SC[grp];
-    const float* __restrict__ bias = a.bias[0];
+    const int wt = NG == 1 ? (int)blockIdx.y : 0;
+    const int j0 = SPW * jg;
+    const int widx = NG == 1 ? wt : grp;
+    const uint4* __restrict__ Wm = widx == 0 ? a.W[0] : (widx == 1 ? a.W[1] : a.W[2]);
+    const float* __restrict__ SCm = widx == 0 ? a.SC[0] : (widx == 1 ? a.SC[1] : a.SC[2]);
+    const float* __restrict__ bias = NG == 1 ? (wt == 0 ? a.bias[0] : (wt == 1 ? a.bias[1] : a.bias[2])) : a.bias[0];
     const float* __restrict__ bias2 = a.bias[1];
     const int voff = gtid * 16;
 
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wm + (int64_t)(j0 < NS ? j0 : 0) * a.RQ, j0 < NS ? (uint32_t)a.RQ * 16u : 0u);
-    const __amdgpu_buffer_rsrc_t rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
-    const float s_all = mode ? SCm[0] : 0.0f;
+    __amdgpu_buffer_rsrc_t rW[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)  // a strip past the last reads zeros and is not stored
+        rW[s] = make_rsrc(Wm + (int64_t)(j0 + s < NS ? j0 + s : 0) * RQ, j0 + s < NS ? (uint32_t)RQ * 16u : 0u);
+    __amdgpu_buffer_rsrc_t rS;
+    float s_all = 0.0f;
+    if constexpr (BITS == 4) {
+        rS = make_rsrc(SCm + (int64_t)a.spc.div(j0) * Kpad, (uint32_t)Kpad * 4u);
+    } else {
+        rS = make_rsrc(SCm, mode ? 4u : (uint32_t)K * 4u);
+        if (mode) s_all = SCm[0];
+    }
     __amdgpu_buffer_rsrc_t rX[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) rX[m] = make_rsrc(x + (int64_t)m * K, m < M ? (uint32_t)K * 4u : 0u);
+
+    __amdgpu_buffer_rsrc_t rG;
+    if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
+    float sq[MT];  // NORM: sum of x^2 per row
+    float sx[MT];  // INT4: sum of xs per row (the offset correction)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) sq[m] = 0.0f, sx[m] = 0.0f;
 
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 
-    const int nit = (a.RQ + RQ_IT - 1) / RQ_IT;
+    const int nit = (RQ + RQ_IT - 1) / RQ_IT;
     for (int it0 = 0; it0 < nit; it0 += U) {
-        uint4 w[U];
+        uint4 w[U][SPW];
         float4 sv[U];
+        float4 gv[NORM ? U : 1];
         float4 xv[U][MT];  // x is loaded with the codes (measured 4-7% faster for M >= 4 than at use)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -277,33 +301,99 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
             // a partial last batch: a branch here would make the compiler wait
             // for every load before the first use instead of one batch entry at a time.
             const int soff = (it0 + u) * RQ_IT * 16;
-            w[u] = STREAM ? buf_load16_stream(rW, voff, soff) : buf_load16(rW, voff, soff);
-            if (!mode) sv[u] = buf_load4f<KALIGN4>(rS, voff, soff);
+#pragma unroll
+            for (int s = 0; s < SPW; ++s)
+                w[u][s] = STREAM ? buf_load16_stream(rW[s], voff, soff) : buf_load16(rW[s], voff, soff);
+            if constexpr (BITS == 4) {
+                sv[u] = buf_load4f<true>(rS, voff, soff);  // devscales rows are padded to 16
+            } else if (!mode) {
+                sv[u] = buf_load4f<KALIGN4>(rS, voff, soff);
+            }
 #pragma unroll
             for (int m = 0; m < MT; ++m) xv[u][m] = buf_load4f<KALIGN4>(rX[m], voff, soff);
+            if constexpr (NORM) gv[u] = buf_load4f<KALIGN4>(rG, voff, soff);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k0 = 4 * ((it0 + u) * RQ_IT) + 4 * gtid;
-            if (mode) {
-                // Rows past K must give exactly zero, also for a non-finite per-tensor scale.
-                sv[u].x = (k0 + 0 < K) ? s_all : 0.0f;
-                sv[u].y = (k0 + 1 < K) ? s_all : 0.0f;
-                sv[u].z = (k0 + 2 < K) ? s_all : 0.0f;
-                sv[u].w = (k0 + 3 < K) ? s_all : 0.0f;
+            if constexpr (BITS == 8) {
+                if (mode) {
+                    // Rows past K must give exactly zero, also for a non-finite per-tensor scale.
+                    sv[u].x = (k0 + 0 < K) ? s_all : 0.0f;
+                    sv[u].y = (k0 + 1 < K) ? s_all : 0.0f;
+                    sv[u].z = (k0 + 2 < K) ? s_all : 0.0f;
+                    sv[u].w = (k0 + 3 < K) ? s_all : 0.0f;
+                }
             }
-            const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
+                const float4 xm = xv[u][m];
                 float xs[4];
+                if constexpr (NORM) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) xs[r] = f4get(xv[u][m], r) * f4get(sv[u], r);
-                float* ac = acc + m * SW;
+                    for (int r = 0; r < 4; ++r) {
+                        sq[m] = fmaf(f4get(xm, r), f4get(xm, r), sq[m]);
+                        xs[r] = f4get(xm, r) * (f4get(gv[u], r) * f4get(sv[u], r));
+                    }
+                } else {
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+                    for (int r = 0; r < 4; ++r) xs[r] = f4get(xm, r) * f4get(sv[u], r);
+                }
+                if constexpr (MIX) sx[m] += (xs[0] + xs[1]) + (xs[2] + xs[3]);
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) ac[d] = fmaf(i8_byte(dw[d], r), xs[r], ac[d]);
+                for (int s = 0; s < SPW; ++s) {
+                    const uint32_t dw[4] = {w[u][s].x, w[u][s].y, w[u][s].z, w[u][s].w};
+                    float* a = acc + m * CW + s * SW;
+                    if constexpr (MIX) {
+                        // Nibble e (column e of the strip) as u * 2^-24 (even e) or
+                        // u * 2^-20 (odd e); the masks are shared by all rows m.
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t ob = dw[r] ^ 0x88888888u;
+                            const uint32_t p04 = ob & 0x000F000Fu, p15 = ob & 0x00F000F0u;
+                            const uint32_t ob8 = ob >> 8;
+                            const uint32_t p26 = ob8 & 0x000F000Fu, p37 = ob8 & 0x00F000F0u;
+                            a[0] = fmaf(half_lo(p04), xs[r], a[0]);
+                            a[4] = fmaf(half_hi(p04), xs[r], a[4]);
+                            a[1] = fmaf(half_lo(p15), xs[r], a[1]);
+                            a[5] = fmaf(half_hi(p15), xs[r], a[5]);
+                            a[2] = fmaf(half_lo(p26), xs[r], a[2]);
+                            a[6] = fmaf(half_hi(p26), xs[r], a[6]);
+                            a[3] = fmaf(half_lo(p37), xs[r], a[3]);
+                            a[7] = fmaf(half_hi(p37), xs[r], a[7]);
+                        }
+                    } else if constexpr (BITS == 4) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t hi = dw[r] & 0xF0F0F0F0u;         // columns 2b+1, as 16*q
+                            const uint32_t lo = (dw[r] << 4) & 0xF0F0F0F0u;  // columns 2b, as 16*q
+#pragma unroll
+                            for (int b = 0; b < 4; ++b) {
+                                a[2 * b] = fmaf(i8_byte(lo, b), xs[r], a[2 * b]);
+                                a[2 * b + 1] = fmaf(i8_byte(hi, b), xs[r], a[2 * b + 1]);
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+#pragma unroll
+                            for (int d = 0; d < 4; ++d) a[d] = fmaf(i8_byte(dw[d], r), xs[r], a[d]);
+                    }
+                }
             }
+        }
+    }
+
+    if constexpr (MIX) {
+        // Undo the scaling (exact) and the offset per lane: the reduction below
+        // is a plain sum, so correcting each lane's partial sums before it gives
+        // the corrected total with no second reduction for sum(xs).
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float off = -8.0f * sx[m];
+#pragma unroll
+            for (int c = 0; c < CW; ++c)
+                acc[m * CW + c] = fmaf(acc[m * CW + c], (c & 1) ? 1048576.0f : 16777216.0f, off);
         }
     }
 
@@ -316,226 +406,6 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv(const GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < left; ++i) red[wave][base + i] = acc[i];
     }
-    __syncthreads();
-
-    for (int v = threadIdx.x; v < V; v += NG * NW * 64) {
-        const int m = v / SW, e = v - m * SW;
-        const int n = j0 * SW + e;
-        if (m < M && n < N) {
-            const int64_t o = (int64_t)(m0 + m) * a.ldy + n;
-            float r = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) r += red[w][v];
-            if (bias) r = r + bias[n];
-            if constexpr (NG == 2) {
-                float r2 = 0.0f;
-#pragma unroll
-                for (int w = NW; w < 2 * NW; ++w) r2 += red[w][v];
-                if (bias2) r2 = r2 + bias2[n];
-                r = silu_f32(r) * r2;
-            }
-            a.y[o] = r;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// INT4 GEMV over the k-octet layout for M <= 8 rows per pass.  A workgroup
-// owns one column block (16 columns over all of K) of one weight and row
-// group; its NW wavefronts split K.  Lane t of the group reads the 16 bytes
-// at 16 t of each 1 KB step of the block's stream, so every wavefront load is
-// 1 KB contiguous: k block 4 * step + t / 16, k octet g = (t >> 2) & 3 and
-// columns 4 j .. 4 j + 3, j = t & 3 (four dwords, eight k each).  The four
-// lanes of a quad share those eight k: each loads two of them (x, the scale
-// and gamma), forms its two x * s and the quad exchanges them by DPP
-// broadcasts, so x and the scales cross the load path once per workgroup.
-// With SHS the block's two strips share their scale column (spc even);
-// otherwise each lane loads the eight scales of its own strip and the quad
-// exchanges x instead of x * s.
-//
-// The decode, the gated form (NG == 2), side-by-side weights (NG == 1,
-// blockIdx.y), the folded RMSNorm (NORM) and the residual are those of
-// k_gemv.  MIX (up to kGemvMixMaxRows rows): nibble i of a dword is row k0 + i,
-// so even and odd rows sit at different fp16 scales (u * 2^-24, u * 2^-20)
-// and accumulate separately; the totals are rescaled (exactly) and offset by
-// -8 * sum(x * s) before the lanes are combined.
-template <int MT, int NW, int U, bool XA, int NG, bool NORM, bool STREAM, bool SHS>
-__global__ __launch_bounds__(NG * NW * 64) void k_gemv4(const GemvArgs a) {
-    const int K = a.K, N = a.N, Kpad = a.Kpad, KB = a.KB;
-    constexpr bool MIX = MT <= kGemvMixMaxRows;
-    constexpr int V = 4 * MT;  // totals per lane: 4 columns x MT rows, index m * 4 + d
-    __shared__ float red[NG * NW][4][V];
-    __shared__ float sqr[NORM ? NG * NW : 1][MT];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / NW);  // weight matrix of this wave
-    const int gtid = threadIdx.x - grp * (NW * 64);                           // thread index within its group
-    const int jq = lane & 3;
-    // Row groups of one column block are neighbours in v (one XCD, so the
-    // second read of the block's codes hits its L2); no integer division
-    // ahead of the first load.
-    const int vg = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
-    const int prow = vg & ((1 << a.Plog) - 1);
-    const int cb = vg >> a.Plog;
-    const int m0 = prow * MT;
-    const float* __restrict__ x = a.x + (int64_t)m0 * K;
-    const int M = min(MT, a.M - m0);  // <= 0 for a padding group: no x rows, no outputs
-    const int wt = NG == 1 ? (int)blockIdx.y : 0;
-    const int widx = NG == 1 ? wt : grp;
-    const uint4* __restrict__ Wm = widx == 0 ? a.W[0] : (widx == 1 ? a.W[1] : a.W[2]);
-    const float* __restrict__ SCm = widx == 0 ? a.SC[0] : (widx == 1 ? a.SC[1] : a.SC[2]);
-    const float* __restrict__ bias = NG == 1 ? (wt == 0 ? a.bias[0] : (wt == 1 ? a.bias[1] : a.bias[2])) : a.bias[0];
-    const float* __restrict__ bias2 = a.bias[1];
-
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(Wm + (int64_t)cb * KB * 16, cb < a.NB ? (uint32_t)KB * 256u : 0u);
-    const int strip = 2 * cb + (SHS ? 0 : (jq >> 1));
-    const __amdgpu_buffer_rsrc_t rS = make_rsrc(SCm + (int64_t)a.spc.div(strip) * Kpad,
-                                                strip < a.NS ? (uint32_t)Kpad * 4u : 0u);
-    __amdgpu_buffer_rsrc_t rX[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) rX[m] = make_rsrc(x + (int64_t)m * K, m < M ? (uint32_t)K * 4u : 0u);
-    __amdgpu_buffer_rsrc_t rG;
-    if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
-    const int voff = gtid * 16;             // codes
-    const int xoff = gtid * 8;              // this lane's pair of k: 2 t, 2 t + 1 of the step's 128 NW
-    const int soff8 = (gtid >> 2) * 32;     // !SHS: the quad's eight k
-
-    float sq[MT];  // NORM: sum of x^2 per row over this lane's pairs
-    float sx[MT];  // MIX: sum of x * s per row (the offset correction)
-    float acc[MIX ? 2 * V : V];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) sq[m] = 0.0f, sx[m] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < (MIX ? 2 * V : V); ++i) acc[i] = 0.0f;
-
-    const int nit = (KB + 4 * NW - 1) / (4 * NW);
-    for (int it0 = 0; it0 < nit; it0 += U) {
-        uint4 w[U];
-        float2 xv[U][MT];
-        float2 sv[U];
-        float4 s8[SHS ? 1 : U][2];
-        float2 gv[NORM ? U : 1];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            // Steps past the stream read zeros (buffer ranges); no guard, so
-            // that each use waits for its own loads only.
-            const int sw = (it0 + u) * NW * 1024, sxo = (it0 + u) * NW * 512;
-            w[u] = STREAM ? buf_load16_stream(rW, voff, sw) : buf_load16(rW, voff, sw);
-            if constexpr (SHS) {
-                sv[u] = buf_load2f<true>(rS, xoff, sxo);  // devscales rows: Kpad floats, 16-byte aligned
-            } else {
-                s8[u][0] = buf_load4f<true>(rS, soff8, sxo);
-                s8[u][1] = buf_load4f<true>(rS, soff8 + 16, sxo);
-            }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) xv[u][m] = buf_load2f<XA>(rX[m], xoff, sxo);
-            if constexpr (NORM) gv[u] = buf_load2f<XA>(rG, xoff, sxo);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-            // Per dword d: the masks of the decode, shared by every row.
-            uint32_t p04[4], p15[4], p26[4], p37[4], lo[4], hi[4];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                if constexpr (MIX) {
-                    const uint32_t ob = dw[d] ^ 0x88888888u, ob8 = ob >> 8;
-                    p04[d] = ob & 0x000F000Fu, p15[d] = ob & 0x00F000F0u;
-                    p26[d] = ob8 & 0x000F000Fu, p37[d] = ob8 & 0x00F000F0u;
-                } else {
-                    lo[d] = (dw[d] << 4) & 0xF0F0F0F0u;  // byte b: row 2b, as 16 q
-                    hi[d] = dw[d] & 0xF0F0F0F0u;         // byte b: row 2b + 1
-                }
-            }
-            float q16[MIX ? 1 : 4][8];  // one convert per code, shared by the rows
-            if constexpr (!MIX) {
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        q16[d][2 * b] = i8_byte(lo[d], b);
-                        q16[d][2 * b + 1] = i8_byte(hi[d], b);
-                    }
-            }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                float xs[8];
-                if constexpr (SHS) {
-                    float p0, p1;
-                    if constexpr (NORM) {
-                        sq[m] = fmaf(xv[u][m].x, xv[u][m].x, sq[m]);
-                        sq[m] = fmaf(xv[u][m].y, xv[u][m].y, sq[m]);
-                        p0 = xv[u][m].x * (gv[u].x * sv[u].x);
-                        p1 = xv[u][m].y * (gv[u].y * sv[u].y);
-                    } else {
-                        p0 = xv[u][m].x * sv[u].x;
-                        p1 = xv[u][m].y * sv[u].y;
-                    }
-                    xs[0] = quad_bcast<0>(p0), xs[1] = quad_bcast<0>(p1);
-                    xs[2] = quad_bcast<1>(p0), xs[3] = quad_bcast<1>(p1);
-                    xs[4] = quad_bcast<2>(p0), xs[5] = quad_bcast<2>(p1);
-                    xs[6] = quad_bcast<3>(p0), xs[7] = quad_bcast<3>(p1);
-                } else {
-                    float xx[8], gg[8];
-                    xx[0] = quad_bcast<0>(xv[u][m].x), xx[1] = quad_bcast<0>(xv[u][m].y);
-                    xx[2] = quad_bcast<1>(xv[u][m].x), xx[3] = quad_bcast<1>(xv[u][m].y);
-                    xx[4] = quad_bcast<2>(xv[u][m].x), xx[5] = quad_bcast<2>(xv[u][m].y);
-                    xx[6] = quad_bcast<3>(xv[u][m].x), xx[7] = quad_bcast<3>(xv[u][m].y);
-                    if constexpr (NORM) {
-                        sq[m] = fmaf(xv[u][m].x, xv[u][m].x, sq[m]);
-                        sq[m] = fmaf(xv[u][m].y, xv[u][m].y, sq[m]);
-                        gg[0] = quad_bcast<0>(gv[u].x), gg[1] = quad_bcast<0>(gv[u].y);
-                        gg[2] = quad_bcast<1>(gv[u].x), gg[3] = quad_bcast<1>(gv[u].y);
-                        gg[4] = quad_bcast<2>(gv[u].x), gg[5] = quad_bcast<2>(gv[u].y);
-                        gg[6] = quad_bcast<3>(gv[u].x), gg[7] = quad_bcast<3>(gv[u].y);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float si = f4get(s8[u][i >> 2], i & 3);
-                        xs[i] = NORM ? xx[i] * (gg[i] * si) : xx[i] * si;
-                    }
-                }
-                if constexpr (MIX) sx[m] += ((xs[0] + xs[1]) + (xs[2] + xs[3])) + ((xs[4] + xs[5]) + (xs[6] + xs[7]));
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    float* ae = acc + m * 4 + d;
-                    if constexpr (MIX) {
-                        float* ao = ae + V;
-                        *ae = fmaf(half_lo(p04[d]), xs[0], *ae);
-                        *ae = fmaf(half_hi(p04[d]), xs[4], *ae);
-                        *ae = fmaf(half_lo(p26[d]), xs[2], *ae);
-                        *ae = fmaf(half_hi(p26[d]), xs[6], *ae);
-                        *ao = fmaf(half_lo(p15[d]), xs[1], *ao);
-                        *ao = fmaf(half_hi(p15[d]), xs[5], *ao);
-                        *ao = fmaf(half_lo(p37[d]), xs[3], *ao);
-                        *ao = fmaf(half_hi(p37[d]), xs[7], *ao);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) *ae = fmaf(q16[MIX ? 0 : d][i], xs[i], *ae);
-                    }
-                }
-            }
-        }
-    }
-
-    // MIX: even rows at 2^-24, odd at 2^-20 (exact rescaling) and the
-    // offset -8 * sum(x * s) of this lane's rows, before the lane sums.
-    float v[V];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const int i = m * 4 + d;
-            v[i] = MIX ? fmaf(acc[i], 16777216.0f, fmaf(acc[V + i], 1048576.0f, -8.0f * sx[m])) : acc[i];
-        }
-    int base = 0;
-    lane_reduce_hi<V, 0>(v, lane, base);
-    constexpr int left = red_hi_left(V);
-    constexpr LaneSel wsel = red_hi_writer(V);
-    if ((lane & wsel.mask) == wsel.value) {
-#pragma unroll
-        for (int i = 0; i < left; ++i) red[wave][jq][base + i] = v[i];
-    }
     if constexpr (NORM) {
         int sbase = 0;
         lane_reduce<MT, 0>(sq, lane, sbase);
@@ -546,16 +416,17 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv4(const GemvArgs a) {
     }
     __syncthreads();
 
-    // Output o = 16 m + c of the block: column 16 cb + c, row m0 + m.
-    for (int o = threadIdx.x; o < 16 * MT; o += NG * NW * 64) {
-        const int m = o >> 4, c = o & 15;
-        const int n = cb * 16 + c;
+    // MIX: a non-finite total (an infinite or NaN input, or an overflow) takes
+    // the exact k-order sum instead.  INT4 without MIX read its codes as
+    // 16 * q: scale by 1/16 (exact).
+    for (int v = threadIdx.x; v < V; v += NG * NW * 64) {
+        const int m = v / CW, e = v - m * CW;
+        const int n = j0 * SW + e;
         if (m < M && n < N) {
-            const int64_t oi = (int64_t)(m0 + m) * a.ldy + (int64_t)wt * N + n;
-            const int ri = m * 4 + (c & 3);
+            const int64_t o = (int64_t)(m0 + m) * a.ldy + (int64_t)wt * N + n;
             float r = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) r += red[w][c >> 2][ri];
+            for (int w = 0; w < NW; ++w) r += red[w][v];
             float inv = 1.0f;
             if constexpr (NORM) {  // every group read all of x: group 0's waves hold the full sum
                 float ss = 0.0f;
@@ -565,25 +436,26 @@ __global__ __launch_bounds__(NG * NW * 64) void k_gemv4(const GemvArgs a) {
             }
             auto i4_total = [&](float t, const uint4* Wg, const float* SCg) {
                 if (!isfinite(t))
-                    t = i4_column_exact<NORM>(Wg, SCg, n, a.mode, Kpad, KB, a.x + (int64_t)(m0 + m) * K, a.gamma, 0, K);
+                    t = i4_column_exact<NORM>(Wg, SCg, j0 + e / SW, e % SW, mode, Kpad, RQ,
+                                              a.x + (int64_t)(m0 + m) * K, a.gamma, 0, K);
                 return t;
             };
             if constexpr (MIX) r = i4_total(r, NG == 1 ? Wm : a.W[0], NG == 1 ? SCm : a.SC[0]);
-            if constexpr (!MIX) r = r * 0.0625f;
+            if constexpr (BITS == 4 && !MIX) r = r * 0.0625f;
             if constexpr (NORM) r = r * inv;
             if (bias) r = r + bias[n];
             if constexpr (NG == 2) {
                 float r2 = 0.0f;
 #pragma unroll
-                for (int w = NW; w < 2 * NW; ++w) r2 += red[w][c >> 2][ri];
+                for (int w = NW; w < 2 * NW; ++w) r2 += red[w][v];
                 if constexpr (MIX) r2 = i4_total(r2, a.W[1], a.SC[1]);
-                if constexpr (!MIX) r2 = r2 * 0.0625f;
+                if constexpr (BITS == 4 && !MIX) r2 = r2 * 0.0625f;
                 if constexpr (NORM) r2 = r2 * inv;
                 if (bias2) r2 = r2 + bias2[n];
                 r = silu_f32(r) * r2;
             }
-            if (a.res) r = r + a.res[oi];
-            a.y[oi] = r;
+            if (a.res) r = r + a.res[o];
+            a.y[o] = r;
         }
     }
 }
@@ -661,15 +533,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     // Buffer resources over this tile's rows of x and strips of W: rows past
     // M and strips past NS read as zero; k past K and row quads past RQ (which
     // would read the next row or strip) get an out-of-range lane offset.
-    // INT8: strips of the strip-major layout.  INT4: column blocks of the
-    // k-octet layout (RQ is then its k blocks per column block).
     const int mrows = (M - m0) < kBM ? (M - m0) : kBM;
     const int nstr = (NS - n0 / SW) < kStrips ? (NS - n0 / SW) : kStrips;
-    const int nblk = ((NS + 1) / 2 - n0 / 16) < (kBN / 16) ? ((NS + 1) / 2 - n0 / 16) : (kBN / 16);
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
-    const __amdgpu_buffer_rsrc_t rW =
-        BITS == 8 ? make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u)
-                  : make_rsrc(W + (int64_t)(n0 / 16) * RQ * 16, (uint32_t)nblk * (uint32_t)RQ * 256u);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
     auto load = [&](Regs& rg, int kt) {
         const int soffA = kt * kBK * 4, soffB = kt * KQ * 16;
 #pragma unroll
@@ -692,15 +559,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int i = 0; i < kBPer; ++i) {
             const int t = tid + kThreads * i;
-            if constexpr (BITS == 8) {
-                const int rq = kt * KQ + t % KQ;
-                const int vo = ((t / KQ) * RQ + t % KQ) * 16;
-                rg.b[i] = buf_load16(rW, (t < kBChunks && rq < RQ) ? vo : kOobOff, soffB);
-            } else {
-                // piece t of the stage: column block t / 16 of the tile, 16 bytes t % 16 of its k block
-                const int vo = (t >> 4) * RQ * 256 + (t & 15) * 16;
-                rg.b[i] = buf_load16(rW, (t < kBChunks && kt < RQ) ? vo : kOobOff, kt * 256);
-            }
+            const int rq = kt * KQ + t % KQ;
+            const int vo = ((t / KQ) * RQ + t % KQ) * 16;
+            rg.b[i] = buf_load16(rW, (t < kBChunks && rq < RQ) ? vo : kOobOff, soffB);
         }
         // Every A float4 of this thread sits at column quad tid % KQ of the stage.
         if constexpr (BITS == 8)
@@ -743,30 +604,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                 (void)k;
                 Bq[buf][jl][kl / 4] = rg.b[i];
             } else {
-                // Piece t: columns c0 .. c0 + 3 of column block bl (one strip,
-                // so one scale column), rows k8 .. k8 + 7 of the stage, dword d
-                // = column c0 + d.  devscales rows stop at Kpad (codes there
-                // are zero); the 1/16 turns the 16*q read of a nibble back
-                // into q (exact).
-                (void)jl;
-                (void)k;
-                static_assert(BITS == 8 || kBK == 32, "an INT4 stage is one k block");
-                const int bl = t >> 4, gq = (t >> 2) & 3, c0 = 4 * (t & 3), k8 = 8 * gq;
-                const int bj = (n0 + bl * 16 + c0) >> 3;
+                const int bj = n0 / SW + jl;
                 const int jc = bj < NS ? bj : NS - 1;
-                const int so = kt * kBK + k8 < Kpad ? ((jc / mode) * Kpad + k8) * 4 : kOobOff;
-                const float4 s0 = buf_load4f<true>(rS, so, kt * kBK * 4), s1 = buf_load4f<true>(rS, so + 16, kt * kBK * 4);
-                const float sc[8] = {s0.x * 0.0625f, s0.y * 0.0625f, s0.z * 0.0625f, s0.w * 0.0625f,
-                                     s1.x * 0.0625f, s1.y * 0.0625f, s1.z * 0.0625f, s1.w * 0.0625f};
+                // devscales rows stop at Kpad (codes there are zero); the
+                // 1/16 turns the 16*q read of a high nibble back into q (exact)
+                const float4 s4 = buf_load4f<true>(rS, k < Kpad ? ((jc / mode) * Kpad + kl) * 4 : kOobOff,
+                                                   kt * kBK * 4);
+                const float sc[4] = {s4.x * 0.0625f, s4.y * 0.0625f, s4.z * 0.0625f, s4.w * 0.0625f};
+                uint32_t lo[4], hi[4];
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint32_t lo = (dw[d] << 4) & 0xF0F0F0F0u;  // byte b: row 2b, as 16 q
-                    const uint32_t hi = dw[d] & 0xF0F0F0F0u;         // byte b: row 2b + 1
-                    float* row = &Bs[buf][bl * 16 + c0 + d][k8];
-                    *(float4*)row = make_float4(i8_byte(lo, 0) * sc[0], i8_byte(hi, 0) * sc[1], i8_byte(lo, 1) * sc[2],
-                                                i8_byte(hi, 1) * sc[3]);
-                    *(float4*)(row + 4) = make_float4(i8_byte(lo, 2) * sc[4], i8_byte(hi, 2) * sc[5],
-                                                      i8_byte(lo, 3) * sc[6], i8_byte(hi, 3) * sc[7]);
+                for (int r = 0; r < 4; ++r) {
+                    hi[r] = dw[r] & 0xF0F0F0F0u;         // byte c: column 2c+1 of row r, as 16*q
+                    lo[r] = (dw[r] << 4) & 0xF0F0F0F0u;  // byte c: column 2c
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    *(float4*)&Bs[buf][jl * 8 + 2 * c][kl] =
+                        make_float4(i8_byte(lo[0], c) * sc[0], i8_byte(lo[1], c) * sc[1], i8_byte(lo[2], c) * sc[2],
+                                    i8_byte(lo[3], c) * sc[3]);
+                    *(float4*)&Bs[buf][jl * 8 + 2 * c + 1][kl] =
+                        make_float4(i8_byte(hi[0], c) * sc[0], i8_byte(hi[1], c) * sc[1], i8_byte(hi[2], c) * sc[2],
+                                    i8_byte(hi[3], c) * sc[3]);
                 }
             }
         }
@@ -923,19 +781,8 @@ __device__ __forceinline__ void split3_4(const float* v, uint2& h, uint2& m, uin
     l = make_uint2(pl[0], pl[1]);
 }
 
-// Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
-// operand: high nibbles masked in place and low nibbles shifted up read as
-// signed bytes 16q, converted exactly.
-__device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
-    const uint32_t hi = t & 0xF0F0F0F0u, lo = (t << 4) & 0xF0F0F0F0u;
-    const uint4 b = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<0>(hi)), pack_hi16(cvt_sbyte<1>(lo), cvt_sbyte<1>(hi)),
-                               pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<2>(hi)), pack_hi16(cvt_sbyte<3>(lo), cvt_sbyte<3>(hi)));
-    return __builtin_bit_cast(bf16x8, b);
-}
-
 // One output of the forward as the reference forms it: sum over k in
 // [k0, k1) of x[k] * (q[k][n] * s), in k order (the non-finite fallback).
-// RQ: INT8 row quads per strip; INT4 k blocks per column block.
 template <int BITS>
 __device__ float output_exact(const float* xrow, const uint4* W, const float* S, int mode, int Kpad, int RQ, int n,
                               int k0, int k1) {
@@ -946,10 +793,9 @@ __device__ float output_exact(const float* xrow, const uint4* W, const float* S,
             q = (float)reinterpret_cast<const signed char*>(W)[((int64_t)(n >> 2) * RQ + (k >> 2)) * 16 + (n & 3) * 4 +
                                                                 (k & 3)];
             s = mode ? S[0] : S[k];
-        } else {  // RQ: the INT4 layout's k blocks per column block
-            const uint32_t d = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const unsigned char*>(W) +
-                                                                  i4_dword_offset(n, k, RQ));
-            q = (float)(((int)(d << (28 - 4 * (k & 7)))) >> 28);
+        } else {
+            const uint32_t d = reinterpret_cast<const uint32_t*>(W + (int64_t)(n >> 3) * RQ)[k];
+            q = (float)(((int)(d << (28 - 4 * (n & 7)))) >> 28);
             s = S[(int64_t)((n >> 3) / mode) * Kpad + k];
         }
         acc = fmaf(xrow[k], q * s, acc);
@@ -1036,22 +882,17 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         rS = make_rsrc(S, PT ? 4u : (uint32_t)K * 4u);
     else
         rS = make_rsrc(S + (int64_t)((n0 / SW) / mode) * Kpad, (uint32_t)K * 4u);
-    // B side: an entry holds the eight k of its k group for one column.
-    // INT8: the column's dword of the two chunks (strip, row quads 2 * kg and
-    // 2 * kg + 1) that hold them; strips past NS read as zero.  INT4: one
-    // dword of the k-octet layout (RQ is then its k blocks per column block),
-    // the tile's BN / 16 column blocks contiguous; blocks past the last read
-    // as zero.
+    // B side: an entry holds the eight k of its k group for one column, read
+    // from the two chunks (strip, row quads 2 * kg and 2 * kg + 1) that hold
+    // them: INT8 the column's dword of each chunk, INT4 the whole chunks (a
+    // nibble of every dword).  Strips past NS read as zero.
     const int nstr = (NS - n0 / SW) < (BN / SW) ? (NS - n0 / SW) : (BN / SW);
-    const int nblk = ((NS + 1) / 2 - n0 / 16) < (BN / 16) ? ((NS + 1) / 2 - n0 / 16) : (BN / 16);
-    const __amdgpu_buffer_rsrc_t rW =
-        BITS == 8 ? make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u)
-                  : make_rsrc(W + (int64_t)(n0 / 16) * RQ * 16, (uint32_t)nblk * (uint32_t)RQ * 256u);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
 
     struct Regs {
         float4 a[EA][2];                      // [entry][quad]
         float4 s[2];                          // scales of the thread's eight k
-        uint4 b[EB];                          // [entry]: INT8 {lo, hi} dwords in .x/.y, INT4 the dword in .x
+        uint4 b[EB][BITS == 8 ? 1 : 2];       // [entry]: INT8 {lo, hi} dwords in .x/.y, INT4 the two chunks
     };
     auto load = [&](Regs& rg, int kt) {
         const int kb = kt * kB3BK + akg * 8;
@@ -1076,18 +917,20 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 #pragma unroll
             for (int q = 0; q < 2; ++q) rg.s[q] = buf_load4f<KALIGN4>(rS, (akg * 8 + 4 * q) * 4, soff);
         }
+        // RQ is a multiple of 4, so both row quads of the pair are in or out together.
+        const bool in = kt * kB3RQ + 2 * akg < RQ;
+        const int bsoff = kt * kB3RQ * 16;
 #pragma unroll
         for (int c = 0; c < EB; ++c) {
             const int n = ar + kStep * c;
+            const int vo = ((n / SW) * RQ + 2 * akg) * 16;
             if constexpr (BITS == 8) {
-                // RQ is a multiple of 4, so both row quads of the pair are in or out together.
-                const bool in = kt * kB3RQ + 2 * akg < RQ;
-                const int vd = ((n / SW) * RQ + 2 * akg) * 16 + (n & 3) * 4;
-                rg.b[c].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, kt * kB3RQ * 16, 0);
-                rg.b[c].y = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd + 16 : kOobOff, kt * kB3RQ * 16, 0);
+                const int vd = vo + (n & 3) * 4;
+                rg.b[c][0].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, bsoff, 0);
+                rg.b[c][0].y = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd + 16 : kOobOff, bsoff, 0);
             } else {
-                const int vd = (n >> 4) * RQ * 256 + (akg * 16 + (n & 15)) * 4;
-                rg.b[c].x = __builtin_amdgcn_raw_buffer_load_b32(rW, kt < RQ ? vd : kOobOff, kt * 256, 0);
+                rg.b[c][0] = buf_load16(rW, in ? vo : kOobOff, bsoff);
+                rg.b[c][1] = buf_load16(rW, in ? vo + 16 : kOobOff, bsoff);
             }
         }
     };
@@ -1103,17 +946,22 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         }
 #pragma unroll
         for (int c = 0; c < EB; ++c) {
+            float f[8];
             if constexpr (BITS == 8) {
                 // bytes of the column's dword in each chunk: k = 0..3, then 4..7
-                const uint32_t lo = rg.b[c].x, hi = rg.b[c].y;
-                Bs[buf][akg][ar + kStep * c] =
-                    make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<1>(lo)), pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<3>(lo)),
-                               pack_hi16(cvt_sbyte<0>(hi), cvt_sbyte<1>(hi)), pack_hi16(cvt_sbyte<2>(hi), cvt_sbyte<3>(hi)));
+                const uint32_t lo = rg.b[c][0].x, hi = rg.b[c][0].y;
+                f[0] = cvt_sbyte<0>(lo), f[1] = cvt_sbyte<1>(lo), f[2] = cvt_sbyte<2>(lo), f[3] = cvt_sbyte<3>(lo);
+                f[4] = cvt_sbyte<0>(hi), f[5] = cvt_sbyte<1>(hi), f[6] = cvt_sbyte<2>(hi), f[7] = cvt_sbyte<3>(hi);
             } else {
-                // the eight k of the entry are the dword's nibbles, as 16 q
-                // (the epilogue's exact 1/16 undoes the factor)
-                Bs[buf][akg][ar + kStep * c] = __builtin_bit_cast(uint4, nibbles_bf16x16(rg.b[c].x));
+                // dword r of a chunk is row r of it; nibble e the column
+                const int sh = 28 - 4 * ((ar + kStep * c) & 7);
+                const uint32_t dw[8] = {rg.b[c][0].x, rg.b[c][0].y, rg.b[c][0].z, rg.b[c][0].w,
+                                        rg.b[c][1].x, rg.b[c][1].y, rg.b[c][1].z, rg.b[c][1].w};
+#pragma unroll
+                for (int r = 0; r < 8; ++r) f[r] = (float)(((int)(dw[r] << sh)) >> 28);
             }
+            Bs[buf][akg][ar + kStep * c] = make_uint4(pack_hi16(f[0], f[1]), pack_hi16(f[2], f[3]),
+                                                       pack_hi16(f[4], f[5]), pack_hi16(f[6], f[7]));
         }
     };
 
@@ -1189,7 +1037,7 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 16 * RB + i * 16 + lkg * 4 + r;
                 if (m < M) {
-                    float v = PT ? acc[i][j][r] * s_all : (BITS == 4 ? acc[i][j][r] * 0.0625f : acc[i][j][r]);
+                    float v = PT ? acc[i][j][r] * s_all : acc[i][j][r];
                     if (!isfinite(v)) v = output_exact<BITS>(x + (int64_t)m * K, W, S, mode, Kpad, RQ, n, klo, khi);
                     out[(int64_t)m * N + n] = (bias && KS == 1) ? v + bv : v;
                 }
@@ -1213,17 +1061,63 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 // order of every sum depends on the K range and NW only, not on C, MB or the
 // number of weights.
 //
-// B operand straight from the k-octet layout, without LDS or any exchange
-// between lanes: block (column block, k block) is the MFMA's B tile, dword
-// 16 g + c = rows 8g .. 8g + 7 of column c, which is exactly what lane
-// 16 g + c supplies.  Each lane loads one dword per column block and k block
-// (a wavefront reads the 256-byte block), and converts its eight nibbles to
-// the bf16 values 16 q.  The codes are read once.
+// B operand straight from the strip layout, without LDS: a 32-row k block of
+// a strip is 128 bytes, dword r = row r's eight nibbles.  Lane l of a 16-lane
+// row takes column e = (l & 3) | (l & 8) >> 1 of strip j = (l >> 2) & 1 and,
+// in lane group g = l >> 4, rows 8g .. 8g+7.  Each lane loads one dword (row
+// 8g + e of its strip, all eight columns); an 8x8 nibble transpose across the
+// eight lanes of (g, j) leaves it with rows 8g .. 8g+7 of column e, which is
+// its B operand.  The codes are read once, in 256-byte runs per wavefront.
 // ---------------------------------------------------------------------------
 
-// The value of lane n ^ 8 within a 16-lane row (DPP row_ror:8): the half-row
-// forms complete an A operand with it.
+// Exchanges within the eight lanes of a transpose group: lane bits 0 and 1
+// are group bits 0 and 1 (DPP quad_perm), lane bit 3 is group bit 2 (DPP
+// row_ror:8 within a 16-lane row).
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); }
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true); }
 __device__ __forceinline__ uint32_t dpp_xor8(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); }
+__device__ __forceinline__ uint32_t rotr32(uint32_t v, uint32_t s) { return __builtin_amdgcn_alignbit(v, v, s); }
+
+// Per-lane constants of the transpose for group lane e.  Step d (4, 2, 1
+// nibbles): the lane keeps its nibbles whose index has bit d equal to its own
+// bit d and takes the other half from its partner (e ^ d), rotated by 4d bits
+// so that partner nibble c lands on c ^ d.
+struct NibbleT {
+    uint32_t keep4, keep2, keep1, rot2, rot1;
+};
+__device__ __forceinline__ NibbleT nibble_t(int e) {
+    NibbleT t;
+    t.keep4 = (e & 4) ? 0xFFFF0000u : 0x0000FFFFu;
+    t.keep2 = (e & 2) ? 0xFF00FF00u : 0x00FF00FFu;
+    t.keep1 = (e & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    t.rot2 = (e & 2) ? 8u : 24u;  // right by 8, or left by 8
+    t.rot1 = (e & 1) ? 4u : 28u;
+    return t;
+}
+// keep ? a : b, bit by bit, as one v_bitop3_b32: the truth table indexes
+// (a, b, keep) as (0xF0, 0xCC, 0xAA), so (0xF0 & 0xAA) | (0xCC & ~0xAA) =
+// 0xE4.  The compiler writes the and/or form as two or three instructions.
+__device__ __forceinline__ uint32_t bit_select(uint32_t a, uint32_t b, uint32_t keep) {
+    return __builtin_amdgcn_bitop3_b32(a, b, keep, 0xE4);
+}
+// On entry nibble c of lane e is T[e][c]; on return nibble r is T[r][e].
+// Three instructions per step: the DPP exchange, a rotate, a bit select.
+__device__ __forceinline__ uint32_t nibble_transpose8(uint32_t w, const NibbleT& t) {
+    w = bit_select(w, rotr32(dpp_xor8(w), 16u), t.keep4);
+    w = bit_select(w, rotr32(dpp_xor2(w), t.rot2), t.keep2);
+    w = bit_select(w, rotr32(dpp_xor1(w), t.rot1), t.keep1);
+    return w;
+}
+
+// Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
+// operand: high nibbles masked in place and low nibbles shifted up read as
+// signed bytes 16q, converted exactly.
+__device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
+    const uint32_t hi = t & 0xF0F0F0F0u, lo = (t << 4) & 0xF0F0F0F0u;
+    const uint4 b = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<0>(hi)), pack_hi16(cvt_sbyte<1>(lo), cvt_sbyte<1>(hi)),
+                               pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<2>(hi)), pack_hi16(cvt_sbyte<3>(lo), cvt_sbyte<3>(hi)));
+    return __builtin_bit_cast(bf16x8, b);
+}
 
 struct SkinnyArgs {
     const float* x;  // [M, K]
@@ -1231,7 +1125,7 @@ struct SkinnyArgs {
     const uint4* W[3];  // NG weights of equal shape (gate, up), or (NG == 1) nw weights side by side
     const float* SC[3];
     const float* bias[3];
-    int spc, Kpad, KB;  // KB: k blocks of 32 rows (the INT4 layout's block stream per column block)
+    int spc, Kpad, RQ;
     FastDiv wpc;  // workgroups (column groups) per scale column
     float* y;     // [M, ldy]
     float* part;  // split K: [NG][2^slog][M][N] partial sums
@@ -1273,6 +1167,7 @@ template <int NW, int U, int C, int NG, bool XA, bool NORM, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
+    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int K = a.K;
     const int vv = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
     const int wt = NG == 1 ? a.wgd.div(vv) : 0;  // weight of the side-by-side set
@@ -1289,7 +1184,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     __amdgpu_buffer_rsrc_t rW[NG], rS[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        rW[q] = make_rsrc(Wq[q] + (int64_t)blk0 * a.KB * 16, (uint32_t)C * (uint32_t)a.KB * 256u);
+        rW[q] = make_rsrc(Wq[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
         rS[q] = make_rsrc(SCq[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
     }
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
@@ -1298,11 +1193,12 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     float sq = 0.0f;  // NORM: sum of x^2 of this lane's row over its k
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = c * a.KB * 256 + 4 * lane;
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + 32 * g + 4 * e;
     constexpr int XV = HALF ? 4 : 8;  // x values per lane and k block
     const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
     const bool row_live = xr < a.M;
     const int xrow = xr * K * 4;
+    const NibbleT tp = nibble_t(e);
     floatx4 acc[NG][C];
 #pragma unroll
     for (int q = 0; q < NG; ++q)
@@ -1310,8 +1206,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
         for (int c = 0; c < C; ++c) acc[q][c] = floatx4{0.f, 0.f, 0.f, 0.f};
     const int nkb = (a.Kpad + 31) >> 5;
     // K blocks kb0, kb0 + NW, ..., U of them per batch.  A block past the end
-    // reads x, the scales and its codes as zeros (buffer ranges), so partial
-    // batches need no branch.
+    // reads x and the scales as zeros (its code dwords are whatever follows
+    // and are multiplied by zero), so partial batches need no branch.
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][NG][C];
         float xv[U][XV], sv[U][NG][XV], gv[NORM ? U : 1][XV];
@@ -1322,7 +1218,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
             for (int q = 0; q < NG; ++q)
 #pragma unroll
                 for (int c = 0; c < C; ++c)
-                    w[u][q][c] = buf_load4_stream(rW[q], kb < a.KB ? wv[c] : kOobOff, kb * 256);
+                    w[u][q][c] = buf_load4_stream(rW[q], wv[c], kb * 128);
             const int k0 = kb * 32 + 8 * g + xk;
 #pragma unroll
             for (int h = 0; h < XV / 4; ++h) {
@@ -1373,7 +1269,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                 }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
-                    const bf16x8 b = nibbles_bf16x16(w[u][q][c]);
+                    const bf16x8 b = nibbles_bf16x16(nibble_transpose8(w[u][q][c], tp));
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), b, acc[q][c], 0, 0, 0);
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), b, acc[q][c], 0, 0, 0);
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), b, acc[q][c], 0, 0, 0);
@@ -1418,7 +1314,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
         for (int i = 0; i < OPT; ++i) {
             const int t = threadIdx.x + i * NW * 64;
             const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
-            const int col = 16 * (blk0 + c) + sl;
+            const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
+            const int col = 8 * strip + el;
             float s = 0.0f;
             if (t < 256 * C && m < a.M && col < a.N) {
 #pragma unroll
@@ -1427,7 +1324,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
                 // h + m + l turns an infinite x * s into inf - inf: recompute
                 // a non-finite total as the reference's k-order sum.
                 if (!isfinite(s))
-                    s = i4_column_exact<NORM>(Wq[q], SCq[q], col, a.spc, a.Kpad, a.KB, a.x + (int64_t)m * K,
+                    s = i4_column_exact<NORM>(Wq[q], SCq[q], strip, el, a.spc, a.Kpad, a.RQ, a.x + (int64_t)m * K,
                                               a.gamma, 0, K);
                 if constexpr (NORM) s = s * inv_rms[m];
                 const float* bq = a.bias[NG == 1 ? wt : q];
@@ -1440,7 +1337,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     for (int i = 0; i < OPT; ++i) {
         const int t = threadIdx.x + i * NW * 64;
         const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
-        const int col = 16 * (blk0 + c) + sl;
+        const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
         if (t < 256 * C && m < a.M && col < a.N) {
             float r0 = o[0][i];
             if constexpr (NG == 2) r0 = silu_f32(o[0][i]) * o[1][i];
@@ -1450,29 +1347,30 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
 }
 
 
-// The super-block form (any row blocks, optional K split).  NG == 2: the
-// gated MLP, gate and up blocks of the same columns in one workgroup, h =
-// silu(gate + bias) * (up + bias2) (split K: in k_skinny_reduce).  XA: x rows
-// are 16-byte aligned and K % 4 == 0 (float4 loads); otherwise one float per
-// load.  MB: row blocks of 16 (M <= 16 MB).
+// The super-block form (any row blocks, optional K split).  NG == 2: the gated MLP, gate and up blocks of the same columns in one
+// workgroup, h = silu(gate + bias) * (up + bias2) (split K: in
+// k_skinny_reduce).  XA: x rows are 16-byte aligned and K % 4 == 0 (float4
+// loads); otherwise one float per load.  MB: row blocks of 16 (M <= 16 MB).
 //
-// The K range is walked in super-blocks of 128 rows (four k blocks),
-// wavefront w taking super-blocks w, w + NW, ...  In a super-block, lane
-// (g, n) loads, per column block, the dword of each of the four k blocks (its
-// B operands, rows 8g .. 8g + 7 of column n of that block) and, per row
-// block, x rows 32 t + 8 g .. 32 t + 8 g + 7 (t = 0..3) of its batch row (two
-// quads each).  MFMA t takes k block t: A = x * s of those eight rows, B =
-// dword t.  The scales of the workgroup's K range sit in LDS (read once,
-// coalesced); the next super-block's codes and x are loaded while the current
-// one is computed.
+// The K range is walked in super-blocks of 128 rows, wavefront w taking
+// super-blocks w, w + NW, ...  In a super-block, lane (g, e) of strip j loads
+// rows 16e + 4g .. 16e + 4g + 3 of its strip (16 bytes, all eight columns; the
+// 32 lanes of a strip read its 512 bytes once) and, for t = 0..7, x rows
+// 16t + 4g .. 16t + 4g + 3 of its batch row (the four lane groups of a batch
+// row read 64 contiguous bytes per load, one cache line).  Dword i of the
+// codes transposed across the eight lanes e gives column e at rows
+// 16e' + 4g + i (e' = 0..7), the B operand of MFMA i; component i of the
+// eight x quads is the matching A operand.  The scales of the workgroup's K
+// range sit in LDS (read once, coalesced); the next super-block's codes and x
+// are loaded while the current one is computed.
 template <int NW, int C, int NG, bool XA, int MB, bool HALF>
 struct SkinnyRegs {
-    uint4 w[NG][C];                // dword t: k block t of the super-block, this lane's column
-    float4 xq[MB][HALF ? 4 : 8];  // x quads of each batch row: quad 2t + h (HALF: quad t, half h of the lane)
+    uint4 w[NG][C];                // 4 rows x 8 columns of each strip
+    float4 xq[MB][HALF ? 4 : 8];  // x quads of each batch row (HALF: half of them)
 };
 
-// HALF (one row block, M <= 8): as in k_skinny3, lane n < 8 takes the first
-// four of each k block's eight rows of row n and lane n + 8 the last four; a
+// HALF (one row block, M <= 8): as in k_skinny3, lane n < 8 takes x quads
+// t = 0..3 of row n and lane n + 8 quads t = 4..7 of the same row; a
 // row_ror:8 exchange completes each A operand (the same bf16 planes).
 template <int NW, int C, int NG, bool XA, int MB, bool SPLIT, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
@@ -1480,6 +1378,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     constexpr int XT = HALF ? 4 : 8;  // x quads per lane, row block and super-block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
+    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int K = a.K;
     // Workgroup v: K range v % S of column group v / S (the ranges of one
     // column group are neighbours, so they share an XCD's L2 for the scales).
@@ -1514,12 +1413,12 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     __amdgpu_buffer_rsrc_t rW[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q)
-        rW[q] = make_rsrc(a.W[q] + (int64_t)blk0 * a.KB * 16, (uint32_t)C * (uint32_t)a.KB * 256u);
+        rW[q] = make_rsrc(a.W[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = c * a.KB * 256 + 4 * lane;
-    const int xr = HALF ? (n & 7) : n, xh = HALF ? 4 * (n >> 3) : 0;
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (16 * e + 4 * g) * 4;
+    const int xr = HALF ? (n & 7) : n, toff = HALF ? 4 * (n >> 3) : 0;
     bool row_live[MB];
     int xrow[MB];
 #pragma unroll
@@ -1527,28 +1426,22 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
         row_live[b] = xr + 16 * b < a.M;
         xrow[b] = row_live[b] ? (xr + 16 * b) * K * 4 : 0;
     }
+    const NibbleT tp = nibble_t(e);
 
-    // Loads of super-block sb; one past the range reads x, the codes and (in
-    // compute) the scales of its last super-block, all times x = 0.
+    // Loads of super-block sb; one past the range reads x as zeros (and codes
+    // that are then multiplied by zero).
     auto load = [&](SkinnyRegs<NW, C, NG, XA, MB, HALF>& r, int sb) {
         const bool in = sb < sb_hi;
 #pragma unroll
         for (int q = 0; q < NG; ++q)
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
-                const int vo = in ? wv[c] : kOobOff;
-                r.w[q][c] = make_uint4(buf_load4_stream(rW[q], vo, (4 * sb + 0) * 256),
-                                       buf_load4_stream(rW[q], vo, (4 * sb + 1) * 256),
-                                       buf_load4_stream(rW[q], vo, (4 * sb + 2) * 256),
-                                       buf_load4_stream(rW[q], vo, (4 * sb + 3) * 256));
-            }
-        const int k0 = sb * kSkinnySB + 8 * g + xh;
+            for (int c = 0; c < C; ++c) r.w[q][c] = buf_load16_stream(rW[q], wv[c], sb * (kSkinnySB * 4));
+        const int k0 = sb * kSkinnySB + 4 * g + 16 * toff;
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
             for (int t = 0; t < XT; ++t) {
-                // quad t: k block t >> 1 (HALF: t), rows 4 (t & 1) .. + 3 of the lane's eight (HALF: its half)
-                const int kk = k0 + (HALF ? 32 * t : 32 * (t >> 1) + 4 * (t & 1));
+                const int kk = k0 + 16 * t;
                 if constexpr (XA) {
                     r.xq[b][t] = buf_load4f<true>(rX, in && row_live[b] && kk < K ? xrow[b] + kk * 4 : kOobOff, 0);
                 } else {
@@ -1576,23 +1469,20 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB, HALF>& r, int sb) {
         // A super-block past the range has x = 0; its scale reads stay inside
         // the range's LDS rows.
-        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + 2 * g + xh / 4;
+        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + g + 4 * toff;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {  // k block t of the super-block
+        for (int q = 0; q < NG; ++q) {
+            float4 s4[XT];
 #pragma unroll
-            for (int q = 0; q < NG; ++q) {
-                float4 s4[HALF ? 1 : 2];
+            for (int t = 0; t < XT; ++t) s4[t] = ssc[q][lr + 4 * t];
 #pragma unroll
-                for (int h = 0; h < (HALF ? 1 : 2); ++h) s4[h] = ssc[q][lr + 8 * t + h];
+            for (int i = 0; i < 4; ++i) {
                 uint4 ah[MB], am[MB], al[MB];
 #pragma unroll
                 for (int b = 0; b < MB; ++b) {
-                    float xs[HALF ? 4 : 8];
+                    float xs[XT];
 #pragma unroll
-                    for (int h = 0; h < (HALF ? 1 : 2); ++h)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            xs[4 * h + i] = f4get(r.xq[b][HALF ? t : 2 * t + h], i) * f4get(s4[h], i);
+                    for (int t = 0; t < XT; ++t) xs[t] = f4get(r.xq[b][t], i) * f4get(s4[t], i);
                     if constexpr (HALF) {
                         uint2 h2, m2, l2;
                         split3_4(xs, h2, m2, l2);
@@ -1605,8 +1495,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
                 }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
-                    const uint32_t wd = t == 0 ? r.w[q][c].x : (t == 1 ? r.w[q][c].y : (t == 2 ? r.w[q][c].z : r.w[q][c].w));
-                    const bf16x8 bq = nibbles_bf16x16(wd);
+                    const uint32_t wd = i == 0 ? r.w[q][c].x : (i == 1 ? r.w[q][c].y : (i == 2 ? r.w[q][c].z : r.w[q][c].w));
+                    const bf16x8 bq = nibbles_bf16x16(nibble_transpose8(wd, tp));
 #pragma unroll
                     for (int b = 0; b < MB; ++b) {
                         acc[q][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[b]), bq,
@@ -1666,7 +1556,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
                 const int t = threadIdx.x + i * NW * 64;
                 const int c = t >> 8, mr = (t >> 4) & 15, sl = t & 15;
                 const int m = mr + 16 * b;
-                const int col = 16 * (blk0 + c) + sl;
+                const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
+                const int col = 8 * strip + el;
                 float s = 0.0f;
                 if (t < 256 * C && m < a.M && col < a.N) {
 #pragma unroll
@@ -1675,8 +1566,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
                     // h + m + l turns an infinite x * s into inf - inf: recompute
                     // a non-finite total as the reference's k-order sum.
                     if (!isfinite(s))
-                        s = i4_column_exact<false>(a.W[q], a.SC[q], col, a.spc, a.Kpad, a.KB, a.x + (int64_t)m * K,
-                                                   nullptr, klo, khi);
+                        s = i4_column_exact<false>(a.W[q], a.SC[q], strip, el, a.spc, a.Kpad, a.RQ,
+                                                   a.x + (int64_t)m * K, nullptr, klo, khi);
                     if (!SPLIT && a.bias[q]) s = s + a.bias[q][col];
                 }
                 o[q][b][i] = s;
@@ -1688,7 +1579,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
         for (int i = 0; i < OPT; ++i) {
             const int t = threadIdx.x + i * NW * 64;
             const int c = t >> 8, m = ((t >> 4) & 15) + 16 * b, sl = t & 15;
-            const int col = 16 * (blk0 + c) + sl;
+            const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
             if (t < 256 * C && m < a.M && col < a.N) {
                 const int64_t at = (int64_t)m * a.N + col;
                 if constexpr (SPLIT) {
@@ -1950,15 +1841,26 @@ __global__ __launch_bounds__(kThreads) void k_linear_i4_flat(const float* __rest
 
 bool x_aligned4(const float* x, int64_t K) { return K % 4 == 0 && (((uintptr_t)x) & 15) == 0; }
 
-template <int MT, int NW, int U, int NG, bool STREAM>
-hipError_t gemv_launch_st(const GemvArgs& a, hipStream_t s) {
-    const dim3 grid((unsigned)(a.NS << a.Plog));
+template <int BITS, int MT, int NW, int U, int NG, int SPW, bool STREAM>
+hipError_t gemv_launch_st(const GemvArgs& a, int nw, hipStream_t s) {
+    const dim3 grid((unsigned)(((a.NS + SPW - 1) / SPW) << a.Plog), (unsigned)nw);
     GemvArgs ag = a;
     ag.nblk = (int)grid.x;
-    if (a.K % 4 == 0)
-        k_gemv<MT, NW, U, true, NG, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
+    const bool k4 = a.K % 4 == 0;
+    if constexpr (BITS == 4 && SPW == 1) {  // the norm-fused form serves the INT4 LLaMA block
+        if (a.gamma) {
+            if (k4)
+                k_gemv<BITS, MT, NW, U, true, NG, SPW, true, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
+            else
+                k_gemv<BITS, MT, NW, U, false, NG, SPW, true, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
+            return hipGetLastError();
+        }
+    }
+    if (a.gamma) return hipErrorInvalidValue;
+    if (k4)
+        k_gemv<BITS, MT, NW, U, true, NG, SPW, false, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
     else
-        k_gemv<MT, NW, U, false, NG, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
+        k_gemv<BITS, MT, NW, U, false, NG, SPW, false, STREAM><<<grid, NG * NW * 64, 0, s>>>(ag);
     return hipGetLastError();
 }
 
@@ -1966,10 +1868,10 @@ hipError_t gemv_launch_st(const GemvArgs& a, hipStream_t s) {
 // always up to four rows); the row groups of a larger batch each read the
 // strip again, and its second read should hit the L2 (measured on 2048->2048
 // at 16 rows: 5.65 us plain, 5.99 streaming).
-template <int MT, int NW, int U, int NG>
-hipError_t gemv_launch_nu(const GemvArgs& a, hipStream_t s) {
-    if (MT <= 4 || a.Plog == 0) return gemv_launch_st<MT, NW, U, NG, true>(a, s);
-    if constexpr (MT > 4) return gemv_launch_st<MT, NW, U, NG, false>(a, s);
+template <int BITS, int MT, int NW, int U, int NG, int SPW>
+hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
+    if (MT <= 4 || a.Plog == 0) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, true>(a, nw, s);
+    if constexpr (MT > 4) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, false>(a, nw, s);
     return hipErrorInvalidValue;
 }
 
@@ -1984,15 +1886,15 @@ constexpr int kGemvWaves = 4;
 // in one batch at M = 1, less as the rows multiply.
 constexpr int gemv_umax(int rows) { return rows <= 1 ? 8 : (rows <= 2 ? 4 : (rows <= 4 ? 2 : 1)); }
 
-template <int MT, int NG, int NW>
-hipError_t gemv_launch_w(const GemvArgs& a, hipStream_t s) {
+template <int BITS, int MT, int NG, int SPW, int NW>
+hipError_t gemv_launch_spw(const GemvArgs& a, int nw, hipStream_t s) {
     // Row quads in flight per lane: enough for all of K in one batch where the
     // register budget allows (gemv_umax), else batches of UMAX.
-    constexpr int UMAX = gemv_umax(MT);
+    constexpr int UMAX = gemv_umax(MT * SPW);
     const int per_lane = (a.RQ + NW * 64 - 1) / (NW * 64);
 #define SGQ_GEMV_NU(U_)                                                                              \
     if constexpr (U_ <= UMAX) {                                                                      \
-        if (per_lane > (U_ == 8 ? 6 : (U_ == 6 ? 4 : U_ / 2)) || U_ == 1) return gemv_launch_nu<MT, NW, U_, NG>(a, s); \
+        if (per_lane > (U_ == 8 ? 6 : (U_ == 6 ? 4 : U_ / 2)) || U_ == 1) return gemv_launch_nu<BITS, MT, NW, U_, NG, SPW>(a, nw, s); \
     }
     SGQ_GEMV_NU(8)
     SGQ_GEMV_NU(6)
@@ -2003,25 +1905,44 @@ hipError_t gemv_launch_w(const GemvArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
-template <int MT, int NG>
-hipError_t gemv_launch(const GemvArgs& a, hipStream_t s) {
+template <int BITS, int MT, int NG>
+hipError_t gemv_launch(const GemvArgs& a, int nw, hipStream_t s) {
+    if constexpr (BITS == 4 && NG == 1 && MT <= 2) {
+        // Two strips per workgroup (they must share a scale column) load each
+        // x and scale quad once for both: a third fewer load instructions per
+        // code byte, which is what the one- and two-row GEMV waits on.  Only
+        // where that still leaves a workgroup per CU, and with enough
+        // wavefronts to keep all of K in one batch of loads.  Measured on
+        // MI355X at M=1: 4096->4096 4.30 -> 4.21 us, 4096->11008 7.67 -> 6.93,
+        // 11008->4096 7.39 -> 7.22 (16 wavefronts); M=2 4096->11008 9.11 -> 8.52.
+        if (nw == 1 && a.mode % 2 == 0 && a.NS >= 2 * a.cus) {
+            constexpr int um = gemv_umax(2 * MT);
+            if (a.RQ <= um * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, kGemvWaves>(a, nw, s);
+            if (a.RQ <= um * 2 * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, 2 * kGemvWaves>(a, nw, s);
+            if (a.RQ <= um * 4 * kGemvWaves * 64) return gemv_launch_spw<BITS, MT, NG, 2, 4 * kGemvWaves>(a, nw, s);
+        }
+    }
     // Few strips for the GPU (under two workgroups per CU) and a K long enough
     // for eight wavefronts: split K over eight wavefronts instead of four, so
-    // each SIMD holds more than one wavefront to hide load latency.
-    if (((int64_t)a.NS << a.Plog) < 2 * a.cus && a.RQ >= 8 * 64) return gemv_launch_w<MT, NG, 2 * kGemvWaves>(a, s);
+    // each SIMD holds more than one wavefront to hide load latency.  Measured
+    // on MI355X: 5632 -> 2048 at M=8 9.1 -> 7.7 us, M=1 4.8 -> 4.6 us;
+    // 2048 -> 2048 at M=4 3.9 -> 3.7 us.
+    if (((int64_t)nw * a.NS << a.Plog) < 2 * a.cus && a.RQ >= 8 * 64)
+        return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
     // A K too long for one batch of four wavefronts but within one batch of
     // eight: eight wavefronts, so that every load is in flight at once instead
-    // of batches that each wait a full memory latency.
+    // of batches that each wait a full memory latency (measured on MI355X,
+    // 11008 -> 4096 at M=1: 8.2 -> 7.8 us).
     if constexpr (MT == 1) {
         constexpr int um = gemv_umax(1);
         if (a.RQ > um * kGemvWaves * 64 && a.RQ <= um * 2 * kGemvWaves * 64)
-            return gemv_launch_w<MT, NG, 2 * kGemvWaves>(a, s);
+            return gemv_launch_spw<BITS, MT, NG, 1, 2 * kGemvWaves>(a, nw, s);
     }
-    return gemv_launch_w<MT, NG, kGemvWaves>(a, s);
+    return gemv_launch_spw<BITS, MT, NG, 1, kGemvWaves>(a, nw, s);
 }
 
-template <int NG>
-hipError_t gemv_dispatch(GemvArgs a, int64_t M, hipStream_t s) {
+template <int BITS, int NG>
+hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.M = (int)M;
     a.cus = device_cus(s);
     a.xlog = xcd_log2(device_xcds(s));
@@ -2030,147 +1951,13 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, hipStream_t s) {
     // of kRowsMax (each a workgroup of its own over the same strip), their
     // count rounded up to a power of two for the index arithmetic.
     a.Plog = 0;
-    if (M <= 1) return gemv_launch<1, NG>(a, s);
-    if (M <= 2) return gemv_launch<2, NG>(a, s);
-    if (M <= 4) return gemv_launch<4, NG>(a, s);
+    if (M <= 1) return gemv_launch<BITS, 1, NG>(a, nw, s);
+    if (M <= 2) return gemv_launch<BITS, 2, NG>(a, nw, s);
+    if (M <= 4) return gemv_launch<BITS, 4, NG>(a, nw, s);
     const int64_t groups = (M + kRowsMax - 1) / kRowsMax;
     while ((int64_t)1 << a.Plog < groups) ++a.Plog;
     if (((int64_t)kRowsMax << a.Plog) > kGemvRowsMax) return hipErrorInvalidValue;
-    return gemv_launch<kRowsMax, NG>(a, s);
-}
-
-// ---- INT4 GEMV (k_gemv4) launch ----------------------------------------
-// 16-byte steps a lane keeps in flight at most (each holds four code dwords,
-// its x pair per row and its scale pair): all of K = 4096 with four
-// wavefronts at one row, fewer as the rows multiply.
-constexpr int gemv4_umax(int rows) { return rows <= 1 ? 16 : (rows <= 2 ? 8 : (rows <= 4 ? 4 : 2)); }
-
-template <int MT, int NW, int U, int NG, bool SHS, bool XA, bool NORM>
-hipError_t gemv4_launch_u(const GemvArgs& a, int nw, hipStream_t s) {
-    const dim3 grid((unsigned)(a.NB << a.Plog), (unsigned)nw);
-    GemvArgs ag = a;
-    ag.nblk = (int)grid.x;
-    // Codes take the streaming policy when one row group reads them; the
-    // row groups of a larger batch each read the block again (its second
-    // read should hit the L2).
-    if (MT <= 2 || a.Plog == 0)
-        k_gemv4<MT, NW, U, XA, NG, NORM, true, SHS><<<grid, NG * NW * 64, 0, s>>>(ag);
-    else if constexpr (MT > 2)
-        k_gemv4<MT, NW, U, XA, NG, NORM, false, SHS><<<grid, NG * NW * 64, 0, s>>>(ag);
-    return hipGetLastError();
-}
-
-// Steps per lane in one batch of loads: every step at once where the
-// register budget allows (gemv4_umax; the norm-fused form at most 4), else
-// batches of the budget.  Shapes off the fast path (K odd or x not 8-byte
-// aligned, or a column block across two scale columns) run one step at a
-// time.
-template <int MT, int NW, int NG, bool SHS, bool XA, bool NORM>
-hipError_t gemv4_launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
-    // 1024-thread workgroups (16 wavefronts) have 128 VGPRs a lane: at most 8 steps.
-    constexpr int UB = NORM && gemv4_umax(MT) > 4 ? 4 : (NG * NW >= 16 && gemv4_umax(MT) > 8 ? 8 : gemv4_umax(MT));
-    constexpr int UMAX = !(SHS && XA) ? 1 : UB;
-    const int nit = (a.KB + 4 * NW - 1) / (4 * NW);
-#define SGQ_GEMV4_U(U_)                                                                           \
-    if constexpr (U_ <= UMAX) {                                                                   \
-        if (nit <= U_ || U_ == UMAX) return gemv4_launch_u<MT, NW, U_, NG, SHS, XA, NORM>(a, nw, s); \
-    }
-    SGQ_GEMV4_U(1)
-    SGQ_GEMV4_U(2)
-    SGQ_GEMV4_U(4)
-    SGQ_GEMV4_U(8)
-    SGQ_GEMV4_U(16)
-#undef SGQ_GEMV4_U
-    return hipErrorInvalidValue;
-}
-
-// Wavefronts per workgroup (each owns one column block, all of K):
-//  - up to two rows with a workgroup per CU: the fewest of 4, 8, 16 that keep
-//    all of K in one batch of loads (4096 rows at one row: four);
-//  - fewer workgroups than CUs and K of at least 2048: eight, so that each
-//    SIMD holds more than one wavefront to hide load latency;
-//  - otherwise four (they keep the cross-wavefront LDS sum short).
-template <int MT, int NG, bool SHS, bool XA, bool NORM>
-hipError_t gemv4_launch_mt(const GemvArgs& a, int nw, hipStream_t s) {
-    if constexpr (!(SHS && XA)) {
-        return gemv4_launch_nw<MT, 4, NG, SHS, XA, NORM>(a, nw, s);
-    } else {
-        const int64_t wgs = ((int64_t)a.NB * nw) << a.Plog;
-        int NW = 4;
-        if (MT <= 2 && wgs >= a.cus) {
-            const int um = NORM && gemv4_umax(MT) > 4 ? 4 : gemv4_umax(MT);
-            NW = a.KB <= um * 16 ? 4 : (a.KB <= (NG == 2 && um > 8 ? 8 : um) * 32 ? 8 : 16);
-        } else if (wgs < a.cus && a.KB >= 64) {
-            NW = 8;
-        }
-        if constexpr (MT <= 2) {
-            if (NW == 16) return gemv4_launch_nw<MT, 16, NG, SHS, XA, NORM>(a, nw, s);
-        }
-        if (NW >= 8) return gemv4_launch_nw<MT, 8, NG, SHS, XA, NORM>(a, nw, s);
-        return gemv4_launch_nw<MT, 4, NG, SHS, XA, NORM>(a, nw, s);
-    }
-}
-
-template <int NG, bool SHS, bool XA, bool NORM>
-hipError_t gemv4_launch_rows(const GemvArgs& a, int MT, int nw, hipStream_t s) {
-    switch (MT) {
-        case 1: return gemv4_launch_mt<1, NG, SHS, XA, NORM>(a, nw, s);
-        case 2: return gemv4_launch_mt<2, NG, SHS, XA, NORM>(a, nw, s);
-        case 4: return gemv4_launch_mt<4, NG, SHS, XA, NORM>(a, nw, s);
-        case 8: return gemv4_launch_mt<8, NG, SHS, XA, NORM>(a, nw, s);
-    }
-    return hipErrorInvalidValue;
-}
-
-template <int NG, bool NORM>
-hipError_t gemv4_launch_form(const GemvArgs& a, int MT, bool shs, bool xa, int nw, hipStream_t s) {
-    if (xa && shs) return gemv4_launch_rows<NG, true, true, NORM>(a, MT, nw, s);
-    if (shs) return gemv4_launch_rows<NG, true, false, NORM>(a, MT, nw, s);
-    if (xa) return gemv4_launch_rows<NG, false, true, NORM>(a, MT, nw, s);
-    return gemv4_launch_rows<NG, false, false, NORM>(a, MT, nw, s);
-}
-
-// Rows per workgroup: one group of M <= 4 rows (rounded up to 1, 2 or 4);
-// larger batches in groups of 8, their count rounded up to a power of two
-// for the index arithmetic, or of 4 (twice the groups) where groups of 8
-// would leave CUs without a workgroup (narrow weights: every group reads
-// the block's codes, the second time from L2, and only its own rows of x).
-template <int NG>
-hipError_t gemv4_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
-    a.M = (int)M;
-    a.cus = device_cus(s);
-    a.xlog = xcd_log2(device_xcds(s));
-    a.Plog = 0;
-    int MT = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
-    if (MT == 8) {
-        while (((int64_t)8 << a.Plog) < M) ++a.Plog;
-        if ((((int64_t)a.NB * nw) << a.Plog) < a.cus && ((int64_t)4 << (a.Plog + 1)) <= kGemvRowsMax) {
-            MT = 4;
-            ++a.Plog;
-        }
-    }
-    if (((int64_t)MT << a.Plog) > kGemvRowsMax) return hipErrorInvalidValue;
-    const bool xa = a.K % 2 == 0 && (((uintptr_t)a.x) & 7) == 0 && (!a.gamma || (((uintptr_t)a.gamma) & 7) == 0);
-    const bool shs = a.mode % 2 == 0;
-    return a.gamma ? gemv4_launch_form<NG, true>(a, MT, shs, xa, nw, s)
-                   : gemv4_launch_form<NG, false>(a, MT, shs, xa, nw, s);
-}
-
-GemvArgs gemv4_args(const float* x, int64_t K, int64_t N, const I4Geom& g, float* y, int64_t ldy, const float* res) {
-    GemvArgs a{};
-    a.x = x;
-    a.K = (int)K;
-    a.N = (int)N;
-    a.mode = (int)g.spc;
-    a.spc = FastDiv((uint32_t)g.spc);
-    a.Kpad = (int)g.Kpad;
-    a.KB = (int)g.KB;
-    a.NB = (int)g.NB;
-    a.NS = (int)g.NS;
-    a.y = y;
-    a.ldy = (int)ldy;
-    a.res = res;
-    return a;
+    return gemv_launch<BITS, kRowsMax, NG>(a, nw, s);
 }
 
 GemvArgs gemv_args(const float* x, int64_t K, int64_t N, int mode, int64_t Kpad, int64_t RQ, int64_t NS, float* y,
@@ -2225,7 +2012,7 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     a.eps = ex.eps;
     a.spc = (int)g.spc;
     a.Kpad = (int)g.Kpad;
-    a.KB = (int)g.KB;
+    a.RQ = (int)g.RQ;
     a.wpc = FastDiv((uint32_t)(g.spc / (2 * C)));
     a.y = y;
     a.part = part;
@@ -2379,7 +2166,7 @@ hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N,
                                 const float* const* devscales, const float* const* bias, const I4Geom& g, float* y,
                                 int64_t ldy, const float* res, const float* gamma, float eps, hipStream_t s) {
     if (nw < 1 || nw > 3) return hipErrorInvalidValue;
-    GemvArgs a = gemv4_args(x, K, N, g, y, ldy, res);
+    GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, y, ldy, res);
     a.gamma = gamma;
     a.eps = eps;
     for (int w = 0; w < nw; ++w) {
@@ -2387,7 +2174,7 @@ hipError_t launch_gemv_i4_multi(const float* x, int64_t M, int64_t K, int64_t N,
         a.SC[w] = devscales[w];
         a.bias[w] = bias[w];
     }
-    return gemv4_dispatch<1>(a, M, nw, s);
+    return gemv_dispatch<4, 1>(a, M, nw, s);
 }
 
 hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed, const float* scales,
@@ -2397,14 +2184,14 @@ hipError_t launch_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const
     a.W[0] = (const uint4*)packed;
     a.SC[0] = scales;
     a.bias[0] = bias;
-    return gemv_dispatch<1>(a, M, s);
+    return gemv_dispatch<8, 1>(a, M, 1, s);
 }
 
 hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
                                  const float* devscales_g, const float* bias_g, const void* packed_u,
                                  const float* devscales_u, const float* bias_u, const I4Geom& g, float* h,
                                  hipStream_t s, const float* gamma, float eps) {
-    GemvArgs a = gemv4_args(x, K, N, g, h, N, nullptr);
+    GemvArgs a = gemv_args(x, K, N, (int)g.spc, g.Kpad, g.RQ, g.NS, h, N, nullptr);
     a.gamma = gamma;
     a.eps = eps;
     a.W[0] = (const uint4*)packed_g;
@@ -2413,7 +2200,7 @@ hipError_t launch_swiglu_gemv_i4(const float* x, int64_t M, int64_t K, int64_t N
     a.SC[1] = devscales_u;
     a.bias[0] = bias_g;
     a.bias[1] = bias_u;
-    return gemv4_dispatch<2>(a, M, 1, s);
+    return gemv_dispatch<4, 2>(a, M, 1, s);
 }
 
 hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N, const void* packed_g,
@@ -2428,7 +2215,7 @@ hipError_t launch_swiglu_gemv_i8(const float* x, int64_t M, int64_t K, int64_t N
     a.SC[1] = scales_u;
     a.bias[0] = bias_g;
     a.bias[1] = bias_u;
-    return gemv_dispatch<2>(a, M, s);
+    return gemv_dispatch<8, 2>(a, M, 1, s);
 }
 
 hipError_t launch_silu_mul(float* h, const float* u, int64_t n, hipStream_t s) {
@@ -2684,7 +2471,7 @@ hipError_t launch_gemm_i8(const float* x, int64_t M, int64_t K, int64_t N, const
 hipError_t launch_gemm_i4(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,
                           const float* devscales, const I4Geom& g, const float* bias, float* y, void* ws,
                           hipStream_t s) {
-    return gemm_launch<4>(x, M, K, N, packed, devscales, (int)g.spc, g.Kpad, g.KB, g.NS, bias, y, ws, s);
+    return gemm_launch<4>(x, M, K, N, packed, devscales, (int)g.spc, g.Kpad, g.RQ, g.NS, bias, y, ws, s);
 }
 
 hipError_t launch_linear_i4_flat(const float* x, int64_t M, int64_t K, int64_t N, const void* packed,

