@@ -177,8 +177,15 @@ class Case:
         untimed sweep graph runs one call on each of the C copies in order, so
         that whatever K is, each timed call's weights were last touched at
         least C calls (more than the 256 MB Infinity Cache) earlier and stream
-        from HBM.  extra_replays > 0 replays it that many more times afterwards
-        (untimed by the contract) and keeps their per-call times in
+        from HBM.  The sweep is queued on the same stream just ahead of the
+        timed replay: the start event fires when the sweep's last call ends,
+        by which time the host has submitted the timed graph, so the region
+        holds the K calls and not the host's submission of the graph (about
+        14 us for 20 calls, spent while the GPU would otherwise sit idle).
+        That cost is kept apart in self.idle_start_ms: the same replay started
+        on an idle GPU, the start event recorded before the graph is
+        submitted.  extra_replays > 0 replays it that many more times
+        afterwards (untimed by the contract) and keeps their per-call times in
         self.replay_ms."""
         import torch
 
@@ -198,6 +205,14 @@ class Case:
         sweep.replay()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        sweep.replay()
+        torch.cuda.synchronize()
+        s.record()  # idle GPU: the region includes the host's submission of the graph
+        g.replay()
+        e.record()
+        torch.cuda.synchronize()
+        self.idle_start_ms = s.elapsed_time(e) / steps
+        sweep.replay()  # untimed; still running while the timed graph is submitted
         s.record()
         g.replay()
         e.record()
@@ -915,7 +930,8 @@ def main() -> int:
         spread = {"p10": round(float(q[0]), 3), "p50": round(float(q[1]), 3), "p90": round(float(q[2]), 3),
                   "replays": 1 + len(case.replay_ms)}
     err = case.check(Oracle(), rows=None if c["M"] <= 256 else np.r_[0:8, c["M"] - 8:c["M"]])
-    log(f"[bench] {args.config}: {ms * 1e3:.3f} us/step (eager {ms_eager * 1e3:.3f} us), rel_err {err:.2e}")
+    idle = "" if args.eager else f", idle-GPU start {case.idle_start_ms * 1e3:.3f} us"
+    log(f"[bench] {args.config}: {ms * 1e3:.3f} us/step (eager {ms_eager * 1e3:.3f} us{idle}), rel_err {err:.2e}")
     if err > 1e-5:
         raise SystemExit(f"parity failure in bench: rel err {err}")
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -952,6 +968,11 @@ def main() -> int:
                    "group_size": c["G"] or None, "bits": c["bits"], "weight_copies": copies,
                    "launch": "eager" if args.eager else "one hipGraph of K back-to-back forward calls",
                    "eager_us_per_step": round(ms_eager * 1e3, 3), "tflops": round(tfl, 4),
+                   "idle_start_us_per_step": None if args.eager else round(case.idle_start_ms * 1e3, 3),
+                   "timed_region": None if args.eager else (
+                       "the K calls only: the untimed cache-evicting sweep runs just ahead on the same stream, "
+                       "so the host's submission of the graph overlaps it; idle_start_us_per_step is the same "
+                       "replay started on an idle GPU, submission included"),
                    "us_per_step_over_replays": spread,
                    "rel_err_vs_oracle": err},
         "roofline": roofline,
