@@ -180,11 +180,11 @@ class Case:
         from HBM.  The sweep is queued on the same stream just ahead of the
         timed replay: the start event fires when the sweep's last call ends,
         by which time the host has submitted the timed graph, so the region
-        holds the K calls and not the host's submission of the graph (about
-        14 us for 20 calls, spent while the GPU would otherwise sit idle).
-        That cost is kept apart in self.idle_start_ms: the same replay started
-        on an idle GPU, the start event recorded before the graph is
-        submitted.  extra_replays > 0 replays it that many more times
+        holds the K calls whatever the host's submission takes.
+        self.idle_start_ms is the same replay started on an idle GPU, the
+        start event recorded before the graph is submitted (measured on
+        MI355X within 0.4% of the other: 4.477 against 4.461 us per call at 20
+        C2 calls).  extra_replays > 0 replays it that many more times
         afterwards (untimed by the contract) and keeps their per-call times in
         self.replay_ms."""
         import torch
@@ -396,6 +396,75 @@ def rocprof_fields(prof: dict, nbytes: float, peak: float, per_second) -> dict:
                                    "profiled_csrc_digest": prof.get("csrc_digest"), "current_csrc_digest": cur,
                                    "summary": prof.get("summary"),
                                    "note": "profiled on other kernel sources than this build's"}}
+
+
+# The dominant kernel of each profiled workload, by the start of its name.
+PROFILED_KERNEL = {"c2": "sgq::k_gemv<", "c4": "sgq::k_gemm3<"}
+
+
+def _plain_kernel_name(name: str) -> str:
+    """A demangled rocprofv3 kernel name without the return type and the
+    anonymous namespace: 'sgq::k_gemv<4, 1, ...>(sgq::GemvArgs)'."""
+    name = name.replace("(anonymous namespace)::", "")
+    return name[5:] if name.startswith("void ") else name
+
+
+def _short_kernel_name(name: str) -> str:
+    plain = _plain_kernel_name(name)
+    return plain[:plain.index("(")].replace("sgq::", "").replace(" ", "") if "(" in plain else plain
+
+
+def _csv_rows(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_trace(csv_path: str, config: str, eager_calls: int, summary: str) -> dict:
+    """profiles/kernel_<config>.json from a rocprofv3 --kernel-trace CSV of
+    bench.py: durations of the workload's dominant kernel, all dispatches and
+    those after its first eager_calls (the graph replays), with the digest of
+    the kernel sources this tree builds."""
+    rows = [r for r in _csv_rows(csv_path) if _plain_kernel_name(r["Kernel_Name"]).startswith(PROFILED_KERNEL[config])]
+    if not rows:
+        raise SystemExit(f"no {PROFILED_KERNEL[config]} dispatches in {csv_path}")
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    names = {r["Kernel_Name"] for r in rows}
+    if len(names) != 1:
+        raise SystemExit(f"more than one {PROFILED_KERNEL[config]} instantiation in {csv_path}: {sorted(names)}")
+    ns = np.array([int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows], dtype=np.float64)
+    graph = ns[eager_calls:] if eager_calls < len(ns) else ns
+    return {"kernel": _short_kernel_name(rows[0]["Kernel_Name"]), "workload": config,
+            "avg_ns_graph_replays": int(round(graph.mean())), "median_ns_graph_replays": int(np.median(graph)),
+            "avg_ns_all_dispatches": int(round(ns.mean())), "min_ns": int(ns.min()), "dispatches": len(ns),
+            "graph_replay_dispatches": len(graph), "csrc_digest": csrc_digest(), "summary": summary}
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str, config: str, summary: str) -> dict:
+    """profiles/traffic_<config>.json from two rocprofv3 --pmc runs of
+    bench.py (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch): the median
+    per-dispatch reading of the workload's dominant kernel, each scaled by
+    what the counter reads for bench.py's 64 MiB calibration copy (64 MiB
+    read and 64 MiB written), with the digest of the kernel sources."""
+    out = {"kernel": None, "workload": config}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = [r for r in _csv_rows(path) if r["Counter_Name"] == counter]
+        copies = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        kern = [r for r in rows if _plain_kernel_name(r["Kernel_Name"]).startswith(PROFILED_KERNEL[config])]
+        if not copies or not kern:
+            raise SystemExit(f"{path}: no calibration copy or no {PROFILED_KERNEL[config]} dispatch")
+        scale = 65536.0 / max(copies)  # the calibration copy is the largest copy of the run
+        kib = float(np.median([float(r["Counter_Value"]) for r in kern]))
+        key = "fetch" if counter == "FETCH_SIZE" else "write"
+        out[f"{key}_kib_per_dispatch"] = round(kib, 1)
+        out[f"{key}_scale"] = round(scale, 4)
+        out[f"{key}_bytes"] = int(round(kib * scale * 1024))
+        out["kernel"] = _short_kernel_name(kern[0]["Kernel_Name"])
+    out["hbm_bytes_per_launch"] = out["fetch_bytes"] + out["write_bytes"]
+    out["csrc_digest"] = csrc_digest()
+    out["summary"] = summary
+    return out
 
 
 def cpu_model() -> str:
@@ -885,7 +954,25 @@ def main() -> int:
                     help="only time the 110-call C5 decode step (for profiling)")
     ap.add_argument("--gemv-size-sweep", action="store_true",
                     help="only time the M=1 INT4 forward over weights of 9 MB to 285 MB")
+    ap.add_argument("--summarize-trace", metavar="CSV",
+                    help="write profiles/kernel_<config>.json from a rocprofv3 --kernel-trace CSV of this script "
+                         "(no GPU use); --eager-calls dispatches of the kernel are left out of the graph figures")
+    ap.add_argument("--eager-calls", type=int, default=0)
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic_<config>.json from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                         "CSVs of this script (no GPU use)")
+    ap.add_argument("--summary", default="", help="the profiles/ summary the written JSON points to")
     args = ap.parse_args()
+
+    if args.summarize_trace or args.summarize_traffic:
+        if args.summarize_trace:
+            rec, name = summarize_trace(args.summarize_trace, args.config, args.eager_calls, args.summary), "kernel"
+        else:
+            rec, name = summarize_traffic(*args.summarize_traffic, args.config, args.summary), "traffic"
+        out = ROOT / "profiles" / f"{name}_{args.config}.json"
+        out.write_text(json.dumps(rec, indent=1) + "\n")
+        print(json.dumps(rec), flush=True)
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (use --gpus 1).", file=sys.stderr)
@@ -970,9 +1057,9 @@ def main() -> int:
                    "eager_us_per_step": round(ms_eager * 1e3, 3), "tflops": round(tfl, 4),
                    "idle_start_us_per_step": None if args.eager else round(case.idle_start_ms * 1e3, 3),
                    "timed_region": None if args.eager else (
-                       "the K calls only: the untimed cache-evicting sweep runs just ahead on the same stream, "
-                       "so the host's submission of the graph overlaps it; idle_start_us_per_step is the same "
-                       "replay started on an idle GPU, submission included"),
+                       "the K calls only: the untimed cache-evicting sweep runs just ahead on the same stream; "
+                       "idle_start_us_per_step is the same replay started on an idle GPU, the host's "
+                       "submission of the graph included"),
                    "us_per_step_over_replays": spread,
                    "rel_err_vs_oracle": err},
         "roofline": roofline,

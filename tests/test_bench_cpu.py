@@ -77,3 +77,52 @@ def test_committed_profiles_count_only_for_the_kernels_they_measured():
     assert h["kernel_ns"] == 4000 and h["profiled_csrc_digest"] == "0" * 16 and h["current_csrc_digest"] == cur
     # No digest at all (a profile written before digests existed) is historical too.
     assert "rocprof_historical" in bench.rocprof_fields({"avg_ns": 1}, 1.0, 1.0, lambda v: v)
+
+
+def _write_csv(path, header, rows):
+    import csv
+
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f, quoting=csv.QUOTE_NONNUMERIC)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+def test_profile_summaries_from_rocprof_csvs(tmp_path):
+    """The profiles/*.json records come from rocprofv3's CSVs: the dominant
+    kernel's durations (graph dispatches after the eager ones) and its HBM
+    bytes per launch scaled by the calibration copy, stamped with the digest
+    of the kernel sources."""
+    import bench
+
+    gemv = "void sgq::(anonymous namespace)::k_gemv<4, 1, 4, 4, true, 1, 2, false, true>(sgq::(anonymous namespace)::GemvArgs)"
+    trace = tmp_path / "t_kernel_trace.csv"
+    hdr = ["Kind", "Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp"]
+    rows = [["KERNEL_DISPATCH", 1, "__amd_rocclr_copyBuffer", 0, 5000]]
+    durs = [9000, 9000, 4000, 4100, 4200, 3900]  # two eager dispatches, then four in graphs
+    t = 10_000
+    for i, d in enumerate(durs):
+        rows.append(["KERNEL_DISPATCH", i + 2, gemv, t, t + d])
+        t += d + 100
+    _write_csv(trace, hdr, rows)
+    r = bench.summarize_trace(str(trace), "c2", 2, "profiles/x.md")
+    assert r["kernel"] == "k_gemv<4,1,4,4,true,1,2,false,true>"
+    assert r["dispatches"] == 6 and r["graph_replay_dispatches"] == 4
+    assert r["avg_ns_graph_replays"] == 4050 and r["median_ns_graph_replays"] == 4050
+    assert r["avg_ns_all_dispatches"] == round(sum(durs) / 6) and r["min_ns"] == 3900
+    assert r["csrc_digest"] == bench.csrc_digest()
+
+    hdr = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
+    fetch, write = tmp_path / "f.csv", tmp_path / "w.csv"
+    # The 64 MiB copy reads as half its bytes on FETCH_SIZE and in full on WRITE_SIZE.
+    _write_csv(fetch, hdr, [[1, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 32768.0],
+                            [2, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 100.0],
+                            [3, gemv, "FETCH_SIZE", 4400.0], [4, gemv, "FETCH_SIZE", 4500.0],
+                            [5, gemv, "FETCH_SIZE", 4467.5]])
+    _write_csv(write, hdr, [[1, "__amd_rocclr_copyBuffer", "WRITE_SIZE", 65536.0],
+                            [3, gemv, "WRITE_SIZE", 16.0], [4, gemv, "WRITE_SIZE", 16.0]])
+    r = bench.summarize_traffic(str(fetch), str(write), "c2", "profiles/y.md")
+    assert r["fetch_scale"] == 2.0 and r["write_scale"] == 1.0
+    assert r["fetch_bytes"] == 4467.5 * 2 * 1024 and r["write_bytes"] == 16 * 1024
+    assert r["hbm_bytes_per_launch"] == r["fetch_bytes"] + r["write_bytes"]
+    assert r["csrc_digest"] == bench.csrc_digest() and r["kernel"] == "k_gemv<4,1,4,4,true,1,2,false,true>"
