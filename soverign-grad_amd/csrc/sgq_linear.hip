@@ -1864,14 +1864,15 @@ hipError_t gemv_launch_st(const GemvArgs& a, int nw, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Codes take the streaming policy when one row group reads them (Plog 0,
-// always up to four rows); the row groups of a larger batch each read the
-// strip again, and its second read should hit the L2 (measured on 2048->2048
-// at 16 rows: 5.65 us plain, 5.99 streaming).
+// Codes take the streaming policy when one row group reads them (Plog 0);
+// the row groups of a larger batch each read the strip again, and its second
+// read should hit the L2 (measured on 2048->2048 at 16 rows: 5.65 us plain,
+// 5.99 streaming; at 8 rows in two groups of four: 4.39 plain, 4.51
+// streaming).  One and two rows always run as one group.
 template <int BITS, int MT, int NW, int U, int NG, int SPW>
 hipError_t gemv_launch_nu(const GemvArgs& a, int nw, hipStream_t s) {
-    if (MT <= 4 || a.Plog == 0) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, true>(a, nw, s);
-    if constexpr (MT > 4) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, false>(a, nw, s);
+    if (MT < 4 || a.Plog == 0) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, true>(a, nw, s);
+    if constexpr (MT >= 4) return gemv_launch_st<BITS, MT, NW, U, NG, SPW, false>(a, nw, s);
     return hipErrorInvalidValue;
 }
 
@@ -1954,6 +1955,17 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     if (M <= 1) return gemv_launch<BITS, 1, NG>(a, nw, s);
     if (M <= 2) return gemv_launch<BITS, 2, NG>(a, nw, s);
     if (M <= 4) return gemv_launch<BITS, 4, NG>(a, nw, s);
+    // Five to eight INT4 rows over a K of at most 2048 (a row quad or two per
+    // lane): two row groups of four, whose lanes reduce 32 accumulators
+    // (with the offset-binary decode) instead of 64; at that K the lane and
+    // wavefront reduction of 64 outweighs the lanes' share of the k loop.
+    // Measured on MI355X (INT4 g128, us): 2048->2048 at 8 rows 4.74-4.80 ->
+    // 4.39; 5632->2048 and 4096->4096 at 8 rows, and 2048->2048 at 16, were
+    // slower in groups of four.
+    if (BITS == 4 && M <= 8 && a.K <= 2048) {
+        a.Plog = 1;
+        return gemv_launch<BITS, 4, NG>(a, nw, s);
+    }
     const int64_t groups = (M + kRowsMax - 1) / kRowsMax;
     while ((int64_t)1 << a.Plog < groups) ++a.Plog;
     if (((int64_t)kRowsMax << a.Plog) > kGemvRowsMax) return hipErrorInvalidValue;

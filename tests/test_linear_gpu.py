@@ -249,6 +249,16 @@ def test_small_batch_int4(sgq, dev, oracle, synth, M, K, N, G):
     assert rel_err(y, yref) <= TOL
 
 
+# Five to eight INT4 rows over K <= 2048 run the GEMV as two row groups of four
+# (the second reading each strip's codes again): odd and even M, K past and on
+# a row-quad boundary, with and without bias.
+@pytest.mark.parametrize("M", [5, 7, 8])
+@pytest.mark.parametrize("K,N,G", [(2048, 2048, 128), (1023, 512, 64), (2048, 256, 32), (6, 64, 16)])
+def test_two_row_groups_of_four(sgq, dev, oracle, synth, M, K, N, G):
+    y, yref = _case(sgq, dev, oracle, synth, 4, M, K, N, G, 0, M % 2 == 1, 13)
+    assert rel_err(y, yref) <= TOL
+
+
 # INT8 strips ragged (N % 4 != 0), per-tensor and per-channel scales.
 @pytest.mark.parametrize("M", [2, 7, 13, 16])
 @pytest.mark.parametrize("K,N,scheme", [(1000, 70, 1), (4099, 30, 0), (333, 1000, 1), (64, 17, 0), (6000, 256, 1)])
