@@ -358,9 +358,10 @@ def measured_traffic(config: str):
 
 
 def csrc_digest() -> str:
-    """A digest of the library's kernel sources (soverign-grad_amd/csrc): a
-    committed profile records the digest of the build it measured, so a
-    profile of other kernels is never reported as this build's."""
+    """A digest of the library's kernel sources (soverign-grad_amd/csrc) and
+    of the Makefile that sets their compiler flags: a committed profile
+    records the digest of the build it measured, so a profile of other
+    kernels is never reported as this build's."""
     import hashlib
 
     h = hashlib.sha256()
@@ -368,6 +369,9 @@ def csrc_digest() -> str:
         if f.suffix in (".hip", ".h"):
             h.update(f.name.encode())
             h.update(f.read_bytes())
+    mk = ROOT / "soverign-grad_amd" / "Makefile"
+    h.update(b"Makefile")
+    h.update(mk.read_bytes())
     return h.hexdigest()[:16]
 
 
