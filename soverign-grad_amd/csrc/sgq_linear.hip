@@ -1178,6 +1178,38 @@ struct SkinnyArgs {
     int xlog;     // log2 of the device's XCD count
 };
 
+// What the skinny kernels' prologues need before their first loads travels
+// ahead of the SkinnyArgs copy as scalar kernel arguments, which gfx950
+// preloads into SGPRs (as for k_gemv: a by-value struct is never preloaded).
+// Kpad is 4 * RQ; pk packs the XCD shift (bits 0-7), the scale-column
+// divider's shift (8-15) and log2 of the K ranges (16-23).
+struct SkinnyHot {
+    const float* x;
+    const uint4* W0;
+    const float* S0;
+    int M, K, RQ, nblk, pk;
+    uint32_t wpcm;
+    int sbs;
+};
+inline SkinnyHot skinny_hot(const SkinnyArgs& a) {
+    SkinnyHot h;
+    h.x = a.x, h.W0 = a.W[0], h.S0 = a.SC[0];
+    h.M = a.M, h.K = a.K, h.RQ = a.RQ, h.nblk = a.nblk;
+    h.pk = a.xlog | (a.wpc.l << 8) | (a.slog << 16);
+    h.wpcm = a.wpc.m;
+    h.sbs = a.sbs;
+    return h;
+}
+#define SGQ_SKINNY_HOT_PARAMS                                                                                    \
+    const float *__restrict__ hx, const uint4 *__restrict__ hW0, const float *__restrict__ hS0, int hM, int K, \
+        int RQ, int nblk, int pk, uint32_t wpcm, int sbs
+#define SGQ_SKINNY_HOT_ARGS(h) h.x, h.W0, h.S0, h.M, h.K, h.RQ, h.nblk, h.pk, h.wpcm, h.sbs
+__device__ __forceinline__ FastDiv fastdiv_of(uint32_t m, int l) {
+    FastDiv f;
+    f.m = m, f.l = l;
+    return f;
+}
+
 // The whole-K form for one row block (5..16 rows over wide weights, no K
 // split): NW = 16 wavefronts take 32-row k blocks in turn, U of them per
 // batch of loads, and every load of a batch is issued before the first is
@@ -1200,39 +1232,43 @@ struct SkinnyArgs {
 // lane n the upper half of its operand.  The bf16 planes are the same bits as
 // without HALF; A rows 8..15 then hold copies whose outputs are never read.
 template <int NW, int U, int C, int NG, bool XA, bool NORM, bool HALF>
-__global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
+__global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
-    const int K = a.K;
-    const int vv = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
-    const int wt = NG == 1 ? a.wgd.div(vv) : 0;  // weight of the side-by-side set
+    const int Kpad = 4 * RQ;
+    // One weight without the norm (every linear call): the preloaded
+    // pointers alone, so that no select waits for the SkinnyArgs copy.
+    constexpr bool ONE = NG == 1 && !NORM;
+    const int vv = xcd_swizzle(blockIdx.x, nblk, pk & 255);
+    const int wt = (NG == 1 && !ONE) ? a.wgd.div(vv) : 0;  // weight of the side-by-side set
     const int v = vv - wt * a.wgpw;
     const int blk0 = v * C;  // first column block
-    const int sc = a.wpc.div(v);
+    const int sc = fastdiv_of(wpcm, (pk >> 8) & 255).div(v);
     const uint4* Wq[NG];
     const float* SCq[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        Wq[q] = a.W[NG == 1 ? wt : q];
-        SCq[q] = a.SC[NG == 1 ? wt : q];
+        const int wi = NG == 1 ? wt : q;
+        Wq[q] = (ONE || wi == 0) ? hW0 : a.W[wi];
+        SCq[q] = (ONE || wi == 0) ? hS0 : a.SC[wi];
     }
     __amdgpu_buffer_rsrc_t rW[NG], rS[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        rW[q] = make_rsrc(Wq[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
-        rS[q] = make_rsrc(SCq[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
+        rW[q] = make_rsrc(Wq[q] + (int64_t)(2 * blk0) * RQ, (uint32_t)(2 * C) * (uint32_t)RQ * 16u);
+        rS[q] = make_rsrc(SCq[q] + (int64_t)sc * Kpad, (uint32_t)Kpad * 4u);
     }
-    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(hx, (uint32_t)hM * (uint32_t)K * 4u);
     __amdgpu_buffer_rsrc_t rG;
     if constexpr (NORM) rG = make_rsrc(a.gamma, (uint32_t)K * 4u);
     float sq = 0.0f;  // NORM: sum of x^2 of this lane's row over its k
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + 32 * g + 4 * e;
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * RQ * 16 + 32 * g + 4 * e;
     constexpr int XV = HALF ? 4 : 8;  // x values per lane and k block
     const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
-    const bool row_live = xr < a.M;
+    const bool row_live = xr < hM;
     const int xrow = xr * K * 4;
     const NibbleT tp = nibble_t(e);
     floatx4 acc[NG][C];
@@ -1240,7 +1276,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(const SkinnyArgs a) {
     for (int q = 0; q < NG; ++q)
 #pragma unroll
         for (int c = 0; c < C; ++c) acc[q][c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int nkb = (a.Kpad + 31) >> 5;
+    const int nkb = (Kpad + 31) >> 5;
     // K blocks kb0, kb0 + NW, ..., U of them per batch.  A block past the end
     // reads x and the scales as zeros (its code dwords are whatever follows
     // and are multiplied by zero), so partial batches need no branch.
@@ -1409,23 +1445,23 @@ struct SkinnyRegs {
 // t = 0..3 of row n and lane n + 8 quads t = 4..7 of the same row; a
 // row_ror:8 exchange completes each A operand (the same bf16 planes).
 template <int NW, int C, int NG, bool XA, int MB, bool SPLIT, bool HALF>
-__global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
+__global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, const SkinnyArgs a) {
     static_assert(!HALF || MB == 1, "the half-row form has one row block");
     constexpr int XT = HALF ? 4 : 8;  // x quads per lane, row block and super-block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
     const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
-    const int K = a.K;
+    const int Kpad = 4 * RQ, slog = (pk >> 16) & 255;
     // Workgroup v: K range v % S of column group v / S (the ranges of one
     // column group are neighbours, so they share an XCD's L2 for the scales).
-    const int v = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);
-    const int split = SPLIT ? (v & ((1 << a.slog) - 1)) : 0;
-    const int cgrp = SPLIT ? (v >> a.slog) : v;
+    const int v = xcd_swizzle(blockIdx.x, nblk, pk & 255);
+    const int split = SPLIT ? (v & ((1 << slog) - 1)) : 0;
+    const int cgrp = SPLIT ? (v >> slog) : v;
     const int blk0 = cgrp * C;  // first column block
-    const int sc = a.wpc.div(cgrp);
-    const int nsb = (a.Kpad + kSkinnySB - 1) / kSkinnySB;
-    const int sb_lo = SPLIT ? split * a.sbs : 0;
-    const int sb_hi = SPLIT ? min(nsb, sb_lo + a.sbs) : nsb;
+    const int sc = fastdiv_of(wpcm, (pk >> 8) & 255).div(cgrp);
+    const int nsb = (Kpad + kSkinnySB - 1) / kSkinnySB;
+    const int sb_lo = SPLIT ? split * sbs : 0;
+    const int sb_hi = SPLIT ? min(nsb, sb_lo + sbs) : nsb;
     const int row0 = sb_lo * kSkinnySB;  // first row of the range
 
     // The range's scales (rows row0 .. row0 + rows - 1 of the scale column,
@@ -1438,7 +1474,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     float4 sreg[NG][SCI];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.SC[q] + (int64_t)sc * a.Kpad, (uint32_t)a.Kpad * 4u);
+        const __amdgpu_buffer_rsrc_t rS = make_rsrc((q == 0 ? hS0 : a.SC[q]) + (int64_t)sc * Kpad, (uint32_t)Kpad * 4u);
 #pragma unroll
         for (int it = 0; it < SCI; ++it) {
             const int r4 = threadIdx.x + it * NW * 64;
@@ -1449,17 +1485,17 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(const SkinnyArgs a) {
     __amdgpu_buffer_rsrc_t rW[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q)
-        rW[q] = make_rsrc(a.W[q] + (int64_t)(2 * blk0) * a.RQ, (uint32_t)(2 * C) * (uint32_t)a.RQ * 16u);
-    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)K * 4u);
+        rW[q] = make_rsrc((q == 0 ? hW0 : a.W[q]) + (int64_t)(2 * blk0) * RQ, (uint32_t)(2 * C) * (uint32_t)RQ * 16u);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(hx, (uint32_t)hM * (uint32_t)K * 4u);
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * a.RQ * 16 + (16 * e + 4 * g) * 4;
+    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * RQ * 16 + (16 * e + 4 * g) * 4;
     const int xr = HALF ? (n & 7) : n, toff = HALF ? 4 * (n >> 3) : 0;
     bool row_live[MB];
     int xrow[MB];
 #pragma unroll
     for (int b = 0; b < MB; ++b) {
-        row_live[b] = xr + 16 * b < a.M;
+        row_live[b] = xr + 16 * b < hM;
         xrow[b] = row_live[b] ? (xr + 16 * b) * K * 4 : 0;
     }
     const NibbleT tp = nibble_t(e);
@@ -1663,35 +1699,58 @@ struct Skinny8Args {
     int nblk;
     int xlog;  // log2 of the device's XCD count
 };
+// k_skinny8's prologue fields as preloaded scalar arguments (as SkinnyHot):
+// Kpad is 4 * RQ; pk packs the XCD shift (bits 0-7) and the column-group
+// divider's shift (8-15).
+struct Skinny8Hot {
+    const float* x;
+    const uint4* W;
+    const float* S;
+    int M, K, RQ, NS, nblk, pk;
+    uint32_t cgdm;
+    int ncg;
+};
+inline Skinny8Hot skinny8_hot(const Skinny8Args& a) {
+    Skinny8Hot h;
+    h.x = a.x, h.W = a.W, h.S = a.S;
+    h.M = a.M, h.K = a.K, h.RQ = a.RQ, h.NS = a.NS, h.nblk = a.nblk;
+    h.pk = a.xlog | (a.cgd.l << 8);
+    h.cgdm = a.cgd.m;
+    h.ncg = a.ncg;
+    return h;
+}
 
 // HALF (one row block, M <= 8): lane n < 8 loads and splits k 8g .. 8g + 3
 // of row n, lane n + 8 k 8g + 4 .. 8g + 7 of the same row, and a row_ror:8
 // exchange completes each A operand (the same bf16 planes), as in k_skinny3.
 template <int NW, int U, int C, int MB, bool PT, bool XA, bool HALF>
-__global__ __launch_bounds__(NW * 64) void k_skinny8(const Skinny8Args a) {
+__global__ __launch_bounds__(NW * 64) void k_skinny8(const float* __restrict__ hx, const uint4* __restrict__ hW,
+                                                        const float* __restrict__ hS, int hM, int K, int RQ, int NS,
+                                                        int nblk, int pk, uint32_t cgdm, int ncg,
+                                                        const Skinny8Args a) {
     static_assert(!HALF || MB == 1, "the half-row form has one row block");
     constexpr int XV = HALF ? 4 : 8;  // x values per lane, row block and k block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const int K = a.K;
-    const int v = xcd_swizzle(blockIdx.x, a.nblk, a.xlog);  // row tile major: an XCD's workgroups share x rows
-    const int rt = a.cgd.div(v), cg = v - rt * a.ncg;
+    const int Kpad = 4 * RQ;
+    const int v = xcd_swizzle(blockIdx.x, nblk, pk & 255);  // row tile major: an XCD's workgroups share x rows
+    const int rt = fastdiv_of(cgdm, (pk >> 8) & 255).div(v), cg = v - rt * ncg;
     const int m0 = rt * 16 * MB, s0 = cg * 4 * C;
-    const int mrows = min(16 * MB, a.M - m0), nstr = min(4 * C, a.NS - s0);
+    const int mrows = min(16 * MB, hM - m0), nstr = min(4 * C, NS - s0);
     // Rows past M and strips past NS lie past the ends of these buffers and read as zeros.
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(a.W + (int64_t)s0 * a.RQ, (uint32_t)nstr * (uint32_t)a.RQ * 16u);
-    const __amdgpu_buffer_rsrc_t rX = make_rsrc(a.x + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
-    const __amdgpu_buffer_rsrc_t rS = make_rsrc(a.S, PT ? 4u : (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(hW + (int64_t)s0 * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
+    const __amdgpu_buffer_rsrc_t rX = make_rsrc(hx + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4u);
+    const __amdgpu_buffer_rsrc_t rS = make_rsrc(hS, PT ? 4u : (uint32_t)K * 4u);
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = ((4 * c + (n >> 2)) * a.RQ + 2 * g) * 16 + (n & 3) * 4;
+    for (int c = 0; c < C; ++c) wv[c] = ((4 * c + (n >> 2)) * RQ + 2 * g) * 16 + (n & 3) * 4;
     const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
     floatx4 acc[MB][C];
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int c = 0; c < C; ++c) acc[b][c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int nkb = (a.Kpad + 31) >> 5;
+    const int nkb = (Kpad + 31) >> 5;
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][C][2];
         float xv[U][MB][XV], sv[U][XV];
@@ -2046,6 +2105,10 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     // Side-by-side weights, a row stride and the folded RMSNorm: whole-K form only.
     const bool plain = ex.nw == 1 && ex.ldy == N && !ex.gamma;
     if ((!plain && form != 0) || ex.nw < 1 || ex.nw > 3 || (NG == 2 && ex.nw != 1)) return hipErrorInvalidValue;
+    // Side-by-side weights come with the norm (the LLaMA block's q, k and v):
+    // the plain kernels take their one weight from the preloaded arguments.
+    if (ex.nw != 1 && !ex.gamma) return hipErrorInvalidValue;
+    if (g.Kpad != 4 * g.RQ) return hipErrorInvalidValue;  // SkinnyHot carries RQ only
     SkinnyArgs a{};
     a.x = x;
     a.M = (int)M;
@@ -2078,11 +2141,12 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
         if constexpr (MB == 1) {
             constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
             a.nblk *= ex.nw;
+            const SkinnyHot h = skinny_hot(a);
 #define SGQ_SKINNY3(NORM_)                                                                                 \
     if (M <= 8)                                                                                            \
-        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, true><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a); \
+        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, true><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a); \
     else                                                                                                   \
-        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+        k_skinny3<kSkinnyWholeKWaves, U, C, NG, XA, NORM_, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a);
             if (ex.gamma) {
                 // The norm-fused form keeps two column blocks (register budget).
                 if constexpr (C == 2) {
@@ -2099,14 +2163,15 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
         return hipErrorInvalidValue;
     }
     const bool half = MB == 1 && M <= 8;
+    const SkinnyHot h = skinny_hot(a);
     if (S > 1 && half)
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a);
     else if (S > 1)
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, true, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a);
     else if (half)
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, MB == 1><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a);
     else
-        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(a);
+        k_skinny_sb<kSkinnyWaves, C, NG, XA, MB, false, false><<<a.nblk, kSkinnyWaves * 64, 0, s>>>(SGQ_SKINNY_HOT_ARGS(h), a);
     if (S > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -2118,6 +2183,8 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     }
     return hipGetLastError();
 }
+#undef SGQ_SKINNY_HOT_ARGS
+#undef SGQ_SKINNY_HOT_PARAMS
 
 template <int NG>
 hipError_t skinny_dispatch(const SkinnyPlan& p, const float* x, int64_t M, int64_t K, int64_t N,
@@ -2169,10 +2236,12 @@ hipError_t skinny8_launch(const float* x, int64_t M, int64_t K, int64_t N, const
     a.nblk = (int)(ceil_div(M, 16 * MB) * a.ncg);
     a.xlog = xcd_log2(device_xcds(s));
     constexpr int U = MB == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU
+    if (g.Kpad != 4 * g.RQ) return hipErrorInvalidValue;  // Skinny8Hot carries RQ only
+    const Skinny8Hot h = skinny8_hot(a);
     if (MB == 1 && M <= 8)
-        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, MB == 1><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, MB == 1><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(h.x, h.W, h.S, h.M, h.K, h.RQ, h.NS, h.nblk, h.pk, h.cgdm, h.ncg, a);
     else
-        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(a);
+        k_skinny8<kSkinnyWholeKWaves, U, C, MB, PT, XA, false><<<a.nblk, kSkinnyWholeKWaves * 64, 0, s>>>(h.x, h.W, h.S, h.M, h.K, h.RQ, h.NS, h.nblk, h.pk, h.cgdm, h.ncg, a);
     return hipGetLastError();
 }
 
