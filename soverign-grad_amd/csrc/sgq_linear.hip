@@ -858,11 +858,32 @@ using G3Tile = G3Shape<2, 4, 2, 4>;  // 128 x 128, 4 wavefronts: INT4
 using G3Rows32 = G3Shape<1, 2, 2, 4>;  // 32 x 128, 2 wavefronts
 using G3Rows64 = G3Shape<2, 2, 2, 4>;  // 64 x 128, 4 wavefronts
 
+// Arguments of one k_gemm3 launch, passed as one struct: the build preloads
+// leading scalar kernel arguments into SGPRs, which the latency-bound GEMV and
+// skinny kernels gain from and a GEMM of this length does not need.
+struct Gemm3Args {
+    const float* x;
+    int M, K, N;
+    const uint4* W;
+    const float* S;
+    int mode, Kpad, RQ, NS, KS, sps;
+    const float* bias;
+    float* y;
+    float* part;
+    int xr, xlog;
+};
+
 template <int BITS, bool KALIGN4, bool PT, class SH>
-__global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(
-    const float* __restrict__ x, int M, int K, int N, const uint4* __restrict__ W, const float* __restrict__ S,
-    int mode, int Kpad, int RQ, int NS, int KS, int sps, const float* __restrict__ bias, float* __restrict__ y,
-    float* __restrict__ part, int xr, int xlog) {
+__global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE))) void k_gemm3(const Gemm3Args ga) {
+    const float* __restrict__ x = ga.x;
+    const int M = ga.M, K = ga.K, N = ga.N;
+    const uint4* __restrict__ W = ga.W;
+    const float* __restrict__ S = ga.S;
+    const int mode = ga.mode, Kpad = ga.Kpad, RQ = ga.RQ, NS = ga.NS, KS = ga.KS, sps = ga.sps;
+    const float* __restrict__ bias = ga.bias;
+    float* __restrict__ y = ga.y;
+    float* __restrict__ part = ga.part;
+    const int xr = ga.xr, xlog = ga.xlog;
     // mode: INT8 -> per-tensor flag (also the template flag PT, so that no
     // stage holds a branch); INT4 -> strips per scale column (a multiple of
     // 16: one scale column per 128-column tile).  Workgroup b computes split
@@ -2545,9 +2566,9 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
     const bool pt = BITS == 8 && mode;
     using Big = typename std::conditional<BITS == 8, G3Wide, G3Tile>::type;
 #define SGQ_GEMM3(SH, A4, PT_)                                                                                 \
-    k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(x, (int)M, (int)K, (int)N,              \
-                                                                    (const uint4*)packed, sc, mode, (int)Kpad, \
-                                                                    (int)RQ, (int)NS, p.KS, p.sps, bias, y, part, xr, xlog)
+    k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(Gemm3Args{                                \
+        x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode, (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, \
+        y, part, xr, xlog})
 #define SGQ_GEMM3_SHAPE(SH)               \
     if (k4 && pt)                         \
         SGQ_GEMM3(SH, true, true);        \
