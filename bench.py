@@ -247,6 +247,7 @@ class Case:
 
 
 # Weights of the M=1 size sweep (INT4 g128, K x N): C2's 9 MB up to 285 MB.
+GEMV_PROBE = (128, 4096)  # C2's 4096 columns (256 workgroups) over 128 rows of K: 0.3 MB per call
 GEMV_SWEEP = [(4096, 4096), (4096, 8192), (4096, 11008), (4096, 16384), (8192, 16384), (8192, 28672),
               (4096, 65536), (8192, 65536)]
 
@@ -262,13 +263,16 @@ def gemv_size_sweep(pkg, dev, steps: int) -> dict:
     shape's output is checked against x @ dequantize(W) in fp64, where
     dequantize is the library's own bit-exact GPU dequantize.  The fit
     t = t0 + bytes / bw over all shapes separates the per-call fixed cost
-    from the streaming rate."""
+    from the streaming rate.  fixed_cost_probe is the same forward on
+    GEMV_PROBE (C2's grid of 256 workgroups over 0.3 MB): what a call costs
+    with next to no bytes to stream, measured directly (not in the fit)."""
     import torch
 
     lib = pkg.load_library()
     gen = torch.Generator(device=dev)
     rows = []
-    for K, N in GEMV_SWEEP:
+
+    def run_shape(K, N):
         G = 128
         nbytes = K * N // 2 + K * N // G * 4 + 4 * K + 4 * N
         copies = max(2, -(-300_000_000 // nbytes))
@@ -324,12 +328,18 @@ def gemv_size_sweep(pkg, dev, steps: int) -> dict:
         log(f"[bench] gemv sweep {K}x{N}: {us:.3f} us/call, {nbytes / us / 1e3:.1f} GB/s")
         del g, sweep, packed, dsc, qw, ws
         torch.cuda.empty_cache()
+        return rows.pop() if (K, N) == GEMV_PROBE else rows[-1]
+
+    for K, N in GEMV_SWEEP:
+        run_shape(K, N)
+    probe = run_shape(*GEMV_PROBE)
     b = np.array([r["bytes"] for r in rows], dtype=np.float64)
     t = np.array([r["us_per_call"] for r in rows], dtype=np.float64)
     slope, t0 = np.polyfit(b, t, 1)
     return {"workload": "INT4 g128 QuantizedLinear forward, M=1, over weights of 9 MB to 285 MB",
             "launch": f"one hipGraph of {steps} calls per shape, median of 5 replays", "shapes": rows,
-            "fit_t0_us": round(float(t0), 3), "fit_GB_s": round(float(1e-3 / slope), 1)}
+            "fit_t0_us": round(float(t0), 3), "fit_GB_s": round(float(1e-3 / slope), 1),
+            "fixed_cost_probe": probe}
 
 
 def calibration_copy(dev, mib: int = 64) -> None:
