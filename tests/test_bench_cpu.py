@@ -79,6 +79,30 @@ def test_committed_profiles_count_only_for_the_kernels_they_measured():
     assert "rocprof_historical" in bench.rocprof_fields({"avg_ns": 1}, 1.0, 1.0, lambda v: v)
 
 
+def test_kernel_digest_covers_sources_and_compiler_flags(tmp_path, monkeypatch):
+    """The digest changes with any kernel source and with the Makefile, whose
+    device-code flags (kernel-argument preloading among them) change the
+    kernels' machine code as much as a source edit does."""
+    import shutil
+
+    import bench
+
+    pkg = tmp_path / "soverign-grad_amd"
+    shutil.copytree(ROOT / "soverign-grad_amd" / "csrc", pkg / "csrc")
+    shutil.copy(ROOT / "soverign-grad_amd" / "Makefile", pkg / "Makefile")
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    d0 = bench.csrc_digest()
+    assert d0 == bench.csrc_digest()
+    mk = pkg / "Makefile"
+    mk.write_text(mk.read_text().replace("-amdgpu-kernarg-preload-count=16", "-amdgpu-kernarg-preload-count=0"))
+    d1 = bench.csrc_digest()
+    assert d1 != d0
+    src = pkg / "csrc" / "sgq_linear.hip"
+    src.write_text(src.read_text() + "\n")
+    assert bench.csrc_digest() not in (d0, d1)
+    assert "-amdgpu-kernarg-preload-count=16" in (ROOT / "soverign-grad_amd" / "Makefile").read_text()
+
+
 def _write_csv(path, header, rows):
     import csv
 
