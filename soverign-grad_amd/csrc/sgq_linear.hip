@@ -2086,6 +2086,16 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
         a.Plog = 1;
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }
+    // INT4 at 5..16 rows whose row groups of eight would leave fewer
+    // workgroups than compute units (narrow weights): groups of four, twice
+    // the workgroups.  Measured on MI355X (us): 8192->1024 at 8 rows 8.34-8.44
+    // -> 5.74-5.79, 2048->512 at 16 rows 4.10-4.12 -> 3.23-3.34; where groups
+    // of eight already fill the device, groups of four were equal or slower
+    // (5632->2048 and 4096->4096 at 8 rows, 2048->2048 at 12 and 16).
+    if (BITS == 4 && M <= 16 && (((int64_t)nw * a.NS) << (M > 8 ? 1 : 0)) < a.cus) {
+        a.Plog = M > 8 ? 2 : 1;
+        return gemv_launch<BITS, 4, NG>(a, nw, s);
+    }
     const int64_t groups = (M + kRowsMax - 1) / kRowsMax;
     while ((int64_t)1 << a.Plog < groups) ++a.Plog;
     if (((int64_t)kRowsMax << a.Plog) > kGemvRowsMax) return hipErrorInvalidValue;

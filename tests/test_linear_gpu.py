@@ -259,6 +259,16 @@ def test_two_row_groups_of_four(sgq, dev, oracle, synth, M, K, N, G):
     assert rel_err(y, yref) <= TOL
 
 
+# Five to sixteen INT4 rows over narrow weights (row groups of eight would leave
+# fewer workgroups than compute units) run the GEMV in row groups of four:
+# K past 2048, ragged K, a single-strip-group N, with and without bias.
+@pytest.mark.parametrize("M", [5, 8, 9, 12, 16])
+@pytest.mark.parametrize("K,N,G", [(8192, 1024, 128), (4100, 256, 128), (2048, 512, 128), (3001, 64, 32)])
+def test_row_groups_of_four_on_narrow_weights(sgq, dev, oracle, synth, M, K, N, G):
+    y, yref = _case(sgq, dev, oracle, synth, 4, M, K, N, G, 0, M % 2 == 0, 17)
+    assert rel_err(y, yref) <= TOL
+
+
 # INT8 strips ragged (N % 4 != 0), per-tensor and per-channel scales.
 @pytest.mark.parametrize("M", [2, 7, 13, 16])
 @pytest.mark.parametrize("K,N,scheme", [(1000, 70, 1), (4099, 30, 0), (333, 1000, 1), (64, 17, 0), (6000, 256, 1)])
