@@ -2074,7 +2074,20 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
     a.Plog = 0;
     if (M <= 1) return gemv_launch<BITS, 1, NG>(a, nw, s);
     if (M <= 2) return gemv_launch<BITS, 2, NG>(a, nw, s);
-    if (M <= 4) return gemv_launch<BITS, 4, NG>(a, nw, s);
+    if (M <= 4) {
+        // Three or four rows over a weight of fewer strips than compute units:
+        // two row groups of two, twice the workgroups.  Measured on MI355X
+        // (us): INT4 8192->1024 at 4 rows 5.81-5.98 -> 4.58-4.66, 4096->512 at
+        // 3 rows 4.20-4.28 -> 3.35-3.38, 2048->512 at 4 rows 3.31-3.32 ->
+        // 2.91-2.97; INT8 4096->512 at 4 rows 3.45-3.56 -> 3.05-3.19.  Two rows
+        // as two groups of one measured equal (INT4 8192->1024, INT8
+        // 4096->512), and 4096->11008 (1376 strips) keeps one group.
+        if (M >= 3 && (int64_t)nw * a.NS < a.cus) {
+            a.Plog = 1;
+            return gemv_launch<BITS, 2, NG>(a, nw, s);
+        }
+        return gemv_launch<BITS, 4, NG>(a, nw, s);
+    }
     // Five to eight INT4 rows over a K of at most 2048 (a row quad or two per
     // lane): two row groups of four, whose lanes reduce 32 accumulators
     // (with the offset-binary decode) instead of 64; at that K the lane and
@@ -2086,13 +2099,14 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
         a.Plog = 1;
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }
-    // INT4 at 5..16 rows whose row groups of eight would leave fewer
-    // workgroups than compute units (narrow weights): groups of four, twice
-    // the workgroups.  Measured on MI355X (us): 8192->1024 at 8 rows 8.34-8.44
-    // -> 5.74-5.79, 2048->512 at 16 rows 4.10-4.12 -> 3.23-3.34; where groups
-    // of eight already fill the device, groups of four were equal or slower
-    // (5632->2048 and 4096->4096 at 8 rows, 2048->2048 at 12 and 16).
-    if (BITS == 4 && M <= 16 && (((int64_t)nw * a.NS) << (M > 8 ? 1 : 0)) < a.cus) {
+    // 5..16 rows whose row groups of eight would leave fewer workgroups than
+    // compute units (narrow weights): groups of four, twice the workgroups.
+    // Measured on MI355X (us): INT4 8192->1024 at 8 rows 8.34-8.44 -> 5.74-5.79,
+    // 2048->512 at 16 rows 4.10-4.12 -> 3.23-3.34; INT8 4096->512 at 8 rows
+    // 4.48-4.60 -> 3.29-3.31.  Where groups of eight already fill the device,
+    // groups of four were equal or slower (INT4 5632->2048 and 4096->4096 at 8
+    // rows, 2048->2048 at 12 and 16).
+    if (M <= 16 && (((int64_t)nw * a.NS) << (M > 8 ? 1 : 0)) < a.cus) {
         a.Plog = M > 8 ? 2 : 1;
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }

@@ -717,9 +717,15 @@ static void test_packed_cache_invalidation() {
                 SG_TEST_HIP(hipMemcpy(m.q_weight.qdata.data(), p, sizeof(float) * (size_t)q.numel(),
                                       hipMemcpyHostToDevice));
         }
+        // To rounding: the GEMV's one- and two-row groups decode offset-binary
+        // codes (sum of xs * (q + 8), less 8 * sum of xs), whose rounding is not
+        // symmetric in q bit for bit.
         const auto y2 = host(m.forward(x));
-        bool flipped = true;
-        for (size_t i = 0; i < y0.size(); ++i) flipped = flipped && y2[i] == -y1[i];
+        double ymax = 0.0;
+        for (float v : y1) ymax = std::max(ymax, (double)std::fabs(v));
+        bool flipped = ymax > 0.0;
+        for (size_t i = 0; i < y0.size(); ++i)
+            flipped = flipped && std::fabs((double)y2[i] + (double)y1[i]) <= 1e-6 * ymax;
         CHECK(flipped);
         // A replaced scales tensor (new impl, maybe at a recycled address) is seen.
         m.q_weight.scales = m.q_weight.scales.clone();
