@@ -2088,14 +2088,16 @@ hipError_t gemv_dispatch(GemvArgs a, int64_t M, int nw, hipStream_t s) {
         }
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }
-    // Five to eight INT4 rows over a K of at most 2048 (a row quad or two per
-    // lane): two row groups of four, whose lanes reduce 32 accumulators
-    // (with the offset-binary decode) instead of 64; at that K the lane and
-    // wavefront reduction of 64 outweighs the lanes' share of the k loop.
-    // Measured on MI355X (INT4 g128, us): 2048->2048 at 8 rows 4.74-4.80 ->
-    // 4.39; 5632->2048 and 4096->4096 at 8 rows, and 2048->2048 at 16, were
-    // slower in groups of four.
-    if (BITS == 4 && M <= 8 && a.K <= 2048) {
+    // Five to eight rows over a K of at most 2048 (a row quad or two per
+    // lane): two row groups of four, whose lanes reduce half as many
+    // accumulators (INT4 32 instead of 64, with the offset-binary decode;
+    // INT8 16 instead of 32); at that K the lane and wavefront reduction
+    // outweighs the lanes' share of the k loop.  Measured on MI355X (us): INT4
+    // g128 2048->2048 at 8 rows 4.74-4.80 -> 4.39; INT8 2048->2048 at 8 rows
+    // 4.81-4.83 -> 4.11-4.16, 1024->1024 at 8 rows 2.99-3.01 -> 2.69-2.70,
+    // 2048->1024 at 6 rows 3.59-3.62 -> 3.14-3.16; INT4 5632->2048 and
+    // 4096->4096 at 8 rows, and 2048->2048 at 16, were slower in groups of four.
+    if (M <= 8 && a.K <= 2048) {
         a.Plog = 1;
         return gemv_launch<BITS, 4, NG>(a, nw, s);
     }

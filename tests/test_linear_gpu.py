@@ -261,8 +261,9 @@ def test_two_row_groups_of_four(sgq, dev, oracle, synth, M, K, N, G):
 
 # Two to sixteen rows over narrow weights (fewer workgroups than compute units
 # in the default grouping) run the GEMV in more, smaller row groups: two groups
-# of two at three and four rows, groups of four from five.  K past 2048,
-# ragged K, a single-strip-group N, with and without bias; INT4 and INT8.
+# of two at three and four rows, groups of four from five (and, at five to
+# eight rows, over any K <= 2048).  K past 2048, ragged K, a single-strip-group
+# N, with and without bias; INT4 and INT8.
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 9, 12, 16])
 @pytest.mark.parametrize("K,N,G", [(8192, 1024, 128), (4100, 256, 128), (2048, 512, 128), (3001, 64, 32)])
 def test_row_groups_on_narrow_weights(sgq, dev, oracle, synth, M, K, N, G):
@@ -270,8 +271,9 @@ def test_row_groups_on_narrow_weights(sgq, dev, oracle, synth, M, K, N, G):
     assert rel_err(y, yref) <= TOL
 
 
-@pytest.mark.parametrize("M", [2, 4, 6, 8, 12])
-@pytest.mark.parametrize("K,N,scheme", [(4096, 512, 0), (2051, 300, 1), (8192, 1020, 0)])
+@pytest.mark.parametrize("M", [2, 4, 5, 6, 8, 12])
+@pytest.mark.parametrize("K,N,scheme", [(4096, 512, 0), (2051, 300, 1), (8192, 1020, 0), (2048, 2048, 0),
+                                        (1023, 500, 1)])
 def test_row_groups_on_narrow_weights_int8(sgq, dev, oracle, synth, M, K, N, scheme):
     y, yref = _case(sgq, dev, oracle, synth, 8, M, K, N, 0, scheme, M % 4 == 0, 19)
     assert rel_err(y, yref) <= TOL
