@@ -25,6 +25,20 @@
 // because group % 8 == 0 and N % 8 == 0 keep every strip inside one group).
 // INT4 flat (any other shape) is the flattened tensor with two codes per
 // byte, element i in byte i/2, low nibble first.
+//
+// INT4 strip-major buffers carry a second copy of the codes after the strips,
+// at byte koct_off() (the strips' bytes rounded up to 256): k-octet blocks.
+// The weight is cut into column blocks of 16 (two strips; NB = ceil(NS / 2))
+// and, within each, k blocks of 32 rows (KB = ceil(Kpad / 32)).  Block (cb, kb)
+// is 256 bytes at koct_off() + (cb * KB + kb) * 256, so a column block is one
+// contiguous run over K.  Dword t = 16 * g + c of a block (g = 0..3, c =
+// 0..15) holds column 16 * cb + c at rows 32 * kb + 8 * g + i in nibble i;
+// rows past Kpad and columns past N are code 0.  A dword is exactly the B
+// operand of lane t of a v_mfma_f32_16x16x32_bf16 (eight consecutive k of one
+// column) and a block that MFMA's whole B tile, so the whole-K skinny MFMA
+// kernel loads one dword per lane with no exchange between lanes.  The GEMV
+// stays on the strips: at one batch row it needs one x * s per code dword
+// there, eight per dword here.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -82,7 +96,13 @@ struct I4Geom {
         nsc = tiled ? ceil_div(NS, spc) : 0;
     }
     int64_t chunks() const { return tiled ? NS * RQ : 0; }
-    int64_t bytes() const { return tiled ? chunks() * 16 : ceil_div(K * N, 2); }
+    // The k-octet copy (strip-major only): KB k blocks of 32 rows, NB column
+    // blocks of 16, starting at byte koct_off().
+    int64_t KB() const { return ceil_div(Kpad, 32); }
+    int64_t NB() const { return ceil_div(NS, 2); }
+    int64_t koct_off() const { return round_up(chunks() * 16, 256); }
+    int64_t koct_bytes() const { return tiled ? NB() * KB() * 256 : 0; }
+    int64_t bytes() const { return tiled ? koct_off() + koct_bytes() : ceil_div(K * N, 2); }
     int64_t devscale_count() const { return tiled ? nsc * Kpad : 0; }
 };
 

@@ -1197,20 +1197,22 @@ struct SkinnyArgs {
     const float* gamma;
     float eps;
     int xlog;     // log2 of the device's XCD count
+    int ko;       // byte offset / 256 of each weight's k-octet copy (I4Geom::koct_off)
 };
 
 // What the skinny kernels' prologues need before their first loads travels
 // ahead of the SkinnyArgs copy as scalar kernel arguments, which gfx950
 // preloads into SGPRs (as for k_gemv: a by-value struct is never preloaded).
 // Kpad is 4 * RQ; pk packs the XCD shift (bits 0-7), the scale-column
-// divider's shift (8-15) and log2 of the K ranges (16-23).
+// divider's shift (8-15) and log2 of the K ranges (16-23); ko is the k-octet
+// copy's offset (fourteen dwords in all, what gfx950 preloads).
 struct SkinnyHot {
     const float* x;
     const uint4* W0;
     const float* S0;
     int M, K, RQ, nblk, pk;
     uint32_t wpcm;
-    int sbs;
+    int sbs, ko;
 };
 inline SkinnyHot skinny_hot(const SkinnyArgs& a) {
     SkinnyHot h;
@@ -1219,12 +1221,13 @@ inline SkinnyHot skinny_hot(const SkinnyArgs& a) {
     h.pk = a.xlog | (a.wpc.l << 8) | (a.slog << 16);
     h.wpcm = a.wpc.m;
     h.sbs = a.sbs;
+    h.ko = a.ko;
     return h;
 }
 #define SGQ_SKINNY_HOT_PARAMS                                                                                    \
     const float *__restrict__ hx, const uint4 *__restrict__ hW0, const float *__restrict__ hS0, int hM, int K, \
-        int RQ, int nblk, int pk, uint32_t wpcm, int sbs
-#define SGQ_SKINNY_HOT_ARGS(h) h.x, h.W0, h.S0, h.M, h.K, h.RQ, h.nblk, h.pk, h.wpcm, h.sbs
+        int RQ, int nblk, int pk, uint32_t wpcm, int sbs, int ko
+#define SGQ_SKINNY_HOT_ARGS(h) h.x, h.W0, h.S0, h.M, h.K, h.RQ, h.nblk, h.pk, h.wpcm, h.sbs, h.ko
 __device__ __forceinline__ FastDiv fastdiv_of(uint32_t m, int l) {
     FastDiv f;
     f.m = m, f.l = l;
@@ -1234,9 +1237,11 @@ __device__ __forceinline__ FastDiv fastdiv_of(uint32_t m, int l) {
 // The whole-K form for one row block (5..16 rows over wide weights, no K
 // split): NW = 16 wavefronts take 32-row k blocks in turn, U of them per
 // batch of loads, and every load of a batch is issued before the first is
-// used.  Lane (g, e) of strip j loads one dword, row 8g + e of its strip in
-// k block kb, and an 8x8 nibble transpose leaves it with rows 8g .. 8g + 7 of
-// column e (its B operand); x and the scales are loaded per k block.  NG == 2:
+// used.  The codes come from the weight's k-octet copy: lane t of a wavefront
+// loads dword t of block (column block, kb), rows 8 (t >> 4) .. + 7 of column
+// t & 15, which is its B operand as it stands (256 contiguous bytes per
+// wavefront load, no exchange between lanes); x and the scales are loaded per
+// k block.  NG == 2:
 // the gated MLP, h = silu(gate + bias) * (up + bias2).  NG == 1 runs a.wgpw
 // workgroups per weight over nw weights of one shape side by side (a LLaMA
 // block's q, k and v).  XA: x rows are 16-byte aligned and K % 4 == 0 (float4
@@ -1256,8 +1261,8 @@ template <int NW, int U, int C, int NG, bool XA, bool NORM, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, const SkinnyArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int Kpad = 4 * RQ;
+    const int nkb = (Kpad + 31) >> 5;  // k blocks of 32 rows (KB of the k-octet copy)
     // One weight without the norm (every linear call): the preloaded
     // pointers alone, so that no select waits for the SkinnyArgs copy.
     constexpr bool ONE = NG == 1 && !NORM;
@@ -1277,7 +1282,9 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
     __amdgpu_buffer_rsrc_t rW[NG], rS[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-        rW[q] = make_rsrc(Wq[q] + (int64_t)(2 * blk0) * RQ, (uint32_t)(2 * C) * (uint32_t)RQ * 16u);
+        // Column blocks blk0 .. blk0 + C - 1 of the k-octet copy, C * nkb
+        // blocks of 256 bytes from block blk0 * nkb.
+        rW[q] = make_rsrc(Wq[q] + ((int64_t)ko + (int64_t)blk0 * nkb) * 16, (uint32_t)C * (uint32_t)nkb * 256u);
         rS[q] = make_rsrc(SCq[q] + (int64_t)sc * Kpad, (uint32_t)Kpad * 4u);
     }
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(hx, (uint32_t)hM * (uint32_t)K * 4u);
@@ -1286,21 +1293,20 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
     float sq = 0.0f;  // NORM: sum of x^2 of this lane's row over its k
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * RQ * 16 + 32 * g + 4 * e;
+    for (int c = 0; c < C; ++c) wv[c] = c * nkb * 256 + 4 * lane;
     constexpr int XV = HALF ? 4 : 8;  // x values per lane and k block
     const int xr = HALF ? (n & 7) : n, xk = HALF ? 4 * (n >> 3) : 0;
     const bool row_live = xr < hM;
     const int xrow = xr * K * 4;
-    const NibbleT tp = nibble_t(e);
     floatx4 acc[NG][C];
 #pragma unroll
     for (int q = 0; q < NG; ++q)
 #pragma unroll
         for (int c = 0; c < C; ++c) acc[q][c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int nkb = (Kpad + 31) >> 5;
     // K blocks kb0, kb0 + NW, ..., U of them per batch.  A block past the end
-    // reads x and the scales as zeros (its code dwords are whatever follows
-    // and are multiplied by zero), so partial batches need no branch.
+    // reads x and the scales as zeros (its code dwords are zeros past the
+    // range, else another column block's, multiplied by zero), so partial
+    // batches need no branch.
     for (int kb0 = wave; kb0 < nkb; kb0 += NW * U) {
         uint32_t w[U][NG][C];
         float xv[U][XV], sv[U][NG][XV], gv[NORM ? U : 1][XV];
@@ -1311,7 +1317,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
             for (int q = 0; q < NG; ++q)
 #pragma unroll
                 for (int c = 0; c < C; ++c)
-                    w[u][q][c] = buf_load4_stream(rW[q], wv[c], kb * 128);
+                    w[u][q][c] = buf_load4_stream(rW[q], wv[c], kb * 256);
             const int k0 = kb * 32 + 8 * g + xk;
 #pragma unroll
             for (int h = 0; h < XV / 4; ++h) {
@@ -1362,7 +1368,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
                 }
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
-                    const bf16x8 b = nibbles_bf16x16(nibble_transpose8(w[u][q][c], tp));
+                    const bf16x8 b = nibbles_bf16x16(w[u][q][c]);
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah), b, acc[q][c], 0, 0, 0);
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, am), b, acc[q][c], 0, 0, 0);
                     acc[q][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al), b, acc[q][c], 0, 0, 0);
@@ -1407,8 +1413,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
         for (int i = 0; i < OPT; ++i) {
             const int t = threadIdx.x + i * NW * 64;
             const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
-            const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
-            const int col = 8 * strip + el;
+            const int col = 16 * (blk0 + c) + sl;
+            const int strip = col >> 3, el = col & 7;
             float s = 0.0f;
             if (t < 256 * C && m < a.M && col < a.N) {
 #pragma unroll
@@ -1430,7 +1436,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
     for (int i = 0; i < OPT; ++i) {
         const int t = threadIdx.x + i * NW * 64;
         const int c = t >> 8, m = (t >> 4) & 15, sl = t & 15;
-        const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
+        const int col = 16 * (blk0 + c) + sl;
         if (t < 256 * C && m < a.M && col < a.N) {
             float r0 = o[0][i];
             if constexpr (NG == 2) r0 = silu_f32(o[0][i]) * o[1][i];
@@ -2184,6 +2190,7 @@ hipError_t skinny_launch(const float* x, int64_t M, int64_t K, int64_t N, const 
     a.sbs = (int)ceil_div(ceil_div(g.Kpad, kSkinnySB), S);
     a.nblk = (int)(g.NS / (2 * C)) << slog;  // skinny_plan: 2C divides spc, which divides NS
     a.xlog = xcd_log2(device_xcds(s));
+    a.ko = (int)(g.koct_off() / 256);
     if (form == 0) {
         if constexpr (MB == 1) {
             constexpr int U = NG == 1 ? 4 : 2;  // register budget of 16 wavefronts per CU

@@ -171,6 +171,34 @@ __global__ void k_pack_i4_tiled(const float* __restrict__ src, int from_codes, i
     }
 }
 
+// The k-octet copy of an INT4 strip-major weight, built from its strips: one
+// thread per dword t of block (cb, kb), column 16 cb + (t & 15), rows
+// 32 kb + 8 (t >> 4) .. + 7 in nibbles 0..7.  Strip dword (j, row k) is dword
+// 4 * (j * RQ + k / 4) + k % 4, column n of it nibble n % 8.  The first ngap
+// threads also zero the ngap dwords between the strips and the copy, so that
+// the whole buffer is a function of the codes.
+__global__ void k_koct_i4(const uint32_t* __restrict__ strips, int64_t N, int64_t Kpad, int64_t RQ, int64_t KB,
+                          int64_t ndw, uint32_t* __restrict__ koct, uint32_t* __restrict__ gap, int ngap) {
+    const int64_t t0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t0 < ngap) gap[t0] = 0u;
+    for (int64_t d = t0; d < ndw; d += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = d >> 6, t = d & 63;
+        const int64_t cb = blk / KB, kb = blk - cb * KB;
+        const int64_t n = 16 * cb + (t & 15), j = n >> 3;
+        const int e = (int)(n & 7);
+        const int64_t k0 = 32 * kb + 8 * (t >> 4);
+        uint32_t word = 0;
+        if (n < N) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t k = k0 + i;
+                if (k < Kpad) word |= ((strips[4 * (j * RQ + (k >> 2)) + (k & 3)] >> (4 * e)) & 0xFu) << (4 * i);
+            }
+        }
+        koct[d] = word;
+    }
+}
+
 // INT4 flat pack: one thread per byte (elements 2b, 2b+1 of the flattened tensor).
 __global__ void k_pack_i4_flat(const float* __restrict__ src, int from_codes, int64_t total, int64_t G,
                                const float* __restrict__ inv, unsigned char* __restrict__ packed,
@@ -341,6 +369,14 @@ hipError_t launch_pack_i4_tiled(const float* src, bool from_codes, int64_t K, in
     if (nchunks <= 0) return hipSuccess;
     k_pack_i4_tiled<<<grid_for(nchunks), kBlock, 0, s>>>(src, from_codes, K, N, g.G, g.RQ, g.NS, nchunks, inv,
                                                          (uint4*)packed, qdata, bad);
+    if (packed) {
+        const int64_t ndw = g.koct_bytes() / 4;
+        const int64_t strip_bytes = g.chunks() * 16;
+        k_koct_i4<<<grid_for(ndw), kBlock, 0, s>>>((const uint32_t*)packed, N, g.Kpad, g.RQ, g.KB(), ndw,
+                                                   (uint32_t*)((char*)packed + g.koct_off()),
+                                                   (uint32_t*)((char*)packed + strip_bytes),
+                                                   (int)((g.koct_off() - strip_bytes) / 4));
+    }
     return hipGetLastError();
 }
 

@@ -112,7 +112,29 @@ def model_pack_i8(codes: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(t).view(np.uint8).reshape(-1)
 
 
-def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
+def i4_koct_geom(K, N, G):
+    """(offset, KB, NB) of the k-octet copy that follows the strips: the
+    strips' bytes rounded up to 256, k blocks of 32 rows, column blocks of 16."""
+    g = i4_geom(K, N, G)
+    return _ceil(g["NS"] * g["RQ"] * 16, 256) * 256, _ceil(g["Kpad"], 32), _ceil(g["NS"], 2)
+
+
+def i4_packed_bytes(K, N, G):
+    g = i4_geom(K, N, G)
+    if not g["tiled"]:
+        return (K * N + 1) // 2
+    off, KB, NB = i4_koct_geom(K, N, G)
+    return off + NB * KB * 256
+
+
+def _nibble_words(t: np.ndarray) -> np.ndarray:
+    """Eight codes along the last axis as one uint32, code i in nibble i."""
+    nib = (t & 0xF).astype(np.uint32)
+    shifts = (np.arange(8, dtype=np.uint32) * 4)
+    return np.bitwise_or.reduce(nib << shifts, axis=-1).astype(np.uint32)
+
+
+def model_pack_i4_strips(codes: np.ndarray, G: int) -> np.ndarray:
     """INT4 strip-major: chunk (strip j, row quad rq) at (j*RQ + rq)*16;
     dword r = row 4*rq+r; nibble e = column 8*j+e (low nibble first)."""
     K, N = codes.shape
@@ -121,10 +143,29 @@ def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
     full[:K, :N] = codes.astype(np.int64)
     t = full.reshape(g["RQ"], 4, g["NS"], 8)  # rq, r, j, e
     t = t.transpose(2, 0, 1, 3)  # j, rq, r, e
-    nib = (t & 0xF).astype(np.uint32)
-    shifts = (np.arange(8, dtype=np.uint32) * 4)
-    words = np.bitwise_or.reduce(nib << shifts, axis=-1).astype(np.uint32)
-    return np.ascontiguousarray(words).view(np.uint8).reshape(-1)
+    return np.ascontiguousarray(_nibble_words(t)).view(np.uint8).reshape(-1)
+
+
+def model_pack_i4_koct(codes: np.ndarray, G: int) -> np.ndarray:
+    """The k-octet copy: block (column block cb, k block kb) of 256 bytes at
+    (cb*KB + kb)*256; dword 16*g + c = column 16*cb + c, rows 32*kb + 8*g + i
+    in nibble i."""
+    K, N = codes.shape
+    _, KB, NB = i4_koct_geom(K, N, G)
+    full = np.zeros((KB * 32, NB * 16), np.int64)
+    full[:K, :N] = codes.astype(np.int64)
+    t = full.reshape(KB, 4, 8, NB, 16)  # kb, g, i, cb, c
+    t = t.transpose(3, 0, 1, 4, 2)  # cb, kb, g, c, i
+    return np.ascontiguousarray(_nibble_words(t)).view(np.uint8).reshape(-1)
+
+
+def model_pack_i4_tiled(codes: np.ndarray, G: int) -> np.ndarray:
+    """The whole INT4 strip-major buffer: the strips, zeros up to the k-octet
+    copy's offset, then the k-octet copy."""
+    K, N = codes.shape
+    strips = model_pack_i4_strips(codes, G)
+    off, _, _ = i4_koct_geom(K, N, G)
+    return np.concatenate([strips, np.zeros(off - strips.size, np.uint8), model_pack_i4_koct(codes, G)])
 
 
 def model_pack_i4_flat(codes: np.ndarray) -> np.ndarray:

@@ -42,7 +42,9 @@ def test_int8_sizes(lib, K, N):
 def test_int4_sizes(lib, K, N, G):
     g = helpers.i4_geom(K, N, G)
     assert lib.sgq_int4_layout(K, N, G) == (0 if g["tiled"] else 1)
-    exp_bytes = g["NS"] * g["RQ"] * 16 if g["tiled"] else (K * N + 1) // 2
+    off, KB, NB = helpers.i4_koct_geom(K, N, G)
+    exp_bytes = off + NB * KB * 256 if g["tiled"] else (K * N + 1) // 2
+    assert helpers.i4_packed_bytes(K, N, G) == exp_bytes
     assert lib.sgq_int4_packed_bytes(K, N, G) == exp_bytes
     assert lib.sgq_int4_devscale_count(K, N, G) == (g["nsc"] * g["Kpad"] if g["tiled"] else 0)
     assert lib.sgq_int4_scale_count(K, N, G) == (K * N + g["G"] - 1) // g["G"]
@@ -244,6 +246,35 @@ def test_model_pack_i4_positions():
         off = ((n // 8) * g["RQ"] + k // 4) * 16 + (k % 4) * 4 + (n % 8) // 2
         nib = (int(buf[off]) >> (4 * (n % 2))) & 0xF
         assert ((nib ^ 8) - 8) == q[k, n]
+
+
+def test_model_pack_i4_koct_positions():
+    """The k-octet copy: each dword holds eight consecutive rows of one column
+    (an MFMA B operand), blocks of 16 columns x 32 rows contiguous over K; the
+    padding rows and columns are code 0."""
+    rng = np.random.default_rng(2)
+    K, N = 40, 24  # two k blocks (the second padded), two column blocks (the second half empty)
+    q = rng.integers(-8, 8, size=(K, N))
+    buf = helpers.model_pack_i4_tiled(q, 8)
+    off, KB, NB = helpers.i4_koct_geom(K, N, 8)
+    assert (KB, NB) == (2, 2) and off % 256 == 0 and buf.size == off + KB * NB * 256
+    words = buf[off:].view(np.uint32)
+    for (k, n) in [(0, 0), (39, 23), (7, 15), (8, 16), (33, 5)]:
+        d = ((n // 16) * KB + k // 32) * 64 + ((k % 32) // 8) * 16 + n % 16
+        nib = (int(words[d]) >> (4 * (k % 8))) & 0xF
+        assert ((nib ^ 8) - 8) == q[k, n]
+    # rows 40..63 of every column and columns 24..31 of every row are zeros
+    dense = np.zeros((KB * 32, NB * 16), np.int64)
+    for d, w in enumerate(words):
+        blk, t = divmod(d, 64)
+        cb, kb = divmod(blk, KB)
+        for i in range(8):
+            nib = (int(w) >> (4 * i)) & 0xF
+            dense[32 * kb + 8 * (t // 16) + i, 16 * cb + t % 16] = (nib ^ 8) - 8
+    assert np.array_equal(dense[:K, :N], q) and not dense[K:].any() and not dense[:, N:].any()
+    # the strips precede it unchanged, zero-filled up to the offset
+    strips = helpers.model_pack_i4_strips(q, 8)
+    assert np.array_equal(buf[:strips.size], strips) and not buf[strips.size:off].any()
 
 
 def test_model_devscales():
