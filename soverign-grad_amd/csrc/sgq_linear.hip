@@ -1118,53 +1118,19 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 // order of every sum depends on the K range and NW only, not on C, MB or the
 // number of weights.
 //
-// B operand straight from the strip layout, without LDS: a 32-row k block of
-// a strip is 128 bytes, dword r = row r's eight nibbles.  Lane l of a 16-lane
-// row takes column e = (l & 3) | (l & 8) >> 1 of strip j = (l >> 2) & 1 and,
-// in lane group g = l >> 4, rows 8g .. 8g+7.  Each lane loads one dword (row
-// 8g + e of its strip, all eight columns); an 8x8 nibble transpose across the
-// eight lanes of (g, j) leaves it with rows 8g .. 8g+7 of column e, which is
-// its B operand.  The codes are read once, in 256-byte runs per wavefront.
+// B operands straight from the weight's k-octet copy, without LDS: block
+// (column block, k block) is 256 bytes whose dword t holds rows 8 (t >> 4) ..
+// + 7 of column t & 15, the B operand of lane t as it stands.  Each lane loads
+// one dword per k block; the codes are read once, in 256-byte runs per
+// wavefront.  (From the strip layout, where a dword holds one row of eight
+// columns, the same operand took an 8x8 nibble transpose across eight lanes:
+// three DPP exchanges, rotates and bit selects per dword, 10-13% of the gate
+// projection's time at 5 to 16 rows.)
 // ---------------------------------------------------------------------------
 
-// Exchanges within the eight lanes of a transpose group: lane bits 0 and 1
-// are group bits 0 and 1 (DPP quad_perm), lane bit 3 is group bit 2 (DPP
-// row_ror:8 within a 16-lane row).
-__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true); }
-__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true); }
+// Lane l's value from lane l ^ 8 within its 16-lane row (DPP row_ror:8): the
+// half-row forms exchange the two halves of an A operand with it.
 __device__ __forceinline__ uint32_t dpp_xor8(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); }
-__device__ __forceinline__ uint32_t rotr32(uint32_t v, uint32_t s) { return __builtin_amdgcn_alignbit(v, v, s); }
-
-// Per-lane constants of the transpose for group lane e.  Step d (4, 2, 1
-// nibbles): the lane keeps its nibbles whose index has bit d equal to its own
-// bit d and takes the other half from its partner (e ^ d), rotated by 4d bits
-// so that partner nibble c lands on c ^ d.
-struct NibbleT {
-    uint32_t keep4, keep2, keep1, rot2, rot1;
-};
-__device__ __forceinline__ NibbleT nibble_t(int e) {
-    NibbleT t;
-    t.keep4 = (e & 4) ? 0xFFFF0000u : 0x0000FFFFu;
-    t.keep2 = (e & 2) ? 0xFF00FF00u : 0x00FF00FFu;
-    t.keep1 = (e & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    t.rot2 = (e & 2) ? 8u : 24u;  // right by 8, or left by 8
-    t.rot1 = (e & 1) ? 4u : 28u;
-    return t;
-}
-// keep ? a : b, bit by bit, as one v_bitop3_b32: the truth table indexes
-// (a, b, keep) as (0xF0, 0xCC, 0xAA), so (0xF0 & 0xAA) | (0xCC & ~0xAA) =
-// 0xE4.  The compiler writes the and/or form as two or three instructions.
-__device__ __forceinline__ uint32_t bit_select(uint32_t a, uint32_t b, uint32_t keep) {
-    return __builtin_amdgcn_bitop3_b32(a, b, keep, 0xE4);
-}
-// On entry nibble c of lane e is T[e][c]; on return nibble r is T[r][e].
-// Three instructions per step: the DPP exchange, a rotate, a bit select.
-__device__ __forceinline__ uint32_t nibble_transpose8(uint32_t w, const NibbleT& t) {
-    w = bit_select(w, rotr32(dpp_xor8(w), 16u), t.keep4);
-    w = bit_select(w, rotr32(dpp_xor2(w), t.rot2), t.keep2);
-    w = bit_select(w, rotr32(dpp_xor1(w), t.rot1), t.keep1);
-    return w;
-}
 
 // Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
 // operand: high nibbles masked in place and low nibbles shifted up read as
@@ -1452,33 +1418,34 @@ __global__ __launch_bounds__(NW * 64) void k_skinny3(SGQ_SKINNY_HOT_PARAMS, cons
 // loads); otherwise one float per load.  MB: row blocks of 16 (M <= 16 MB).
 //
 // The K range is walked in super-blocks of 128 rows, wavefront w taking
-// super-blocks w, w + NW, ...  In a super-block, lane (g, e) of strip j loads
-// rows 16e + 4g .. 16e + 4g + 3 of its strip (16 bytes, all eight columns; the
-// 32 lanes of a strip read its 512 bytes once) and, for t = 0..7, x rows
-// 16t + 4g .. 16t + 4g + 3 of its batch row (the four lane groups of a batch
-// row read 64 contiguous bytes per load, one cache line).  Dword i of the
-// codes transposed across the eight lanes e gives column e at rows
-// 16e' + 4g + i (e' = 0..7), the B operand of MFMA i; component i of the
-// eight x quads is the matching A operand.  The scales of the workgroup's K
-// range sit in LDS (read once, coalesced); the next super-block's codes and x
-// are loaded while the current one is computed.
+// super-blocks w, w + NW, ...  A super-block is four k blocks of 32 rows of
+// the weight's k-octet copy: for k block i = 0..3, lane t loads dword t of
+// block (column block, 4 sb + i), rows 8 (t >> 4) .. + 7 of column t & 15,
+// which is the B operand of MFMA i as it stands (four 256-byte runs per
+// wavefront and column block, 1 KB contiguous), and x rows 32 i + 8 g ..
+// 32 i + 8 g + 7 of its batch row as two quads, the matching A operand.  The
+// scales of the workgroup's K range sit in LDS (read once, coalesced); the
+// next super-block's codes and x are loaded while the current one is
+// computed.
 template <int NW, int C, int NG, bool XA, int MB, bool HALF>
 struct SkinnyRegs {
-    uint4 w[NG][C];                // 4 rows x 8 columns of each strip
+    uint4 w[NG][C];                // dword i: the B operand of k block i
     float4 xq[MB][HALF ? 4 : 8];  // x quads of each batch row (HALF: half of them)
 };
 
-// HALF (one row block, M <= 8): as in k_skinny3, lane n < 8 takes x quads
-// t = 0..3 of row n and lane n + 8 quads t = 4..7 of the same row; a
-// row_ror:8 exchange completes each A operand (the same bf16 planes).
+// Quad t of a lane covers k block i = t / 2, rows 32 i + 8 g + 4 (t % 2) ..
+// + 3.  HALF (one row block, M <= 8): as in k_skinny3, lane n < 8 takes the
+// first quad of each k block of row n (quad t is k block t) and lane n + 8 the
+// second; a row_ror:8 exchange completes each A operand (the same bf16
+// planes).
 template <int NW, int C, int NG, bool XA, int MB, bool SPLIT, bool HALF>
 __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, const SkinnyArgs a) {
     static_assert(!HALF || MB == 1, "the half-row form has one row block");
     constexpr int XT = HALF ? 4 : 8;  // x quads per lane, row block and super-block
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const int e = (n & 3) | ((n >> 1) & 4), j = (n >> 2) & 1;
     const int Kpad = 4 * RQ, slog = (pk >> 16) & 255;
+    const int nkb = (Kpad + 31) >> 5;  // k blocks of 32 rows (KB of the k-octet copy)
     // Workgroup v: K range v % S of column group v / S (the ranges of one
     // column group are neighbours, so they share an XCD's L2 for the scales).
     const int v = xcd_swizzle(blockIdx.x, nblk, pk & 255);
@@ -1512,12 +1479,13 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
     __amdgpu_buffer_rsrc_t rW[NG];
 #pragma unroll
     for (int q = 0; q < NG; ++q)
-        rW[q] = make_rsrc((q == 0 ? hW0 : a.W[q]) + (int64_t)(2 * blk0) * RQ, (uint32_t)(2 * C) * (uint32_t)RQ * 16u);
+        rW[q] = make_rsrc((q == 0 ? hW0 : a.W[q]) + ((int64_t)ko + (int64_t)blk0 * nkb) * 16,
+                          (uint32_t)C * (uint32_t)nkb * 256u);
     const __amdgpu_buffer_rsrc_t rX = make_rsrc(hx, (uint32_t)hM * (uint32_t)K * 4u);
     int wv[C];
 #pragma unroll
-    for (int c = 0; c < C; ++c) wv[c] = (2 * c + j) * RQ * 16 + (16 * e + 4 * g) * 4;
-    const int xr = HALF ? (n & 7) : n, toff = HALF ? 4 * (n >> 3) : 0;
+    for (int c = 0; c < C; ++c) wv[c] = c * nkb * 256 + 4 * lane;
+    const int xr = HALF ? (n & 7) : n, hq = HALF ? (n >> 3) : 0;
     bool row_live[MB];
     int xrow[MB];
 #pragma unroll
@@ -1525,7 +1493,9 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
         row_live[b] = xr + 16 * b < hM;
         xrow[b] = row_live[b] ? (xr + 16 * b) * K * 4 : 0;
     }
-    const NibbleT tp = nibble_t(e);
+    // Quad t of a lane: k block t / 2 (HALF: t) of the super-block, rows
+    // 8 g + 4 (t % 2) (HALF: 8 g + 4 hq) .. + 3 of it.
+    auto qrow = [&](int t) { return HALF ? 32 * t + 8 * g + 4 * hq : 32 * (t >> 1) + 8 * g + 4 * (t & 1); };
 
     // Loads of super-block sb; one past the range reads x as zeros (and codes
     // that are then multiplied by zero).
@@ -1534,13 +1504,16 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
 #pragma unroll
         for (int q = 0; q < NG; ++q)
 #pragma unroll
-            for (int c = 0; c < C; ++c) r.w[q][c] = buf_load16_stream(rW[q], wv[c], sb * (kSkinnySB * 4));
-        const int k0 = sb * kSkinnySB + 4 * g + 16 * toff;
+            for (int c = 0; c < C; ++c) {
+                const int so = sb * (4 * 256);
+                r.w[q][c] = make_uint4(buf_load4_stream(rW[q], wv[c], so), buf_load4_stream(rW[q], wv[c], so + 256),
+                                       buf_load4_stream(rW[q], wv[c], so + 512), buf_load4_stream(rW[q], wv[c], so + 768));
+            }
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
             for (int t = 0; t < XT; ++t) {
-                const int kk = k0 + 16 * t;
+                const int kk = sb * kSkinnySB + qrow(t);
                 if constexpr (XA) {
                     r.xq[b][t] = buf_load4f<true>(rX, in && row_live[b] && kk < K ? xrow[b] + kk * 4 : kOobOff, 0);
                 } else {
@@ -1568,20 +1541,26 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
     auto compute = [&](SkinnyRegs<NW, C, NG, XA, MB, HALF>& r, int sb) {
         // A super-block past the range has x = 0; its scale reads stay inside
         // the range's LDS rows.
-        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4) + g + 4 * toff;
+        const int lr = (min(sb, sb_hi - 1) - sb_lo) * (kSkinnySB / 4);
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
             float4 s4[XT];
 #pragma unroll
-            for (int t = 0; t < XT; ++t) s4[t] = ssc[q][lr + 4 * t];
+            for (int t = 0; t < XT; ++t) s4[t] = ssc[q][lr + qrow(t) / 4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 uint4 ah[MB], am[MB], al[MB];
 #pragma unroll
                 for (int b = 0; b < MB; ++b) {
-                    float xs[XT];
+                    // k block i: quads 2i, 2i + 1 (HALF: quad i, the other half in lane n ^ 8).
+                    float xs[8];
 #pragma unroll
-                    for (int t = 0; t < XT; ++t) xs[t] = f4get(r.xq[b][t], i) * f4get(s4[t], i);
+                    for (int h = 0; h < (HALF ? 1 : 2); ++h)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const int t = HALF ? i : 2 * i + h;
+                            xs[4 * h + u] = f4get(r.xq[b][t], u) * f4get(s4[t], u);
+                        }
                     if constexpr (HALF) {
                         uint2 h2, m2, l2;
                         split3_4(xs, h2, m2, l2);
@@ -1595,7 +1574,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
 #pragma unroll
                 for (int c = 0; c < C; ++c) {
                     const uint32_t wd = i == 0 ? r.w[q][c].x : (i == 1 ? r.w[q][c].y : (i == 2 ? r.w[q][c].z : r.w[q][c].w));
-                    const bf16x8 bq = nibbles_bf16x16(nibble_transpose8(wd, tp));
+                    const bf16x8 bq = nibbles_bf16x16(wd);
 #pragma unroll
                     for (int b = 0; b < MB; ++b) {
                         acc[q][b][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[b]), bq,
@@ -1655,8 +1634,8 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
                 const int t = threadIdx.x + i * NW * 64;
                 const int c = t >> 8, mr = (t >> 4) & 15, sl = t & 15;
                 const int m = mr + 16 * b;
-                const int strip = 2 * (blk0 + c) + ((sl >> 2) & 1), el = (sl & 3) | ((sl >> 1) & 4);
-                const int col = 8 * strip + el;
+                const int col = 16 * (blk0 + c) + sl;
+                const int strip = col >> 3, el = col & 7;
                 float s = 0.0f;
                 if (t < 256 * C && m < a.M && col < a.N) {
 #pragma unroll
@@ -1678,7 +1657,7 @@ __global__ __launch_bounds__(NW * 64) void k_skinny_sb(SGQ_SKINNY_HOT_PARAMS, co
         for (int i = 0; i < OPT; ++i) {
             const int t = threadIdx.x + i * NW * 64;
             const int c = t >> 8, m = ((t >> 4) & 15) + 16 * b, sl = t & 15;
-            const int col = 8 * (2 * (blk0 + c) + ((sl >> 2) & 1)) + ((sl & 3) | ((sl >> 1) & 4));
+            const int col = 16 * (blk0 + c) + sl;
             if (t < 256 * C && m < a.M && col < a.N) {
                 const int64_t at = (int64_t)m * a.N + col;
                 if constexpr (SPLIT) {
