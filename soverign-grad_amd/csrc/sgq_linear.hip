@@ -780,6 +780,16 @@ __device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
 }
 __device__ __forceinline__ float trunc_bf16(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFF0000u); }
 
+// Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
+// operand: high nibbles masked in place and low nibbles shifted up read as
+// signed bytes 16q, converted exactly.
+__device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
+    const uint32_t hi = t & 0xF0F0F0F0u, lo = (t << 4) & 0xF0F0F0F0u;
+    const uint4 b = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<0>(hi)), pack_hi16(cvt_sbyte<1>(lo), cvt_sbyte<1>(hi)),
+                               pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<2>(hi)), pack_hi16(cvt_sbyte<3>(lo), cvt_sbyte<3>(hi)));
+    return __builtin_bit_cast(bf16x8, b);
+}
+
 // Splits eight floats into the bf16 planes h, m, l (four dwords each).
 __device__ __forceinline__ void split3(const float* v, uint4& h, uint4& m, uint4& l) {
     // No fma: fused with the multiply that made v (x * s), a - trunc(a)
@@ -871,6 +881,7 @@ struct Gemm3Args {
     float* y;
     float* part;
     int xr, xlog;
+    int ko;  // INT4: byte offset / 256 of the k-octet copy
 };
 
 template <int BITS, bool KALIGN4, bool PT, class SH>
@@ -939,17 +950,26 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         rS = make_rsrc(S, PT ? 4u : (uint32_t)K * 4u);
     else
         rS = make_rsrc(S + (int64_t)((n0 / SW) / mode) * Kpad, (uint32_t)K * 4u);
-    // B side: an entry holds the eight k of its k group for one column, read
-    // from the two chunks (strip, row quads 2 * kg and 2 * kg + 1) that hold
-    // them: INT8 the column's dword of each chunk, INT4 the whole chunks (a
-    // nibble of every dword).  Strips past NS read as zero.
-    const int nstr = (NS - n0 / SW) < (BN / SW) ? (NS - n0 / SW) : (BN / SW);
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
+    // B side: an entry holds the eight k of its k group for one column.
+    // INT8: the column's dword of the two strip chunks (row quads 2 * kg and
+    // 2 * kg + 1) that hold them; strips past NS read as zero.  INT4: one
+    // dword of the k-octet copy, block (column / 16, stage) dword 16 kg +
+    // column % 16, which holds exactly those eight codes; column blocks past
+    // the weight's read as zero.
+    const int KB = (Kpad + kB3BK - 1) / kB3BK;
+    __amdgpu_buffer_rsrc_t rW;
+    if constexpr (BITS == 8) {
+        const int nstr = (NS - n0 / SW) < (BN / SW) ? (NS - n0 / SW) : (BN / SW);
+        rW = make_rsrc(W + (int64_t)(n0 / SW) * RQ, (uint32_t)nstr * (uint32_t)RQ * 16u);
+    } else {
+        const int ncb = ((NS + 1) / 2 - n0 / 16) < (BN / 16) ? ((NS + 1) / 2 - n0 / 16) : (BN / 16);
+        rW = make_rsrc(W + ((int64_t)ga.ko + (int64_t)(n0 / 16) * KB) * 16, (uint32_t)ncb * (uint32_t)KB * 256u);
+    }
 
     struct Regs {
-        float4 a[EA][2];                      // [entry][quad]
-        float4 s[2];                          // scales of the thread's eight k
-        uint4 b[EB][BITS == 8 ? 1 : 2];       // [entry]: INT8 {lo, hi} dwords in .x/.y, INT4 the two chunks
+        float4 a[EA][2];  // [entry][quad]
+        float4 s[2];      // scales of the thread's eight k
+        uint2 b[EB];      // [entry]: INT8 {lo, hi} dwords, INT4 the k-octet dword in .x
     };
     auto load = [&](Regs& rg, int kt) {
         const int kb = kt * kB3BK + akg * 8;
@@ -974,20 +994,24 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 #pragma unroll
             for (int q = 0; q < 2; ++q) rg.s[q] = buf_load4f<KALIGN4>(rS, (akg * 8 + 4 * q) * 4, soff);
         }
-        // RQ is a multiple of 4, so both row quads of the pair are in or out together.
-        const bool in = kt * kB3RQ + 2 * akg < RQ;
-        const int bsoff = kt * kB3RQ * 16;
+        if constexpr (BITS == 8) {
+            // RQ is a multiple of 4, so both row quads of the pair are in or out together.
+            const bool in = kt * kB3RQ + 2 * akg < RQ;
+            const int bsoff = kt * kB3RQ * 16;
 #pragma unroll
-        for (int c = 0; c < EB; ++c) {
-            const int n = ar + kStep * c;
-            const int vo = ((n / SW) * RQ + 2 * akg) * 16;
-            if constexpr (BITS == 8) {
-                const int vd = vo + (n & 3) * 4;
-                rg.b[c][0].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, bsoff, 0);
-                rg.b[c][0].y = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd + 16 : kOobOff, bsoff, 0);
-            } else {
-                rg.b[c][0] = buf_load16(rW, in ? vo : kOobOff, bsoff);
-                rg.b[c][1] = buf_load16(rW, in ? vo + 16 : kOobOff, bsoff);
+            for (int c = 0; c < EB; ++c) {
+                const int n = ar + kStep * c;
+                const int vd = ((n / SW) * RQ + 2 * akg) * 16 + (n & 3) * 4;
+                rg.b[c].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, bsoff, 0);
+                rg.b[c].y = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd + 16 : kOobOff, bsoff, 0);
+            }
+        } else {
+            const bool in = kt < KB;
+#pragma unroll
+            for (int c = 0; c < EB; ++c) {
+                const int n = ar + kStep * c;
+                const int vd = (n >> 4) * KB * 256 + (16 * akg + (n & 15)) * 4;
+                rg.b[c].x = __builtin_amdgcn_raw_buffer_load_b32(rW, in ? vd : kOobOff, kt * 256, 0);
             }
         }
     };
@@ -1003,22 +1027,18 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
         }
 #pragma unroll
         for (int c = 0; c < EB; ++c) {
-            float f[8];
             if constexpr (BITS == 8) {
                 // bytes of the column's dword in each chunk: k = 0..3, then 4..7
-                const uint32_t lo = rg.b[c][0].x, hi = rg.b[c][0].y;
+                const uint32_t lo = rg.b[c].x, hi = rg.b[c].y;
+                float f[8];
                 f[0] = cvt_sbyte<0>(lo), f[1] = cvt_sbyte<1>(lo), f[2] = cvt_sbyte<2>(lo), f[3] = cvt_sbyte<3>(lo);
                 f[4] = cvt_sbyte<0>(hi), f[5] = cvt_sbyte<1>(hi), f[6] = cvt_sbyte<2>(hi), f[7] = cvt_sbyte<3>(hi);
+                Bs[buf][akg][ar + kStep * c] = make_uint4(pack_hi16(f[0], f[1]), pack_hi16(f[2], f[3]),
+                                                           pack_hi16(f[4], f[5]), pack_hi16(f[6], f[7]));
             } else {
-                // dword r of a chunk is row r of it; nibble e the column
-                const int sh = 28 - 4 * ((ar + kStep * c) & 7);
-                const uint32_t dw[8] = {rg.b[c][0].x, rg.b[c][0].y, rg.b[c][0].z, rg.b[c][0].w,
-                                        rg.b[c][1].x, rg.b[c][1].y, rg.b[c][1].z, rg.b[c][1].w};
-#pragma unroll
-                for (int r = 0; r < 8; ++r) f[r] = (float)(((int)(dw[r] << sh)) >> 28);
+                // the eight codes as 16q (the epilogue divides by 16)
+                Bs[buf][akg][ar + kStep * c] = __builtin_bit_cast(uint4, nibbles_bf16x16(rg.b[c].x));
             }
-            Bs[buf][akg][ar + kStep * c] = make_uint4(pack_hi16(f[0], f[1]), pack_hi16(f[2], f[3]),
-                                                       pack_hi16(f[4], f[5]), pack_hi16(f[6], f[7]));
         }
     };
 
@@ -1094,7 +1114,8 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm * 16 * RB + i * 16 + lkg * 4 + r;
                 if (m < M) {
-                    float v = PT ? acc[i][j][r] * s_all : acc[i][j][r];
+                    // INT4 codes entered as 16q: an exact division by 16.
+                    float v = BITS == 4 ? acc[i][j][r] * 0.0625f : (PT ? acc[i][j][r] * s_all : acc[i][j][r]);
                     if (!isfinite(v)) v = output_exact<BITS>(x + (int64_t)m * K, W, S, mode, Kpad, RQ, n, klo, khi);
                     out[(int64_t)m * N + n] = (bias && KS == 1) ? v + bv : v;
                 }
@@ -1131,16 +1152,6 @@ __global__ __launch_bounds__(SH::NT) __attribute__((amdgpu_waves_per_eu(SH::WPE)
 // Lane l's value from lane l ^ 8 within its 16-lane row (DPP row_ror:8): the
 // half-row forms exchange the two halves of an A operand with it.
 __device__ __forceinline__ uint32_t dpp_xor8(uint32_t v) { return __builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true); }
-
-// Eight nibble codes (k order, nibble 0 first) as the bf16 values 16q of a B
-// operand: high nibbles masked in place and low nibbles shifted up read as
-// signed bytes 16q, converted exactly.
-__device__ __forceinline__ bf16x8 nibbles_bf16x16(uint32_t t) {
-    const uint32_t hi = t & 0xF0F0F0F0u, lo = (t << 4) & 0xF0F0F0F0u;
-    const uint4 b = make_uint4(pack_hi16(cvt_sbyte<0>(lo), cvt_sbyte<0>(hi)), pack_hi16(cvt_sbyte<1>(lo), cvt_sbyte<1>(hi)),
-                               pack_hi16(cvt_sbyte<2>(lo), cvt_sbyte<2>(hi)), pack_hi16(cvt_sbyte<3>(lo), cvt_sbyte<3>(hi)));
-    return __builtin_bit_cast(bf16x8, b);
-}
 
 struct SkinnyArgs {
     const float* x;  // [M, K]
@@ -2576,11 +2587,14 @@ hipError_t gemm_launch(const float* x, int64_t M, int64_t K, int64_t N, const vo
     const int xlog = xcd_log2(xcds);
     const bool k4 = x_aligned4(x, K);
     const bool pt = BITS == 8 && mode;
+    // INT4: the k-octet copy follows the strips at their bytes rounded up to
+    // 256 (I4Geom::koct_off).
+    const int ko = BITS == 4 ? (int)ceil_div(NS * RQ * 16, 256) : 0;
     using Big = typename std::conditional<BITS == 8, G3Wide, G3Tile>::type;
 #define SGQ_GEMM3(SH, A4, PT_)                                                                                 \
     k_gemm3<BITS, A4, (PT_) && BITS == 8, SH><<<grid, SH::NT, 0, s>>>(Gemm3Args{                                \
         x, (int)M, (int)K, (int)N, (const uint4*)packed, sc, mode, (int)Kpad, (int)RQ, (int)NS, p.KS, p.sps, bias, \
-        y, part, xr, xlog})
+        y, part, xr, xlog, ko})
 #define SGQ_GEMM3_SHAPE(SH)               \
     if (k4 && pt)                         \
         SGQ_GEMM3(SH, true, true);        \
