@@ -131,15 +131,19 @@ inline bool linear_uses_gemv(int64_t M, int64_t K, int64_t N) {
 //    each workgroup all of K.  Measured on MI355X (INT4 g128, graphs of 100
 //    calls, GEMV -> MFMA): 4096->11008 at 5 / 8 / 16 rows 19.0 / 19.9 / 31.0
 //    -> 15.4 / 15.9 / 17.0 us; 2048->6144 at 8 / 16 rows 8.4 / 12.9 -> 7.4 /
-//    8.4; 4096->14336 at 16 rows 37.9 -> 17.4.  Four rows stay on the GEMV
-//    (4096->11008 12.8 vs 15.3 us), as does K below 2048.
+//    8.4; 4096->14336 at 16 rows 37.9 -> 17.4.  With B operands from the
+//    k-octet copy three and four rows go there too (GEMV -> MFMA, builds
+//    interleaved: 4096->11008 at 3 / 4 rows 11.7-12.0 / 12.7-13.3 -> 11.1-11.4
+//    / 11.6-11.8 us, 2048->6144 5.2 / 5.3-5.4 -> 5.0-5.1 / 5.1, 8192->28672 at
+//    4 rows 46.5-47.0 -> 39.8-40.0); two rows stay on the GEMV (4096->11008
+//    8.8 vs 10.9-11.3 us), as does K below 2048.
 //  - narrower weights split K into S ranges (a power of two, enough
 //    workgroups to fill the device, at least kSkinnyMinRangeBlocks 32-row k
 //    blocks each).  Every workgroup of the GEMV or of the unsplit kernel
 //    reads all M rows of x, which for M >= 4 is more than its codes; a range
 //    reads its own slice.  The partial sums go to the caller's workspace and
 //    a second kernel adds them in range order.
-constexpr int64_t kSkinnyMinRows = 5;        // wide weights
+constexpr int64_t kSkinnyMinRows = 3;        // wide weights
 constexpr int64_t kSkinnyNarrowMinRows = 5;  // split K
 constexpr int64_t kSkinnyMaxRows = 32;       // two row blocks of 16
 constexpr int64_t kSkinnyMinK = 2048;        // wide weights

@@ -439,20 +439,21 @@ def test_plan_skinny_int8(lib):
 
 
 def test_plan_skinny_mfma(lib):
-    """Batches of 5..16 rows over a wide INT4 weight take the skinny bf16 MFMA
+    """Batches of 3..16 rows over a wide INT4 weight take the skinny bf16 MFMA
     kernel (path 4, whole K) when its 32- or 64-column workgroups fill at least
     5/8 of the CUs, and need 2C strips per scale column; 17..32 rows take its
     super-block form, and weights too narrow to fill the device split K
     (k_splits > 1) from 5 rows once M (rounded up to 8) * K * N reaches 2^28.
     Everything else stays on the GEMV (path 0) or the GEMM (path 1)."""
-    for M in range(5, 33):
+    for M in range(3, 33):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (4, 1)  # 172 workgroups of 64 columns
         assert _plan(lib, 4, M, 2048, 6144, 128, 256) == (4, 1)  # 192 of 32
     for M in range(1, 33):  # 128 column blocks of 16: split K from 24 rows' worth of work (2^28), else GEMV
         assert _plan(lib, 4, M, 5632, 2048, 128, 256) == ((4, 4) if M >= 17 else (0, 1))
         assert _plan(lib, 4, M, 2048, 2048, 128, 256) == (0, 1)
-    for M in (1, 2, 3, 4):
+    for M in (1, 2):
         assert _plan(lib, 4, M, 4096, 11008, 128, 256) == (0, 1)
+        assert _plan(lib, 4, M, 2048, 6144, 128, 256) == (0, 1)
     assert _plan(lib, 4, 33, 4096, 11008, 128, 256)[0] == 1  # the GEMM from 33 rows
     # Narrow weights: K split into 4 ranges of 2752 rows (64 column groups x 4
     # = 256 workgroups) from 5 rows with M (rounded up to 8) * K * N >= 2^28.

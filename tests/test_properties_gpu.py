@@ -34,7 +34,9 @@ TOL = 1e-5
 # (name, bits, M, K, N, group_size or scheme)
 CASES = [
     ("c2_gemv", 4, 1, 4096, 4096, 128),
-    ("c3_gate_m4_gemv", 4, 4, 4096, 11008, 128),
+    ("c3_gate_m2_gemv", 4, 2, 4096, 11008, 128),
+    ("c3_gate_m4_skinny", 4, 4, 4096, 11008, 128),
+    ("c3_down_m4_gemv", 4, 4, 11008, 4096, 128),
     ("c3_gate_m8_skinny", 4, 8, 4096, 11008, 128),
     ("c3_down_m16_skinny_splitk", 4, 16, 11008, 4096, 128),
     ("c3_gate_m32_skinny_two_row_blocks", 4, 32, 4096, 11008, 128),

@@ -62,7 +62,7 @@ def _quantized(sgq, dev, oracle, synth, K, N, G, seed):
 # the BASELINE gate/up (4096->11008) and NanoLLaMA q/k/v and gate/up widths,
 # groups 64 and 32 (fewer strips per scale column), a K that ends inside a
 # 32-row k block, and a long K.
-@pytest.mark.parametrize("M", [5, 8, 12, 16])
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("K,N,G", [(4096, 11008, 128), (2048, 6144, 128), (2048, 5632, 128), (4096, 8192, 64),
                                    (2048, 5120, 32), (4112, 6144, 128), (11008, 5632, 128)])
 def test_skinny_shapes(sgq, dev, oracle, synth, M, K, N, G):
@@ -79,18 +79,20 @@ def test_skinny_shapes(sgq, dev, oracle, synth, M, K, N, G):
 
 
 def test_skinny_boundaries(sgq, dev):
-    # Four rows, narrow weights of little work and groups whose scale column
-    # holds a single strip stay on the GEMV; 5..32 rows over wide weights, and
-    # narrow ones from (M rounded up to 8) * K * N = 2^28, take the MFMA
-    # kernel; 33 rows the GEMM.
-    assert _path(sgq, 4, 4096, 11008, 128) == 0
+    # Two rows, narrow weights of little work and groups whose scale column
+    # holds a single strip stay on the GEMV; 3..32 rows over wide weights, and
+    # narrow ones from (M rounded up to 8) * K * N = 2^28 and 5 rows, take the
+    # MFMA kernel; 33 rows the GEMM.
+    assert _path(sgq, 2, 4096, 11008, 128) == 0
+    assert _path(sgq, 3, 4096, 11008, 128) == SKINNY
+    assert _path(sgq, 4, 2048, 6144, 128) == SKINNY
     assert _path(sgq, 33, 4096, 11008, 128) == 1
     assert _path(sgq, 8, 5632, 2048, 128) == 0
     assert _path(sgq, 8, 2048, 6144, 8) == 0
     assert _path(sgq, 4, 11008, 4096, 128) == 0
     assert _path(sgq, 8, 11008, 4096, 128) == SKINNY
     assert _path(sgq, 16, 11008, 4096, 128) == SKINNY
-    for M in range(5, 33):
+    for M in range(3, 33):
         assert _path(sgq, M, 4096, 11008, 128) == SKINNY
 
 
