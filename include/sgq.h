@@ -59,7 +59,9 @@ extern "C" {
 /* Message for the calling thread's last failed call ("" if none). */
 const char* sgq_last_error(void);
 
-/* Library ABI version (SGQ_ABI_VERSION). */
+/* Library ABI version (SGQ_ABI_VERSION).  2: packed INT4 buffers of the
+ * strip-major layout hold a second, k-octet copy of the codes (one byte per
+ * code in all); buffers packed by version 1 must be packed again. */
 int sgq_abi_version(void);
 
 /* ---- size queries (host-only; no GPU work) ----------------------------- */
@@ -71,7 +73,11 @@ int64_t sgq_int8_packed_bytes(int64_t K, int64_t N);
  * (group_size <= 0 means 32, as src/quantization.cpp:118). */
 int sgq_int4_layout(int64_t K, int64_t N, int64_t group_size);
 
-/* Bytes of the packed INT4 buffer for a [K,N] weight. */
+/* Bytes of the packed INT4 buffer for a [K,N] weight.  The strip-major
+ * layout (sgq_int4_layout() == 0) holds the codes twice, in the strips the
+ * GEMV reads and in blocks whose dwords are matrix-core operands (read by
+ * the 3..32-row and GEMM forms), about one byte per code; the flat layout
+ * half a byte per code. */
 int64_t sgq_int4_packed_bytes(int64_t K, int64_t N, int64_t group_size);
 
 /* Number of floats in the INT4 device-scale buffer (0 for the flat layout,

@@ -13,7 +13,7 @@
 #include <cstdio>
 #include <mutex>
 
-#define SGQ_ABI_VERSION 1
+#define SGQ_ABI_VERSION 2
 
 using namespace sgq;
 

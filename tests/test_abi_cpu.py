@@ -25,7 +25,7 @@ def test_exports_every_declared_symbol(sgq):
 
 
 def test_abi_version(lib):
-    assert lib.sgq_abi_version() == 1
+    assert lib.sgq_abi_version() == 2  # 2: INT4 strip-major buffers carry the k-octet copy
     assert lib.sgq_last_error() is not None
 
 
