@@ -229,14 +229,14 @@ class Case:
         self.sweep = sweep
         return ms
 
-    def time_queued(self, steps: int, repeats: int = 10, max_sweeps: int = 64) -> list:
+    def time_queued(self, steps: int, host_ms_per_call: float, repeats: int = 10, max_sweeps: int = 64) -> list:
         """K eager launches (call i on weight copy i % C, as in the graph)
         queued on the stream behind untimed replays of the sweep graph that
         time_graph leaves in self.sweep.  The start event is recorded after
         the sweeps, so it fires when the last sweep call ends; the sweep is
-        replayed long enough (twice the host's measured submission time of
-        the K calls) that the host has queued all K calls and the end event
-        by then, which a query of the start event confirms: it must still be
+        replayed long enough (twice K times host_ms_per_call, the rate of
+        eager calls the host sustains) that the host has queued all K calls
+        and the end event by then, which a query of the start event confirms: it must still be
         pending once everything is queued, else that repetition is dropped.
         The region then holds the K calls back to back with no host gap and
         without a graph replay's fixed cost (about 8 us per replay on MI355X:
@@ -255,12 +255,7 @@ class Case:
         e.record()
         torch.cuda.synchronize()
         sweep_s = s.elapsed_time(e) * 1e-3
-        t0 = time.perf_counter()
-        for i in range(steps):
-            self.launch(i)
-        host_s = time.perf_counter() - t0
-        torch.cuda.synchronize()
-        n_sweeps = max(1, math.ceil(2.0 * host_s / sweep_s))
+        n_sweeps = max(1, math.ceil(2.0 * steps * host_ms_per_call * 1e-3 / sweep_s))
         self.queued_sweeps = n_sweeps
         if n_sweeps > max_sweeps:
             return []
@@ -1085,7 +1080,7 @@ def main() -> int:
                  "idle_start_us_per_step": round(case.idle_start_ms * 1e3, 3)}
         # The K calls queued eagerly behind the sweep: the figure reported,
         # unless the host could not get ahead of the GPU (then the graph's).
-        queued = case.time_queued(args.steps)
+        queued = case.time_queued(args.steps, ms_eager)
         ms = queued[0] if queued else ms_graph
         spread = spread_of(queued) if queued else graph["us_per_step_over_replays"]
     err = case.check(Oracle(), rows=None if c["M"] <= 256 else np.r_[0:8, c["M"] - 8:c["M"]])
