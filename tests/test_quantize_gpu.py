@@ -110,6 +110,21 @@ def test_pack_from_codes_roundtrip(sgq, dev, synth):
             assert torch.equal(re.devscales, qx.devscales)
 
 
+@pytest.mark.parametrize("K,N,G", [(40, 72, 8), (17, 24, 8), (96, 80, 16), (33, 136, 136)])
+def test_int4_buffer_with_koct_copy(sgq, dev, oracle, synth, K, N, G):
+    """The whole INT4 strip-major buffer, from the quantizer and from codes:
+    the strips, zeros up to the 256-byte boundary, and the k-octet copy, with
+    K inside a 32-row k block and a half-empty last column block (N % 16 == 8)."""
+    print(f"  case int4 {K}x{N} G={G}", flush=True)
+    W = synth.normal((K, N), synth.config_seed(5), synth.STREAM_W, 0.0, 0.02)
+    q, s = oracle.quantize_int4(W, G)
+    exp = helpers.model_pack_i4_tiled(q.astype(np.int64), G)
+    qx = sgq.quantize_int4(_to_dev(W, dev), G)
+    assert np.array_equal(_np(qx.packed), exp)
+    re = sgq.pack_int4(qx.qdata, qx.scales, G)
+    assert np.array_equal(_np(re.packed), exp)
+
+
 @pytest.mark.parametrize("bad", [0.5, 128.0, float("nan"), float("inf"), -129.0])
 def test_pack_rejects_bad_codes_int8(sgq, dev, bad):
     q = torch.zeros((8, 8), dtype=torch.float32, device=dev)
