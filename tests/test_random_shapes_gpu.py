@@ -8,7 +8,8 @@ multiple of 8, 16 or the group (strip layout, its k-octet copy with a
 half-empty column block, the flat INT4 layout), INT4 groups 24..128 and INT8
 per tensor and per channel.  Each output is checked against the oracle's
 dequantize-then-matmul on the same quantized weight, to the forward's 1e-5.
-The draws are fixed by the seed, so a failure names a reproducible case.
+Twenty-four more draws run the gated MLP the same way.  The draws are fixed
+by the seed, so a failure names a reproducible case.
 """
 import ctypes
 
@@ -90,5 +91,51 @@ def test_random_shape(sgq, dev, oracle, synth, bits, M, K, N, g, bias, i):
         yref = oracle.quantized_matmul_int4(x[rows], q, s, g, b)
     torch.cuda.synchronize()
     e = rel_err(y.cpu().numpy()[rows], yref)
+    print(f"    rel_err={e:.3e}", flush=True)
+    assert e <= TOL
+
+
+def _swiglu_draws(n=24, seed=20261203, max_work=1 << 27):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        bits = int(rng.choice([4, 8]))
+        M, K, N = int(rng.choice(MS + [96, 128])), int(rng.choice(KS)), int(rng.choice(NS))
+        if M * K * N > max_work:
+            continue
+        g = int(rng.choice(GS)) if bits == 4 else int(rng.integers(0, 2))
+        out.append((bits, M, K, N, g, bool(rng.integers(0, 2)), len(out)))
+    return out
+
+
+SWIGLU_CASES = _swiglu_draws()
+
+
+@pytest.mark.parametrize("bits,M,K,N,g,bias,i", SWIGLU_CASES,
+                         ids=[f"s{c[6]}_{c[0]}b_{c[1]}x{c[2]}x{c[3]}" for c in SWIGLU_CASES])
+def test_random_swiglu(sgq, dev, oracle, synth, bits, M, K, N, g, bias, i):
+    """The gated MLP, silu(x Wg + bg) * (x Wu + bu), on the same kind of draws."""
+    print(f"  case {i}: bits={bits} M={M} K={K} N={N} g={g} bias={bias}", flush=True)
+    seed = synth.config_seed(300 + i)
+    Wg = synth.normal((K, N), seed, synth.STREAM_W, 0.0, 0.02)
+    Wu = synth.normal((K, N), seed, synth.STREAM_W2, 0.0, 0.02)
+    x = synth.normal((M, K), seed, synth.STREAM_X, 0.0, 1.0)
+    bg = synth.normal((1, N), seed, synth.STREAM_BIAS, 0.0, 0.02) if bias else None
+    bu = synth.normal((1, N), seed, synth.STREAM_BIAS2, 0.0, 0.02) if bias else None
+
+    def dev_(a):
+        return None if a is None else torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+
+    if bits == 8:
+        wg, wu = sgq.quantize_int8(dev_(Wg), g), sgq.quantize_int8(dev_(Wu), g)
+        (qg, sg), (qu, su) = oracle.quantize_int8(Wg, g), oracle.quantize_int8(Wu, g)
+        href = oracle.swiglu_int8(x, qg, sg, qu, su, g, bg, bu)
+    else:
+        wg, wu = sgq.quantize_int4(dev_(Wg), g), sgq.quantize_int4(dev_(Wu), g)
+        (qg, sg), (qu, su) = oracle.quantize_int4(Wg, g), oracle.quantize_int4(Wu, g)
+        href = oracle.swiglu_int4(x, qg, sg, qu, su, g, bg, bu)
+    h = sgq.quantized_swiglu(dev_(x), wg, wu, dev_(bg), dev_(bu))
+    torch.cuda.synchronize()
+    e = rel_err(h.cpu().numpy(), href)
     print(f"    rel_err={e:.3e}", flush=True)
     assert e <= TOL
